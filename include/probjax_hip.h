@@ -1,0 +1,129 @@
+/*
+ * probjax_hip.h -- C ABI of the MI355X (gfx950) fused-attention kernels that
+ * back probjax.nn's attention path.
+ *
+ * Plain pointers and sizes only: every pointer is a device pointer into HBM
+ * owned by the caller (XLA, torch, or a ctypes harness), valid for the
+ * duration of the call; nothing is cached across calls.  `stream` is a
+ * hipStream_t passed as void* (NULL = the default stream).  Every entry point
+ * only enqueues work on `stream`: no device synchronisation, no host<->device
+ * copies, no allocation.  Entry points are reentrant; the only global state is
+ * a thread-local error string.
+ *
+ * Layout conventions are probjax's: q [B, Lq, Hq, D], k/v [B, Lk, Hkv, D]
+ * row-major (D fastest), query head h uses KV head h / (Hq / Hkv)
+ * (probjax/nn/pallas_kernels/kernels/attention.py:2164-2165,2189-2196).
+ *
+ * Return value: PJX_OK, or an error code with a message in pjx_last_error().
+ */
+#ifndef PROBJAX_HIP_H_
+#define PROBJAX_HIP_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PJX_DTYPE_F32 0
+#define PJX_DTYPE_BF16 1
+
+#define PJX_OK 0
+#define PJX_ERR_INVALID 1  /* unsupported shape / dtype / argument */
+#define PJX_ERR_LAUNCH 2   /* the HIP runtime rejected a launch */
+#define PJX_ERR_WORKSPACE 3 /* workspace missing or too small */
+
+/* Library version (major*10000 + minor*100 + patch). */
+int pjx_version(void);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* pjx_last_error(void);
+
+/*
+ * Flash-attention forward.  Replaces the Pallas `mha_forward` kernel and its
+ * launch (`_mha_impl_raw`, probjax/nn/pallas_kernels/kernels/attention.py:
+ * 377-533, 2130-2278) for the masks/biases of the path, with the semantics of
+ * the XLA reference (kernels/attention_xla.py:339-429):
+ *
+ *   s = sm_scale * q.k (fp32)  [+ bias[b|0, h|0, q, k]]  then masked -> -inf,
+ *   o = softmax(s) . v with fp32 accumulation; P is rounded to bf16 before the
+ *   P.V product in bf16 mode; rows without a valid key give 0.
+ *
+ * Masks (ANDed), all optional:
+ *   causal      -- CausalMask, q >= k (attention_mask_bias.py:615-646)
+ *   kv_lengths  -- KVLenMask, k < kv_lengths[b], int32 [B] (:1399-1532)
+ *   q_valid / kv_valid -- QKVLengthMask static lengths (:1077-1127);
+ *                  pass q_len / kv_len for none.
+ * bias: DenseBias data, fp32 [bias_batch, bias_heads, Lq, Lk] with
+ *   bias_batch in {1, B}, bias_heads in {1, Hq} (attention_mask_bias.py:
+ *   1807-1922); NULL for none.
+ * lse: optional fp32 [B, Hq, Lq] natural-log log-sum-exp of the scores
+ *   (+inf for rows without a valid key, as attention_xla.py:420); NULL skips.
+ *
+ * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim in {64, 128}
+ * (k and v share it).  sm_scale must be > 0.
+ */
+int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                  float* lse, const int32_t* kv_lengths, const float* bias,
+                  int64_t bias_batch, int64_t bias_heads, int64_t batch, int64_t q_len,
+                  int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                  int64_t q_valid, int64_t kv_valid, int causal, float sm_scale,
+                  void* stream);
+
+/*
+ * Bytes of workspace pjx_splitkv_decode / pjx_mla_decode need for these sizes
+ * (partial outputs and log-sum-exp terms of every KV chunk).
+ *   rows   -- query rows per (batch, kv head): (Hq/Hkv)*Lq for GQA decode,
+ *             Lq*H for MLA (heads folded onto the query axis).
+ *   groups -- kv heads (GQA decode) or 1 (MLA).
+ *   v_dim  -- output head dim.
+ */
+size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
+                                 int64_t kv_len, int64_t v_dim, int64_t chunk);
+
+/*
+ * GQA split-KV decode.  Replaces `splitkv_forward` / `_splitkv_kernel` and the
+ * XLA log-sum-exp merge (probjax/nn/pallas_kernels/kernels/attention_splitkv.py:
+ * 43-250) and extends it with the per-sequence KVLenMask that the reference
+ * routes to the regular forward (kernels/attention.py:2672-2675).
+ *
+ * q [B, Lq, Hq, D] bf16; k, v [B, Lk, Hkv, D] bf16 (Lk = KV capacity);
+ * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, D] bf16;
+ * lse optional fp32 [B, Hq, Lq], natural log (attention_splitkv.py:248-250).
+ * The (Hq/Hkv)*Lq query rows of a KV head are packed row = g*Lq + t
+ * (attention_splitkv.py:121-126); at most 16 rows per KV head.
+ * Only keys < kv_lengths[b] are read.  head_dim == 128.
+ * chunk: keys per work item (0 = default 256; a multiple of 64).
+ * workspace: at least pjx_decode_workspace_size(B, Hkv, rows, Lk, D, chunk) bytes.
+ */
+int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
+                       const int32_t* kv_lengths, void* o, float* lse, void* workspace,
+                       size_t workspace_bytes, int64_t batch, int64_t q_len,
+                       int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                       int64_t head_dim, float sm_scale, int64_t chunk, void* stream);
+
+/*
+ * Latent (MLA) attention decode, absorbed form K = V = cache.  Replaces the
+ * absorbed `mla_forward` kernel (probjax/nn/pallas_kernels/kernels/
+ * latent_attention.py:79-197, 247-377, 636-766) with heads folded onto the
+ * query axis (layers/latent_attention.py:458-469, row = t*H + h).
+ *
+ * q [B, Lq, H, R] bf16; cache [B, S, R] bf16; kv_lengths int32 [B] or NULL;
+ * o [B, Lq, H, v_dim] bf16 = the first v_dim columns of mla(q, cache, None,
+ * None) (v_dim == R gives the API-exact output); lse optional fp32 [B, H, Lq].
+ * Lq*H <= 16.  R a multiple of 64, R <= 576; v_dim a multiple of 64, <= R.
+ * workspace: at least pjx_decode_workspace_size(B, 1, Lq*H, S, v_dim, chunk)
+ * bytes, chunk = 0 (default) in this call.
+ */
+int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* kv_lengths,
+                   void* o, float* lse, void* workspace, size_t workspace_bytes,
+                   int64_t batch, int64_t q_len, int64_t heads, int64_t kv_len,
+                   int64_t rank, int64_t v_dim, float sm_scale, int64_t chunk,
+                   void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PROBJAX_HIP_H_ */

@@ -1,0 +1,574 @@
+// Flash-attention forward for gfx950 (MI355X): causal / KV-length / static
+// length masks and an fp32 dense additive bias, bf16 or fp32 inputs.
+//
+// Semantics follow probjax's XLA attention reference
+// (probjax/nn/pallas_kernels/kernels/attention_xla.py:339-429): scores are
+// sm_scale * q.k in fp32, then the bias, then the mask (masked -> -inf); an
+// online softmax in the exp2 domain (as the Pallas kernel,
+// kernels/attention.py:483-494); P is rounded to bf16 before the P.V product
+// in bf16 mode (attention_xla.py:349; attention.py:506); rows with no valid
+// key give 0 (attention_xla.py:417-420).
+//
+// Work decomposition: one workgroup = 4 waves = 128 query rows of one
+// (batch, head); each wave owns 32 rows.  Per KV tile of BK keys a wave
+// computes S^T = K Q^T with the keys as MFMA rows, so every lane holds the
+// scores of ONE query for 16 keys per 32-key block: the row max / row sum are
+// lane-local plus one v_permlane32_swap, with no shuffle trees.  P feeds
+// O^T = V^T P^T straight from registers (the lane layout of S^T's C operand is
+// the B-operand layout of the next MFMA up to a key permutation that V^T's
+// A operand reproduces), so the per-row rescale and 1/l are lane-local too.
+// K tiles are stored row-major in LDS; V tiles are transposed into LDS once
+// per tile (bf16) so that the A operand of P.V is two 8-byte LDS reads.
+// LDS is double-buffered with register prefetch: the global loads of tile
+// t+1 are in flight while tile t is computed; one barrier per tile.
+//
+// Grid: one workgroup per (q tile, batch, head), ordered heaviest causal
+// q-tile first (longest-processing-time order), and batch*head fastest so
+// that every q-tile of one (batch, head) lands on the same XCD (workgroups are
+// dispatched round-robin over the 8 XCDs; batch*head is a multiple of 8 in
+// the configs) and shares its K/V in that XCD's L2.
+#include "pjx_common.h"
+#include "pjx_internal.h"
+
+namespace pjx {
+
+struct FlashArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  float* lse;
+  const int32_t* kv_lengths;
+  const float* bias;
+  long bias_bstride;  // elements between batch slices of the bias (0: broadcast)
+  long bias_hstride;  // elements between head slices of the bias (0: broadcast)
+  int B, Lq, Lk, Hq, Hkv;
+  int q_valid, kv_valid, causal;
+  float scale;
+  int n_qtiles;
+};
+
+constexpr int kBQ = 128;
+constexpr int kThreads = 256;
+
+// Per-block geometry shared by both dtype paths.
+struct BlockGeom {
+  int b, h, hkv, q0, qw, qi;
+  int q_hi;     // rows >= q_hi are fully masked (QKVLengthMask / Lq)
+  int kv_end;   // keys >= kv_end are masked (KVLenMask, QKVLengthMask, Lk)
+  int kv_stop;  // keys the block visits (kv_end, clipped causally)
+};
+
+__device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) {
+  BlockGeom g;
+  const int BH = a.B * a.Hq;
+  const int idx = blockIdx.x;
+  const int bh = idx % BH;
+  const int qt = a.n_qtiles - 1 - idx / BH;
+  g.b = bh / a.Hq;
+  g.h = bh % a.Hq;
+  g.hkv = g.h / (a.Hq / a.Hkv);
+  g.q0 = qt * kBQ;
+  const int w = threadIdx.x >> 6;
+  g.qw = g.q0 + 32 * w;
+  g.qi = g.qw + (threadIdx.x & 31);
+  g.q_hi = min(a.Lq, a.q_valid);
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[g.b], 0));
+  g.kv_end = kv_end;
+  int stop = kv_end;
+  if (g.q0 >= g.q_hi) {
+    stop = 0;
+  } else if (a.causal) {
+    stop = min(stop, min(g.q0 + kBQ, g.q_hi));
+  }
+  g.kv_stop = stop;
+  return g;
+}
+
+// Bias for this lane's query row at 4 consecutive keys starting at kk.
+template <bool VEC>
+__device__ __forceinline__ f32x4 load_bias4(const float* row, int kk, int Lk) {
+  if (VEC && kk + 3 < Lk) return *(const f32x4*)(row + kk);
+  f32x4 r;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) r[j] = (kk + j < Lk) ? row[kk + j] : 0.f;
+  return r;
+}
+
+// ---------------------------------------------------------------------------
+// bf16 path: v_mfma_f32_32x32x16_bf16 for both products.
+// ---------------------------------------------------------------------------
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
+  constexpr int BK = 64;
+  constexpr int KS = D + 8;   // K row stride in LDS (bf16): 16 B pad -> conflict-free b128 reads
+  constexpr int VS = BK + 4;  // V^T row stride (bf16): 34 dwords -> conflict-free b64 reads
+  constexpr int DC = D / 8;   // 16-byte chunks per K/V row
+  constexpr int K_PER_T = BK * DC / kThreads;
+  constexpr int V_UNITS = (BK / 4) * DC;  // 4 keys x 8 dims per unit
+  static_assert(K_PER_T >= 1 && V_UNITS <= kThreads, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BK * KS];
+  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * VS];
+
+  const BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int col = lane & 31, half = lane >> 5;
+  const size_t kv_row = (size_t)a.Hkv * D;
+  const uint16_t* Kb = (const uint16_t*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const uint16_t* Vb = (const uint16_t*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const bool row_in = g.qi < a.Lq;
+  const bool row_ok = g.qi < g.q_hi;
+
+  // Q^T as the B operand: lane holds query `col`, dims 16*s + 8*half + [0,8).
+  bf16x8 qf[D / 16];
+  {
+    const uint16_t* qrow =
+        (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (row_in) raw = *(const u32x4*)(qrow + 16 * s + 8 * half);
+      qf[s] = as_bf16x8(raw);
+    }
+  }
+
+  const float* brow = nullptr;
+  if constexpr (BIAS) {
+    brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
+           (size_t)(row_in ? g.qi : 0) * a.Lk;
+  }
+  const bool bias_vec = (a.Lk & 3) == 0;
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;  // score units -> log2 units
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  float m_run = kMaxInit, l_run = 0.f;
+
+  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int q_last_w = g.qw + 31;
+
+  u32x4 kreg[K_PER_T];
+  u32x4 vreg[4];
+
+  auto load_tile = [&](int t) {
+    const int k0 = t * BK;
+#pragma unroll
+    for (int i = 0; i < K_PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      const int kk = k0 + u / DC, dc = u % DC;
+      u32x4 r = {0u, 0u, 0u, 0u};
+      if (kk < g.kv_stop) r = *(const u32x4*)(Kb + (size_t)kk * kv_row + dc * 8);
+      kreg[i] = r;
+    }
+    if (tid < V_UNITS) {
+      const int dc = tid % DC, kq = tid / DC;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int kk = k0 + 4 * kq + j;
+        u32x4 r = {0u, 0u, 0u, 0u};
+        if (kk < g.kv_stop) r = *(const u32x4*)(Vb + (size_t)kk * kv_row + dc * 8);
+        vreg[j] = r;
+      }
+    }
+  };
+
+  auto store_tile = [&](int buf) {
+    uint16_t* kl = k_lds[buf];
+#pragma unroll
+    for (int i = 0; i < K_PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      *(u32x4*)(kl + (u / DC) * KS + (u % DC) * 8) = kreg[i];
+    }
+    if (tid < V_UNITS) {
+      uint16_t* vl = v_lds[buf];
+      const int dc = tid % DC, kq = tid / DC;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int dw = e >> 1;
+        u32x2 pk;
+        if (e & 1) {
+          pk[0] = pack_hi_halves(vreg[0][dw], vreg[1][dw]);
+          pk[1] = pack_hi_halves(vreg[2][dw], vreg[3][dw]);
+        } else {
+          pk[0] = pack_lo_halves(vreg[0][dw], vreg[1][dw]);
+          pk[1] = pack_lo_halves(vreg[2][dw], vreg[3][dw]);
+        }
+        *(u32x2*)(vl + (dc * 8 + e) * VS + 4 * kq) = pk;
+      }
+    }
+  };
+
+  auto compute = [&](int t, int buf) {
+    const int k0 = t * BK;
+    if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    const uint16_t* kl = k_lds[buf];
+    const uint16_t* vl = v_lds[buf];
+
+    // S^T[key][query] = K Q^T
+    f32x16 s[BK / 32];
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb) {
+      s[kb] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 kf = as_bf16x8(*(const u32x4*)(kl + (kb * 32 + col) * KS + 16 * st + 8 * half));
+        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+      }
+    }
+
+    // Register r of block kb holds key k0 + kb*32 + 8*(r/4) + 4*half + r%4.
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb) {
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
+        }
+      }
+    }
+    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                           (g.qw + 31 >= g.q_hi);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = k0 + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool keep = row_ok && kk < g.kv_end && (!a.causal || kk <= g.qi);
+          if (!keep) s[kb][r] = -INFINITY;
+        }
+      }
+    }
+
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = xor32_max(mx);
+    const float m_new = fmaxf(m_run, mx * cx);
+    const float corr = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_new));
+        rs += p;
+        s[kb][r] = p;
+      }
+    l_run = fmaf(l_run, corr, rs);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+
+    // P^T as the B operand, 16 keys per MFMA step c:
+    // slot j <-> key 16c + 8*(j/4) + 4*half + j%4 (registers 8*(c%2)+j of block c/2).
+    bf16x8 pf[BK / 16];
+#pragma unroll
+    for (int c = 0; c < BK / 16; ++c) {
+      u32x4 pk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
+      pf[c] = as_bf16x8(pk);
+    }
+    // O^T[d][query] += V^T P^T; the A operand reads the same key order from V^T.
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+      for (int c = 0; c < BK / 16; ++c) {
+        const uint16_t* vp = vl + (db * 32 + col) * VS + 16 * c + 4 * half;
+        const u32x2 lo = *(const u32x2*)vp;
+        const u32x2 hi = *(const u32x2*)(vp + 8);
+        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
+        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+      }
+    }
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    compute(t, t & 1);
+    if (t + 1 < n_tiles) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  const float l_tot = xor32_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (row_in) {
+    uint16_t* orow = (uint16_t*)a.o + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2 pk;
+        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
+      }
+    if (a.lse && half == 0)
+      a.lse[((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi] =
+          l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// fp32 path: v_mfma_f32_32x32x2f32 (full fp32 products) for both products.
+// The k index of one MFMA step is the wave half: half 0 contracts dim s,
+// half 1 dim D/2 + s, so each lane reads a contiguous half row of K.  For
+// P.V the step pairs key (r, half 0) with key (r, half 1) of the S^T layout,
+// so V is read in its natural [key][dim] layout: no transpose needed.
+// ---------------------------------------------------------------------------
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a) {
+  constexpr int BK = (D == 128) ? 32 : 64;
+  constexpr int KS = D + 4;  // floats; b128 reads of 16 rows hit distinct banks
+  constexpr int VS = D + 8;  // floats; rows 4 apart land 32 banks apart
+  constexpr int DC = D / 4;  // float4 chunks per row
+  constexpr int PER_T = BK * DC / kThreads;
+  static_assert(PER_T >= 1, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) float k_lds[2][BK * KS];
+  __shared__ __attribute__((aligned(16))) float v_lds[2][BK * VS];
+
+  const BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int col = lane & 31, half = lane >> 5;
+  const size_t kv_row = (size_t)a.Hkv * D;
+  const float* Kb = (const float*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const float* Vb = (const float*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const bool row_in = g.qi < a.Lq;
+  const bool row_ok = g.qi < g.q_hi;
+
+  float qf[D / 2];
+  {
+    const float* qrow =
+        (const float*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D + half * (D / 2);
+#pragma unroll
+    for (int s = 0; s < D / 8; ++s) {
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+      if (row_in) r = *(const f32x4*)(qrow + 4 * s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[4 * s + j] = r[j];
+    }
+  }
+  const float* brow = nullptr;
+  if constexpr (BIAS) {
+    brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
+           (size_t)(row_in ? g.qi : 0) * a.Lk;
+  }
+  const bool bias_vec = (a.Lk & 3) == 0;
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  float m_run = kMaxInit, l_run = 0.f;
+  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int q_last_w = g.qw + 31;
+
+  f32x4 kreg[PER_T], vreg[PER_T];
+  auto load_tile = [&](int t) {
+    const int k0 = t * BK;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      const int kk = k0 + u / DC, dc = u % DC;
+      f32x4 rk = {0.f, 0.f, 0.f, 0.f}, rv = {0.f, 0.f, 0.f, 0.f};
+      if (kk < g.kv_stop) {
+        rk = *(const f32x4*)(Kb + (size_t)kk * kv_row + dc * 4);
+        rv = *(const f32x4*)(Vb + (size_t)kk * kv_row + dc * 4);
+      }
+      kreg[i] = rk;
+      vreg[i] = rv;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      *(f32x4*)(&k_lds[buf][(u / DC) * KS + (u % DC) * 4]) = kreg[i];
+      *(f32x4*)(&v_lds[buf][(u / DC) * VS + (u % DC) * 4]) = vreg[i];
+    }
+  };
+
+  auto compute = [&](int t, int buf) {
+    const int k0 = t * BK;
+    if (a.causal && k0 > q_last_w) return;
+    const float* kl = k_lds[buf];
+    const float* vl = v_lds[buf];
+    f32x16 s[BK / 32];
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb) {
+      s[kb] = f32x16{};
+      const float* kp = kl + (kb * 32 + col) * KS + half * (D / 2);
+#pragma unroll
+      for (int st4 = 0; st4 < D / 8; ++st4) {
+        const f32x4 kf = *(const f32x4*)(kp + 4 * st4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[kb] = mfma32x32x2f32(kf[j], qf[4 * st4 + j], s[kb]);
+      }
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
+        }
+    }
+    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                           (g.qw + 31 >= g.q_hi);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = k0 + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool keep = row_ok && kk < g.kv_end && (!a.causal || kk <= g.qi);
+          if (!keep) s[kb][r] = -INFINITY;
+        }
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
+    mx = xor32_max(mx);
+    const float m_new = fmaxf(m_run, mx * cx);
+    const float corr = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_new));
+        rs += p;
+        s[kb][r] = p;
+      }
+    l_run = fmaf(l_run, corr, rs);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          acc[db] = mfma32x32x2f32(vl[key * VS + db * 32 + col], s[kb][r], acc[db]);
+        }
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    compute(t, t & 1);
+    if (t + 1 < n_tiles) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  const float l_tot = xor32_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (row_in) {
+    float* orow = (float*)a.o + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = acc[db][4 * gq + j] * inv;
+        *(f32x4*)(orow + db * 32 + 8 * gq + 4 * half) = v;
+      }
+    if (a.lse && half == 0)
+      a.lse[((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi] =
+          l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : INFINITY;
+  }
+}
+
+template <typename K>
+static int launch(K kernel, const FlashArgs& a, hipStream_t stream) {
+  const long blocks = (long)a.n_qtiles * a.B * a.Hq;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  return check_launch("pjx_flash_fwd");
+}
+
+}  // namespace pjx
+
+using namespace pjx;
+
+extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                             float* lse, const int32_t* kv_lengths, const float* bias,
+                             int64_t bias_batch, int64_t bias_heads, int64_t batch,
+                             int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                             int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
+                             float sm_scale, void* stream) {
+  clear_error();
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
+  if (!q || !k || !v || !o) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: q, k, v, o must be non-null");
+  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: negative or zero size");
+  if (q_heads % kv_heads != 0)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: q_heads must be a multiple of kv_heads");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128");
+  if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: sm_scale must be > 0");
+  if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: bias must be [1|B, 1|Hq, Lq, Lk]");
+  const int64_t elems = batch * q_len * q_heads * head_dim;
+  if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30))
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: sizes out of range");
+  if (batch == 0 || q_len == 0) return PJX_OK;
+
+  FlashArgs a;
+  a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
+  a.kv_lengths = kv_lengths;
+  a.bias = bias;
+  a.bias_hstride = (bias && bias_heads != 1) ? q_len * kv_len : 0;
+  a.bias_bstride = (bias && bias_batch != 1) ? bias_heads * q_len * kv_len : 0;
+  a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len;
+  a.Hq = (int)q_heads; a.Hkv = (int)kv_heads;
+  a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
+  a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
+  a.causal = causal ? 1 : 0;
+  a.scale = sm_scale;
+  a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
+  if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: grid too large");
+  hipStream_t s = (hipStream_t)stream;
+  const bool hb = bias != nullptr;
+  if (dtype == PJX_DTYPE_BF16) {
+    if (head_dim == 128) return hb ? launch(flash_fwd_bf16_kernel<128, true>, a, s) : launch(flash_fwd_bf16_kernel<128, false>, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<64, true>, a, s) : launch(flash_fwd_bf16_kernel<64, false>, a, s);
+  }
+  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true>, a, s) : launch(flash_fwd_f32_kernel<128, false>, a, s);
+  return hb ? launch(flash_fwd_f32_kernel<64, true>, a, s) : launch(flash_fwd_f32_kernel<64, false>, a, s);
+}

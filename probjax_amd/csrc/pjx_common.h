@@ -1,0 +1,87 @@
+// Shared device helpers for the probjax_amd attention kernels (gfx950 only).
+//
+// MFMA lane layouts used throughout (checked on the device against a CPU
+// matmul):
+//   v_mfma_f32_32x32x16_bf16 : A lane l holds A[l%32][8*(l/32)+j], j<8;
+//                              B lane l holds B[8*(l/32)+j][l%32];
+//                              C reg r of lane l is C[8*(r/4)+4*(l/32)+r%4][l%32].
+//   v_mfma_f32_16x16x32_bf16 : A lane l holds A[l%16][8*(l/16)+j];
+//                              B lane l holds B[8*(l/16)+j][l%16];
+//                              C reg r of lane l is C[4*(l/16)+r][l%16].
+//   v_mfma_f32_32x32x2f32    : A lane l holds A[l%32][l/32]; B lane l holds
+//                              B[l/32][l%32]; C as for 32x32x16.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace pjx {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+// Finite "minus infinity" for running maxima (log2 units): masked scores are
+// -inf, so exp2(-inf - kMaxInit) == 0 while exp2(kMaxInit - kMaxInit) == 1.
+constexpr float kMaxInit = -1e30f;
+
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
+  return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(u32x4, v); }
+
+// Value of lane l^32 combined with lane l, identical in both halves.
+__device__ __forceinline__ float xor32_max(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Two floats -> packed bf16 pair (round to nearest even; v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 p;
+  p[0] = (__bf16)lo;
+  p[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, p);
+}
+
+__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
+  return __uint_as_float(bits16 << 16);
+}
+
+// Select 16-bit halves of two dwords: lo halves (sel 0) or hi halves (sel 1)
+// of a and b packed as {a_half, b_half}.
+__device__ __forceinline__ uint32_t pack_lo_halves(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x05040100u);
+}
+__device__ __forceinline__ uint32_t pack_hi_halves(uint32_t a, uint32_t b) {
+  return __builtin_amdgcn_perm(b, a, 0x07060302u);
+}
+
+template <typename T>
+__device__ __forceinline__ T ldg_or_zero(const T* p, bool ok) {
+  if (ok) return *p;
+  T z;
+  __builtin_memset(&z, 0, sizeof(T));
+  return z;
+}
+
+}  // namespace pjx

@@ -1,0 +1,177 @@
+"""Device-tensor wrappers over the C ABI (torch provides HBM buffers and streams).
+
+Each function validates shapes/dtypes on the host (``ValueError`` for what the
+kernels do not take), allocates the outputs, and enqueues the kernels on the
+tensors' current HIP stream.  Inputs must already be resident on one ROCm
+device; nothing is copied between host and device.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import native
+
+_DTYPES = {torch.bfloat16: native.PJX_DTYPE_BF16, torch.float32: native.PJX_DTYPE_F32}
+
+
+def _dtype_code(t: torch.Tensor) -> int:
+    try:
+        return _DTYPES[t.dtype]
+    except KeyError:
+        raise ValueError(f"unsupported dtype {t.dtype}; expected bfloat16 or float32") from None
+
+
+def _on_device(*ts):
+    dev = None
+    for t in ts:
+        if t is None:
+            continue
+        if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+            raise ValueError("the HIP attention kernels need tensors on a ROCm device")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def _stream(dev) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(dev).cuda_stream)
+
+
+def _lengths(kv_lengths, batch, dev):
+    if kv_lengths is None:
+        return None
+    L = torch.as_tensor(kv_lengths, device=dev).reshape(-1).to(torch.int32).contiguous()
+    if L.numel() != batch:
+        raise ValueError(f"kv_lengths has {L.numel()} entries for batch {batch}")
+    return L
+
+
+def flash_attention_fwd(
+    q, k, v, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
+    q_valid: int | None = None, kv_valid: int | None = None, return_lse: bool = False,
+):
+    """``pjx_flash_fwd``: ``q [B, Lq, Hq, D]``, ``k/v [B, Lk, Hkv, D]`` -> ``o``.
+
+    ``bias`` is fp32 ``[1|B, 1|Hq, Lq, Lk]``; ``kv_lengths`` int ``[B]``;
+    ``q_valid``/``kv_valid`` are static query/key lengths (QKVLengthMask).
+    Returns ``o`` (and the natural-log LSE ``[B, Hq, Lq]`` with ``return_lse``).
+    """
+    dev = _on_device(q, k, v, bias)
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, v must be [B, T, H, D]")
+    B, Lq, Hq, D = q.shape
+    _, Lk, Hkv, Dk = k.shape
+    if k.shape != v.shape or k.shape[0] != B or Dk != D:
+        raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if q.dtype != k.dtype or q.dtype != v.dtype:
+        raise ValueError("q, k, v must share a dtype")
+    if Hq % Hkv:
+        raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if not sm_scale > 0:
+        raise ValueError("sm_scale must be > 0")
+    code = _dtype_code(q)
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    bb = bh = 1
+    if bias is not None:
+        if bias.ndim != 4 or tuple(bias.shape[-2:]) != (Lq, Lk):
+            raise ValueError(f"bias must be [1|B, 1|H, {Lq}, {Lk}], got {tuple(bias.shape)}")
+        bb, bh = bias.shape[:2]
+        if bb not in (1, B) or bh not in (1, Hq):
+            raise ValueError(f"bias {tuple(bias.shape)} does not broadcast to B={B}, H={Hq}")
+        bias = bias.to(torch.float32).contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    lib = native.load()
+    rc = lib.pjx_flash_fwd(
+        code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(L), _ptr(bias), bb, bh,
+        B, Lq, Lk, Hq, Hkv, D, Lq if q_valid is None else int(q_valid),
+        Lk if kv_valid is None else int(kv_valid), int(bool(causal)), float(sm_scale), _stream(dev),
+    )
+    native.check(rc)
+    return (o, lse) if return_lse else o
+
+
+def decode_workspace_bytes(batch, groups, rows, kv_len, v_dim, chunk=0) -> int:
+    return int(native.load().pjx_decode_workspace_size(batch, groups, rows, kv_len, v_dim, chunk))
+
+
+def _workspace(nbytes, dev, workspace):
+    if workspace is None:
+        return torch.empty((max(nbytes, 1),), dtype=torch.uint8, device=dev)
+    if workspace.device != dev or workspace.numel() * workspace.element_size() < nbytes:
+        raise ValueError(f"workspace must hold {nbytes} bytes on {dev}")
+    return workspace
+
+
+def splitkv_decode(
+    q, k, v, *, sm_scale: float, kv_lengths=None, chunk: int = 0, return_lse: bool = False,
+    workspace=None,
+):
+    """``pjx_splitkv_decode``: bf16 ``q [B, Lq, Hq, D]``, ``k/v [B, S, Hkv, D]``."""
+    dev = _on_device(q, k, v)
+    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
+        raise ValueError("q must be [B, Lq, Hq, D] and k, v [B, S, Hkv, D]")
+    B, Lq, Hq, D = q.shape
+    _, S, Hkv, Dk = k.shape
+    if Dk != D or k.shape[0] != B or Hq % Hkv:
+        raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}")
+    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
+        raise ValueError("split-KV decode takes bfloat16 q, k, v")
+    rows = (Hq // Hkv) * Lq
+    if rows > 16 or D not in (64, 128):
+        raise ValueError("split-KV decode needs (Hq/Hkv)*Lq <= 16 and head_dim 64 or 128")
+    q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    nbytes = decode_workspace_bytes(B, Hkv, rows, S, D, chunk)
+    ws = _workspace(nbytes, dev, workspace)
+    o = torch.empty_like(q)
+    lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    rc = native.load().pjx_splitkv_decode(
+        native.PJX_DTYPE_BF16, _ptr(q), _ptr(k), _ptr(v), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
+        nbytes, B, Lq, S, Hq, Hkv, D, float(sm_scale), int(chunk), _stream(dev),
+    )
+    native.check(rc)
+    return (o, lse) if return_lse else o
+
+
+def mla_decode(
+    q, cache, *, sm_scale: float, v_dim: int | None = None, kv_lengths=None, chunk: int = 0,
+    return_lse: bool = False, workspace=None,
+):
+    """``pjx_mla_decode``: bf16 ``q [B, Lq, H, R]`` over ``cache [B, S, R]`` (K = V)."""
+    dev = _on_device(q, cache)
+    if q.ndim != 4 or cache.ndim != 3:
+        raise ValueError("q must be [B, Lq, H, R] and cache [B, S, R]")
+    B, Lq, H, R = q.shape
+    if cache.shape[0] != B or cache.shape[2] != R:
+        raise ValueError(f"incompatible shapes q {tuple(q.shape)}, cache {tuple(cache.shape)}")
+    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
+        raise ValueError("MLA decode takes bfloat16 q and cache")
+    dv = R if v_dim is None else int(v_dim)
+    if (R, dv) not in ((576, 512), (576, 576), (512, 512), (128, 128)) or Lq * H > 16:
+        raise ValueError(f"MLA decode supports (R, v_dim) in (576,512),(576,576),(512,512),(128,128) and Lq*H <= 16; got ({R}, {dv}), Lq*H={Lq * H}")
+    S = cache.shape[1]
+    q, cache = q.contiguous(), cache.contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    nbytes = decode_workspace_bytes(B, 1, Lq * H, S, dv, chunk)
+    ws = _workspace(nbytes, dev, workspace)
+    o = torch.empty((B, Lq, H, dv), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    rc = native.load().pjx_mla_decode(
+        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
+        nbytes, B, Lq, H, S, R, dv, float(sm_scale), int(chunk), _stream(dev),
+    )
+    native.check(rc)
+    return (o, lse) if return_lse else o

@@ -1,0 +1,121 @@
+"""Parity of the HIP flash-attention forward with the CPU oracle.
+
+Tolerances (stated by the task for this path): fp32 max-abs <= 1e-5 against
+the oracle; bf16 max-abs <= 2e-2 against an fp32 oracle computed from the same
+bf16-rounded inputs; fully masked rows and masked keys agree exactly.
+"""
+
+import math
+
+import numpy as np
+import pytest
+
+import oracle
+from tests._helpers import max_abs, rng_normal, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+F32_TOL = 1e-5
+BF16_TOL = 2e-2
+
+
+def _flash(*a, **kw):
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    return flash_attention_fwd(*a, **kw)
+
+
+def _inputs(seed, b, lq, lk, hq, hkv, d):
+    return rng_normal(seed, (b, lq, hq, d), (b, lk, hkv, d), (b, lk, hkv, d))
+
+
+@pytest.mark.parametrize(
+    "b,lq,lk,hq,hkv,d,causal",
+    [
+        (1, 512, 512, 4, 4, 64, True),   # config 1
+        (2, 300, 300, 2, 2, 64, True),   # ragged
+        (1, 200, 333, 4, 2, 128, False),  # GQA, unaligned
+        (1, 130, 130, 2, 1, 128, True),
+    ],
+)
+def test_flash_f32_matches_oracle(device, b, lq, lk, hq, hkv, d, causal):
+    import torch
+
+    q, k, v = _inputs(0, b, lq, lk, hq, hkv, d)
+    scale = 1.0 / math.sqrt(d)
+    mask = oracle.CausalMask() if causal else None
+    want, want_lse = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale, return_lse=True)
+    got, lse = _flash(*(to_dev(x, device, torch.float32) for x in (q, k, v)), sm_scale=scale,
+                      causal=causal, return_lse=True)
+    torch.cuda.synchronize()
+    assert max_abs(to_np(got), want) <= F32_TOL
+    assert max_abs(to_np(lse), want_lse) <= 1e-4
+
+
+@pytest.mark.parametrize(
+    "b,lq,lk,hq,hkv,d,causal",
+    [
+        (1, 256, 256, 2, 2, 128, True),
+        (2, 300, 300, 4, 2, 128, True),
+        (1, 100, 517, 2, 2, 64, False),
+        (1, 640, 640, 2, 1, 64, True),
+    ],
+)
+def test_flash_bf16_matches_oracle(device, b, lq, lk, hq, hkv, d, causal):
+    import torch
+
+    q, k, v = (oracle.round_bf16(x) for x in _inputs(1, b, lq, lk, hq, hkv, d))
+    scale = 1.0 / math.sqrt(d)
+    mask = oracle.CausalMask() if causal else None
+    ref32 = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale)
+    got = _flash(*(to_dev(x, device, torch.bfloat16) for x in (q, k, v)), sm_scale=scale, causal=causal)
+    torch.cuda.synchronize()
+    assert max_abs(to_np(got), ref32) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype_name", ["f32", "bf16"])
+def test_flash_bias_kvlen(device, dtype_name):
+    import torch
+
+    b, l, h, d = 2, 256, 4, 64
+    q, k, v = _inputs(2, b, l, l, h, h, d)
+    (bias,) = rng_normal(3, (1, h, l, l), scale=0.5)
+    lengths = np.array([200, 77], np.int32)
+    tdt = torch.float32 if dtype_name == "f32" else torch.bfloat16
+    if dtype_name == "bf16":
+        q, k, v = (oracle.round_bf16(x) for x in (q, k, v))
+    mask = oracle.KVLenMask(lengths)
+    want = oracle.xla_attention(q, k, v, mask=mask, bias=oracle.DenseBias(bias), sm_scale=0.125)
+    got = _flash(*(to_dev(x, device, tdt) for x in (q, k, v)), sm_scale=0.125,
+                 kv_lengths=torch.from_numpy(lengths).to(device), bias=to_dev(bias, device, torch.float32))
+    torch.cuda.synchronize()
+    assert max_abs(to_np(got), want) <= (F32_TOL if dtype_name == "f32" else BF16_TOL)
+
+
+def test_flash_fully_masked_rows_are_zero_and_masked_keys_exact(device):
+    import torch
+
+    b, l, h, d = 2, 128, 2, 128
+    q, k, v = (oracle.round_bf16(x) for x in _inputs(4, b, l, l, h, h, d))
+    lengths = torch.tensor([0, 50], dtype=torch.int32, device=device)
+    args = [to_dev(x, device, torch.bfloat16) for x in (q, k, v)]
+    o1 = _flash(*args, sm_scale=0.1, kv_lengths=lengths)
+    # perturb masked keys/values of batch 1 (positions >= 50)
+    k2, v2 = args[1].clone(), args[2].clone()
+    k2[1, 50:] = 7.0
+    v2[1, 50:] = -3.0
+    o2 = _flash(args[0], k2, v2, sm_scale=0.1, kv_lengths=lengths)
+    torch.cuda.synchronize()
+    assert torch.all(o1[0] == 0)
+    assert torch.equal(o1, o2)
+
+
+def test_flash_deterministic(device):
+    import torch
+
+    q, k, v = (oracle.round_bf16(x) for x in _inputs(5, 1, 384, 384, 2, 2, 128))
+    args = [to_dev(x, device, torch.bfloat16) for x in (q, k, v)]
+    o1 = _flash(*args, sm_scale=0.09, causal=True)
+    o2 = _flash(*args, sm_scale=0.09, causal=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2)
