@@ -1,0 +1,297 @@
+"""Benchmark of the MI355X fused-attention path (one GPU).
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W]`` prints ONE JSON line.
+
+Headline workload (the BASELINE metric's prefill half): the bf16 causal flash
+forward at B=4, H=16, L=4096, D=128 (``configs[1]``).  One step = one
+``pjx_flash_fwd`` call over that batch, inputs resident in HBM.  ``value`` is
+TFLOP/s with the reference's FLOP convention ``4*B*H*Lq*Lk*D``, halved for
+causal (probjax docs/scripts/benchmark_gpu_attention.py:179-187).
+
+The other configurations are measured the same way after the headline and
+reported under ``"configs"`` (decode and MLA as HBM GB/s of the bytes the
+algorithm must move: valid K/V + q + o; bias configs include the bias once).
+
+``cpu_baseline`` times the numpy restatement of probjax's XLA CPU path
+(``oracle.xla_attention``, 256x256 tiles with causal tile skipping) on one
+(batch, head) slice of the headline workload on the host cores, and scales it
+to TFLOP/s.  It is a reported baseline only.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_F32_TFLOPS = 157.3     # MI355X fp32 matrix
+PEAK_HBM_GBS = 8000.0       # MI355X HBM3E
+
+METRIC = "flash-attn fwd TFLOP/s (% bf16 MFMA peak); split-KV decode HBM GB/s (% peak)"
+
+
+def _parse():
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--no-cpu-baseline", action="store_true",
+                   help="skip the timed CPU oracle leg")
+    p.add_argument("--only", default="",
+                   help="comma list of configs to run (C1..C5); default all")
+    return p.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# Workloads: each returns (name, fn, flop, bytes, bound, dtype, extra dict)
+# ---------------------------------------------------------------------------
+
+def _randn(shape, gen, dev, dtype, scale=1.0):
+    import torch
+
+    x = torch.randn(shape, generator=gen, device=dev, dtype=torch.float32)
+    if scale != 1.0:
+        x.mul_(scale)
+    return x.to(dtype)
+
+
+def make_c1(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 1, 512, 4, 64
+    q, k, v = (_randn((B, L, H, D), gen, dev, torch.float32) for _ in range(3))
+    flop = 4 * B * H * L * L * D / 2
+    nbytes = 4 * B * L * H * D * 4
+    fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, causal=True)  # noqa: E731
+    return dict(name="C1 causal fwd f32 B=1 H=4 L=512 D=64", fn=fn, flop=flop, bytes=nbytes,
+                bound="latency", dtype="f32", kernel="flash_fwd_f32_kernel<64,false>")
+
+
+def make_c2(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 4, 4096, 16, 128
+    q, k, v = (_randn((B, L, H, D), gen, dev, torch.bfloat16) for _ in range(3))
+    flop = 4 * B * H * L * L * D / 2
+    nbytes = 4 * B * L * H * D * 2
+    fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
+    return dict(name="C2 causal fwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
+                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_kernel<128,false>")
+
+
+def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
+    """Per-sequence valid lengths, uniform integers in [lo, hi] (seeded)."""
+    return np.random.default_rng(seed).integers(lo, hi + 1, size=batch).astype(np.int32)
+
+
+def make_c3(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import decode_workspace_bytes, splitkv_decode
+
+    B, S, Hq, Hkv, D = 32, 8192, 32, 8, 128
+    q = _randn((B, 1, Hq, D), gen, dev, torch.bfloat16)
+    k = _randn((B, S, Hkv, D), gen, dev, torch.bfloat16)
+    v = _randn((B, S, Hkv, D), gen, dev, torch.bfloat16)
+    lens = c3_lengths()
+    L = torch.from_numpy(lens).to(dev)
+    ws = torch.empty(decode_workspace_bytes(B, Hkv, Hq // Hkv, S, D), dtype=torch.uint8, device=dev)
+    tot = int(lens.sum())
+    nbytes = tot * Hkv * D * 2 * 2 + 2 * B * Hq * D * 2
+    flop = 4 * Hq * D * tot
+    fn = lambda: splitkv_decode(q, k, v, sm_scale=1 / math.sqrt(D), kv_lengths=L, workspace=ws)  # noqa: E731
+    return dict(name="C3 GQA split-KV decode bf16 B=32 Hq=32 Hkv=8 D=128 S=8192 ragged",
+                fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
+                kernel="decode_chunk_kernel<128,2,false>", sum_len=tot)
+
+
+def c4_lengths(seed=0, batch=2, length=2048):
+    """Valid keys per sequence: the last ~10% dropped, offset jittered by +-16 (seeded)."""
+    rng = np.random.default_rng(seed)
+    drop = int(round(0.1 * length)) + rng.integers(-16, 17, size=batch)
+    return (length - drop).astype(np.int32)
+
+
+def make_c4(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 2, 2048, 8, 64
+    q, k, v = (_randn((B, L, H, D), gen, dev, torch.bfloat16) for _ in range(3))
+    bias = _randn((1, H, L, L), gen, dev, torch.float32, scale=0.5)
+    L_ = torch.from_numpy(c4_lengths()).to(dev)
+    flop = 4 * B * H * L * L * D
+    nbytes = H * L * L * 4 + 4 * B * L * H * D * 2
+    fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, kv_lengths=L_, bias=bias)  # noqa: E731
+    return dict(name="C4 bias+kvlen fwd bf16 B=2 H=8 L=2048 D=64, bias f32 [8,2048,2048]",
+                fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
+                kernel="flash_fwd_bf16_kernel<64,true>")
+
+
+def make_c5(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import decode_workspace_bytes, mla_decode
+
+    B, H, S, R, DV = 16, 16, 4096, 576, 512
+    q = _randn((B, 1, H, R), gen, dev, torch.bfloat16)
+    cache = _randn((B, S, R), gen, dev, torch.bfloat16)
+    ws = torch.empty(decode_workspace_bytes(B, 1, H, S, DV), dtype=torch.uint8, device=dev)
+    nbytes = B * S * R * 2 + B * H * R * 2 + B * H * R * 2
+    flop = 2 * B * H * S * (R + DV)
+    fn = lambda: mla_decode(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, workspace=ws)  # noqa: E731
+    return dict(name="C5 MLA absorbed decode bf16 B=16 H=16 S=4096 R=576 Dv=512",
+                fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
+                kernel="decode_chunk_kernel<576,8,true>")
+
+
+MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
+
+
+def _time(fn, steps, warmup):
+    """Wall time of `steps` back-to-back calls between device syncs, and the
+    per-call average from HIP events recorded on the launch stream."""
+    import torch
+
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record(stream)
+    for _ in range(steps):
+        fn()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    return wall / steps * 1e3, e0.elapsed_time(e1) / steps
+
+
+def _rates(w, ms):
+    tflops = w["flop"] / (ms * 1e-3) / 1e12
+    gbs = w["bytes"] / (ms * 1e-3) / 1e9
+    if w["bound"] == "hbm":
+        frac = gbs / PEAK_HBM_GBS
+    elif w["dtype"] == "f32":
+        frac = tflops / PEAK_F32_TFLOPS
+    else:
+        frac = tflops / PEAK_BF16_TFLOPS
+    return tflops, gbs, frac
+
+
+def cpu_baseline(target_s=12.0):
+    """numpy XLA-path restatement on one (b, h) slice of the headline workload."""
+    import oracle
+
+    threads = len(os.sched_getaffinity(0))
+    try:
+        from threadpoolctl import threadpool_limits
+
+        limiter = threadpool_limits(limits=threads)
+    except Exception:  # pragma: no cover - threadpoolctl is optional
+        limiter = None
+    rng = np.random.default_rng(0)
+    L, D = 4096, 128
+    q, k, v = (oracle.round_bf16(rng.standard_normal((1, L, 1, D), dtype=np.float32))
+               for _ in range(3))
+    flop = 4 * L * L * D / 2
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.xla_attention(q, k, v, mask=oracle.CausalMask(), sm_scale=1 / math.sqrt(D),
+                             dtype="bf16")
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= target_s or n >= 50:
+            break
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    per = el / n
+    return {
+        "value": flop / per / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"numpy restatement of xla_attention (256x256 tiles, causal tile skip, bf16 P "
+                  f"rounding), one (b,h) slice 1x4096x1x128 of C2, {n} runs, {per * 1e3:.1f} ms each",
+    }
+
+
+def main():
+    args = _parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
+              "the path's multi-GPU sharding is design-only", file=sys.stderr)
+        sys.exit(2)
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py: no ROCm device visible", file=sys.stderr)
+        sys.exit(1)
+    from probjax_amd import native
+
+    native.load()
+    dev = torch.device("cuda", 0)
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    only = [s.strip() for s in args.only.split(",") if s.strip()] or list(MAKERS)
+
+    results = {}
+    head = None
+    for key in only:
+        w = MAKERS[key](dev, gen)
+        wall_ms, ev_ms = _time(w["fn"], args.steps, args.warmup)
+        tflops, gbs, frac = _rates(w, ev_ms)
+        row = {"workload": w["name"], "ms": round(ev_ms, 5), "wall_ms": round(wall_ms, 5),
+               "tflops": round(tflops, 2), "gbs": round(gbs, 1),
+               "roofline_bound": w["bound"], "roofline_frac": round(frac, 4),
+               "dtype": w["dtype"]}
+        if "sum_len" in w:
+            row["sum_valid_len"] = w["sum_len"]
+        results[key] = row
+        print(f"[bench] {key}: {json.dumps(row)}", file=sys.stderr, flush=True)
+        if key == "C2":
+            head = (w, wall_ms, ev_ms, tflops, frac)
+        del w
+        torch.cuda.empty_cache()
+
+    out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+           "data": "synthetic (torch.randn N(0,1) on device, seed 0)"}
+    if head is not None:
+        w, wall_ms, ev_ms, tflops, frac = head
+        out.update({
+            "value": round(w["flop"] / (wall_ms * 1e-3) / 1e12, 2),
+            "unit": "TFLOP/s",
+            "ms_per_step": round(wall_ms, 5),
+            "dtype": "bf16",
+            "config": {"workload": w["name"], "batch": 4, "heads": 16, "seq_len": 4096,
+                       "head_dim": 128, "mask": "causal", "flop_per_step": w["flop"]},
+            "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
+                         "unit": "TFLOP/s", "frac": round(frac, 4), "traffic": None,
+                         "kernel": w["kernel"]},
+        })
+    if "C3" in results:
+        r = results["C3"]
+        out["decode_roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": PEAK_HBM_GBS,
+                                  "unit": "GB/s", "frac": r["roofline_frac"],
+                                  "kernel": "decode_chunk_kernel<128,2,false> + decode_merge_kernel"}
+    out["configs"] = results
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()
