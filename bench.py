@@ -49,7 +49,23 @@ def _parse():
                    help="skip the timed CPU oracle leg")
     p.add_argument("--only", default="",
                    help="comma list of configs to run (C1..C5); default all")
+    p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                   help="only run a plain device copy of MIB MiB (counter calibration) and exit")
     return p.parse_args()
+
+
+def copy_calibration(mib, reps=5):
+    """A plain device-to-device copy of known size: the reference point that
+    scales FETCH_SIZE / WRITE_SIZE counter readings to bytes."""
+    import torch
+
+    n = mib * (1 << 20) // 4
+    src = torch.ones(n, dtype=torch.float32, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(reps):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "reps": reps}), flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -239,6 +255,9 @@ def main():
     if not torch.cuda.is_available():
         print("bench.py: no ROCm device visible", file=sys.stderr)
         sys.exit(1)
+    if args.copy_calibration:
+        copy_calibration(args.copy_calibration)
+        return
     from probjax_amd import native
 
     native.load()

@@ -86,7 +86,11 @@ def split_partials(q, k, v, *, sm_scale, split_len, kv_lengths=None, dtype="f32"
         valid = np.arange(k0, k1)[None, :] < lengths[:, None]  # [B, keys]
         qk = np.where(valid[:, None, None, :], qk, np.float32(NEG_INF))
         m = np.maximum(np.float32(NEG_INF), qk.max(axis=-1))
-        p = np.exp2(qk - m[..., None])
+        # The reference loads masked K/V as zeros, so a split whose keys are all
+        # masked contributes o = 0 with an LSE of about -1e15 (zero weight in the
+        # merge).  Masked keys get weight exactly 0 here, which gives the same
+        # merged result and also holds for masked keys whose V is not zero.
+        p = np.where(valid[:, None, None, :], np.exp2(qk - m[..., None]), np.float32(0.0))
         l_ = p.sum(axis=-1)
         pv = round_bf16(p) if bf16 else p
         o = np.matmul(pv, vt[:, :, k0:k1])

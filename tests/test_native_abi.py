@@ -1,0 +1,101 @@
+"""The C-ABI library loads and exports every entry point its header declares.
+
+No kernel is launched here: only argument validation paths that return
+before any HIP call are exercised, so this runs without a GPU.
+"""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from probjax_amd import native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "probjax_hip.h"
+
+
+def _declared():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(pjx_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not native.LIB_PATH.exists():
+        pytest.fail(f"{native.LIB_PATH} is not built: run __graft_entry__.build()")
+    return native.load()
+
+
+def test_header_declarations_are_bound():
+    declared = _declared()
+    assert declared, "no entry points parsed from the header"
+    assert sorted(native.EXPORTED) == declared
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert getattr(lib, name, None) is not None, name
+
+
+def test_version_and_error_string(lib):
+    assert lib.pjx_version() >= 100
+    assert isinstance(lib.pjx_last_error(), bytes)
+
+
+def _flash_args(**over):
+    a = dict(dtype=native.PJX_DTYPE_BF16, q=1, k=1, v=1, o=1, lse=None, kvl=None, bias=None,
+             bb=1, bh=1, B=1, Lq=16, Lk=16, Hq=2, Hkv=1, D=128, qv=16, kv=16, causal=1,
+             scale=0.1, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "over,msg",
+    [
+        (dict(dtype=7), "dtype"),
+        (dict(q=None), "non-null"),
+        (dict(D=96), "head_dim"),
+        (dict(Hq=3, Hkv=2), "multiple of kv_heads"),
+        (dict(scale=0.0), "sm_scale"),
+        (dict(bias=1, bb=3), "bias"),
+        (dict(B=-1), "negative"),
+    ],
+)
+def test_flash_rejects_invalid_arguments(lib, over, msg):
+    rc = lib.pjx_flash_fwd(*_flash_args(**over))
+    assert rc == 1
+    assert msg in lib.pjx_last_error().decode()
+
+
+def test_flash_empty_batch_is_a_no_op(lib):
+    assert lib.pjx_flash_fwd(*_flash_args(B=0)) == 0
+
+
+def test_decode_rejects_invalid_arguments(lib):
+    P = ctypes.c_void_p
+    ok = [native.PJX_DTYPE_BF16, P(1), P(1), P(1), None, P(1), None, P(1), 1 << 30,
+          1, 1, 64, 32, 8, 128, 0.1, 0, None]
+    bad_rows = list(ok)
+    bad_rows[12] = 256  # (Hq/Hkv)*Lq = 32 rows > 16
+    assert lib.pjx_splitkv_decode(*bad_rows) == 1
+    assert "<= 16" in lib.pjx_last_error().decode()
+    bad_chunk = list(ok)
+    bad_chunk[16] = 100
+    assert lib.pjx_splitkv_decode(*bad_chunk) == 1
+    assert "chunk" in lib.pjx_last_error().decode()
+    f32 = list(ok)
+    f32[0] = native.PJX_DTYPE_F32
+    assert lib.pjx_splitkv_decode(*f32) == 1
+    mla = [native.PJX_DTYPE_BF16, P(1), P(1), None, P(1), None, P(1), 1 << 30,
+           1, 1, 16, 64, 300, 512, 0.1, 0, None]
+    assert lib.pjx_mla_decode(*mla) == 1
+    assert "rank" in lib.pjx_last_error().decode() or "supported" in lib.pjx_last_error().decode()
+
+
+def test_workspace_size_formula(lib):
+    # partial outputs + (max, sum) per (batch, group, chunk, row), fp32
+    n = lib.pjx_decode_workspace_size(2, 8, 4, 1000, 128, 256)
+    chunks = -(-1000 // 256)
+    assert n == 2 * 8 * chunks * 4 * (128 + 2) * 4

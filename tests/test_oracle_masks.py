@@ -1,0 +1,137 @@
+"""Known-answer tests of the oracle's mask/bias objects.
+
+Restates the reference's own known-answer tests for the masks and biases on
+the path (probjax tests/test_attention_mask_bias.py:54-68 NoMask/Causal,
+:130-136 QKVLengthMask, :152-163 KVLenMask.dense, :191-209 ComposeMask,
+:263-294 DenseBias, :425-453 block masks) against closed forms.
+"""
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle.masks import AttentionMask
+
+
+def _idx(n):
+    return np.arange(n, dtype=np.int32)
+
+
+def _block_from_dense(dense, bq, bk):
+    q_len, k_len = dense.shape
+    nq, nk = -(-q_len // bq), -(-k_len // bk)
+    out = np.zeros((nq, nk), bool)
+    for i in range(nq):
+        for j in range(nk):
+            out[i, j] = dense[i * bq : (i + 1) * bq, j * bk : (j + 1) * bk].any()
+    return out
+
+
+def test_no_mask_all_true():
+    m = oracle.NoMask()(_idx(5), _idx(7))
+    assert m.shape == (5, 7) and m.all()
+    assert oracle.NoMask().block_mask(16, 12, 4, 3) is None
+
+
+def test_causal_lower_triangular_top_left():
+    got = oracle.CausalMask()(_idx(6), _idx(6))
+    np.testing.assert_array_equal(got, np.tril(np.ones((6, 6), bool)))
+    # top-left aligned also for Q != K: row 0 sees key 0 only
+    got = oracle.CausalMask()(_idx(3), _idx(5))
+    assert got[0].tolist() == [True, False, False, False, False]
+
+
+def test_qkv_length_mask_clips_both_axes():
+    got = oracle.QKVLengthMask(4, 6)(_idx(7), _idx(9))
+    want = (_idx(7)[:, None] < 4) & (_idx(9)[None, :] < 6)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_kv_len_mask_dense():
+    lengths = np.array([2, 4, 6], np.int32)
+    dense = oracle.KVLenMask(lengths).dense(5, 6, batch_size=3, num_heads=2)
+    want = np.broadcast_to((_idx(6)[None, :] < lengths[:, None])[:, None, None, :], (3, 2, 5, 6))
+    np.testing.assert_array_equal(dense, want)
+    # explicit rows for batch 0: keys 0, 1 valid
+    assert dense[0, 1, 3].tolist() == [True, True, False, False, False, False]
+
+
+def test_kv_len_mask_payload_and_no_block_mask():
+    m = oracle.KVLenMask([3, 9])
+    data, _ = m.get_data()
+    assert data.shape == (2, 1, 1, 1) and data.ravel().tolist() == [3, 9]
+    assert m.block_mask(16, 16, 4, 4) is None
+    assert m.query_independent and m.stateful
+
+
+@pytest.mark.parametrize("op", ["and", "or", "xor"])
+def test_compose_mask_ops(op):
+    a, b = oracle.CausalMask(), oracle.QKVLengthMask(5, 6)
+    va, vb = a(_idx(8), _idx(8)), b(_idx(8), _idx(8))
+    got = oracle.ComposeMask(op, a, b)(_idx(8), _idx(8))
+    want = {"and": va & vb, "or": va | vb, "xor": va ^ vb}[op]
+    np.testing.assert_array_equal(got, want)
+    np.testing.assert_array_equal((a & b)(_idx(8), _idx(8)), va & vb)
+
+
+def test_compose_two_stateful_raises():
+    with pytest.raises(ValueError, match="Cannot compose two stateful masks"):
+        oracle.ComposeMask("and", oracle.KVLenMask([1]), oracle.KVLenMask([2]))
+
+
+def test_compose_kvlen_and_causal_tile_keep():
+    m = oracle.CausalMask() & oracle.KVLenMask([3, 5])
+    got = m.tile_keep(1, _idx(6), _idx(6))
+    want = np.tril(np.ones((6, 6), bool)) & (_idx(6)[None, :] < 5)
+    np.testing.assert_array_equal(got, want)
+
+
+def test_dense_bias_adds_tile_and_broadcasts():
+    scores = np.ones((2, 3), np.float32)
+    tile = np.arange(6, dtype=np.float32).reshape(2, 3)
+    b = oracle.DenseBias(np.zeros((1, 1, 2, 3), np.float32))
+    np.testing.assert_allclose(b(scores, 0, _idx(2), _idx(3), data=tile), scores + tile)
+    dense = np.arange(12, dtype=np.float32).reshape(1, 1, 3, 4)
+    np.testing.assert_allclose(
+        oracle.DenseBias(dense)(np.zeros((3, 4), np.float32), 0, _idx(3), _idx(4)), dense[0, 0]
+    )
+    got = oracle.DenseBias(dense).dense(3, 4, batch_size=2, num_heads=3)
+    np.testing.assert_array_equal(got, np.broadcast_to(dense, (2, 3, 3, 4)))
+    with pytest.raises(ValueError, match="requires bias batch dimension to be 1"):
+        oracle.DenseBias(np.zeros((2, 1, 3, 4), np.float32))(np.zeros((3, 4)), 0, _idx(3), _idx(4))
+
+
+def test_dense_bias_tile_add_selects_batch_and_head():
+    bias = np.arange(2 * 3 * 4 * 5, dtype=np.float32).reshape(2, 3, 4, 5)
+    s = np.zeros((2, 2), np.float32)
+    got = oracle.DenseBias(bias).tile_add(s, 1, 2, 2, 2, 3, 2)
+    np.testing.assert_array_equal(got, bias[1, 2, 2:4, 3:5])
+    # broadcast head: head index ignored
+    got = oracle.DenseBias(bias[:, :1]).tile_add(s, 1, 2, 0, 2, 0, 2)
+    np.testing.assert_array_equal(got, bias[1, 0, :2, :2])
+    # ragged tile is zero padded
+    got = oracle.DenseBias(bias).tile_add(np.zeros((3, 3), np.float32), 0, 0, 2, 3, 3, 3)
+    assert got[2].tolist() == [0, 0, 0] and got[0, 2] == 0 and got[0, 0] == bias[0, 0, 2, 3]
+
+
+def test_sum_bias_no_double_counting():
+    dense = np.arange(15, dtype=np.float32).reshape(1, 1, 3, 5)
+    s = np.full((3, 5), 2.0, np.float32)
+    b = oracle.DenseBias(dense) + oracle.DenseBias(dense)
+    np.testing.assert_allclose(b.tile_add(s, 0, 0, 0, 3, 0, 5), s + 2 * dense[0, 0])
+
+
+@pytest.mark.parametrize(
+    "mask,q_len,kv_len,bq,bk",
+    [
+        (oracle.CausalMask(), 11, 10, 4, 3),
+        (oracle.QKVLengthMask(6, 7), 9, 11, 4, 3),
+        (oracle.CausalMask() & oracle.QKVLengthMask(6, 7), 12, 12, 4, 4),
+    ],
+)
+def test_block_mask_matches_dense_nonempty_blocks(mask, q_len, kv_len, bq, bk):
+    dense = mask(_idx(q_len), _idx(kv_len))
+    np.testing.assert_array_equal(mask.block_mask(q_len, kv_len, bq, bk), _block_from_dense(dense, bq, bk))
+    # the generic (evaluate every tile) fallback agrees
+    np.testing.assert_array_equal(AttentionMask.block_mask(mask, q_len, kv_len, bq, bk),
+                                  _block_from_dense(dense, bq, bk))
