@@ -94,7 +94,8 @@ size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
  * The (Hq/Hkv)*Lq query rows of a KV head are packed row = g*Lq + t
  * (attention_splitkv.py:121-126); at most 16 rows per KV head.
  * Only keys < kv_lengths[b] are read.  head_dim == 128.
- * chunk: keys per work item (0 = default 256; a multiple of 64).
+ * chunk: keys per work item (0 = automatic: a power of two in [128, 2048]
+ *   leaving about 2048 items at full capacity; else a multiple of 128).
  * workspace: at least pjx_decode_workspace_size(B, Hkv, rows, Lk, D, chunk) bytes.
  */
 int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
@@ -113,8 +114,10 @@ int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
  * o [B, Lq, H, v_dim] bf16 = the first v_dim columns of mla(q, cache, None,
  * None) (v_dim == R gives the API-exact output); lse optional fp32 [B, H, Lq].
  * Lq*H <= 16.  R a multiple of 64, R <= 576; v_dim a multiple of 64, <= R.
+ * chunk: keys per work item (0 = automatic, as for pjx_splitkv_decode; else a
+ *   multiple of 64).
  * workspace: at least pjx_decode_workspace_size(B, 1, Lq*H, S, v_dim, chunk)
- * bytes, chunk = 0 (default) in this call.
+ * bytes with the same chunk.
  */
 int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* kv_lengths,
                    void* o, float* lse, void* workspace, size_t workspace_bytes,
