@@ -98,26 +98,56 @@ __device__ __forceinline__ f32x4 load_bias4(const float* row, int kk, int Lk) {
 
 // ---------------------------------------------------------------------------
 // bf16 path: v_mfma_f32_32x32x16_bf16 for both products.
+//
+// K/V tiles of BK keys go HBM -> LDS with buffer loads that write LDS
+// directly (no VGPR staging), two stages: the loads of tile t+1 are issued
+// right after the barrier that opens tile t, so they overlap its arithmetic.
+// Each buffer resource spans only the tile's valid rows, so rows past the
+// last visited key read as zero without any predication.  Per-lane LDS
+// offsets are computed once; the key loop does no address arithmetic.
+//
+// LDS layout: row-major [key][dim] rows of D*2 bytes, 16-byte chunks XOR-
+// swizzled per row (K: chunk ^ (row & (NC-1)); V: chunk ^ f(row) chosen so a
+// transposing read of 4 rows x 32 bytes per 16 lanes hits distinct banks).
+// K fragments are ds_read_b128; V^T fragments come from ds_read_b64_tr_b16
+// straight out of the row-major V tile.
+//
+// Softmax: the running max used for exponentiation is only raised when a
+// row's tile max exceeds it by more than kRescaleLog2 (wave-uniform branch),
+// so the O rescale (D/2 multiplies per lane) runs on a few tiles per row
+// instead of every tile; P stays <= 2^kRescaleLog2, exact in bf16 range.  The
+// normalised output is the same softmax: O / l with l accumulated against the
+// same reference max.
 // ---------------------------------------------------------------------------
+constexpr float kRescaleLog2 = 8.0f;
+
+template <int D>
+struct Bf16Tile {
+  static constexpr int BK = 64;             // keys per tile
+  static constexpr int ROWB = D * 2;        // bytes per K/V row
+  static constexpr int NC = D / 8;          // 16-byte chunks per row
+  static constexpr int TILE_B = BK * ROWB;  // bytes of one K (or V) tile
+  static constexpr int STAGE_B = 2 * TILE_B;
+  static constexpr int RPI = 64 / NC;       // rows per 1 KiB buffer->LDS load
+  static constexpr int NLD = (BK / 4) / RPI;  // loads per wave per tensor per tile
+  __device__ static int swz_k(int r) { return r & (NC - 1); }
+  __device__ static int swz_v(int r) {
+    return D == 128 ? 4 * (r & 3) + 2 * ((r >> 1) & 1) : 4 * ((r >> 1) & 1) + 2 * (r & 1);
+  }
+};
+
 template <int D, bool BIAS>
 __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
-  constexpr int BK = 64;
-  constexpr int KS = D + 8;   // K row stride in LDS (bf16): 16 B pad -> conflict-free b128 reads
-  constexpr int VS = BK + 4;  // V^T row stride (bf16): 34 dwords -> conflict-free b64 reads
-  constexpr int DC = D / 8;   // 16-byte chunks per K/V row
-  constexpr int K_PER_T = BK * DC / kThreads;
-  constexpr int V_UNITS = (BK / 4) * DC;  // 4 keys x 8 dims per unit
-  static_assert(K_PER_T >= 1 && V_UNITS <= kThreads, "tile shape");
-
-  __shared__ __attribute__((aligned(16))) uint16_t k_lds[2][BK * KS];
-  __shared__ __attribute__((aligned(16))) uint16_t v_lds[2][D * VS];
+  using T = Bf16Tile<D>;
+  constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_B];
 
   const BlockGeom g = block_geom(a);
-  const int tid = threadIdx.x, lane = tid & 63;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane & 31, half = lane >> 5;
-  const size_t kv_row = (size_t)a.Hkv * D;
-  const uint16_t* Kb = (const uint16_t*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
-  const uint16_t* Vb = (const uint16_t*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
+  const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
+  const unsigned char* Vb = (const unsigned char*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
   const bool row_in = g.qi < a.Lq;
   const bool row_ok = g.qi < g.q_hi;
 
@@ -133,7 +163,6 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
       qf[s] = as_bf16x8(raw);
     }
   }
-
   const float* brow = nullptr;
   if constexpr (BIAS) {
     brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
@@ -141,6 +170,28 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   }
   const bool bias_vec = (a.Lk & 3) == 0;
   const float cx = BIAS ? kLog2e : a.scale * kLog2e;  // score units -> log2 units
+
+  // Per-lane byte offsets, fixed for the whole key loop.
+  uint32_t voffK[T::NLD], voffV[T::NLD];
+#pragma unroll
+  for (int j = 0; j < T::NLD; ++j) {
+    const int r = 16 * w + T::RPI * j + lane / T::NC, slot = lane % T::NC;
+    voffK[j] = r * rowstride + 16 * (slot ^ T::swz_k(r));
+    voffV[j] = r * rowstride + 16 * (slot ^ T::swz_v(r));
+  }
+  uint32_t offK[D / 16];  // K row `col` (of a 32-key block), dims 16*st + 8*half
+#pragma unroll
+  for (int st = 0; st < D / 16; ++st) offK[st] = col * ROWB + 16 * ((2 * st + half) ^ T::swz_k(col));
+  uint32_t offV[D / 32];  // transposing-read source of this lane for output dims 32*db..
+  {
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int r = 4 * half + s16 / 4;  // row within a 16-key step (mod 4 = s16/4)
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int chunk = 4 * db + 2 * (grp & 1) + ((s16 & 3) >> 1);
+      offV[db] = r * ROWB + 16 * (chunk ^ T::swz_v(r)) + 8 * (s16 & 1);
+    }
+  }
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -150,62 +201,26 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   const int n_tiles = (g.kv_stop + BK - 1) / BK;
   const int q_last_w = g.qw + 31;
 
-  u32x4 kreg[K_PER_T];
-  u32x4 vreg[4];
-
-  auto load_tile = [&](int t) {
+  auto issue = [&](int t, int stage) {
     const int k0 = t * BK;
+    const int nvalid = min(BK, g.kv_stop - k0);
+    const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
+    const rsrc_t rk = make_rsrc(Kb + (size_t)k0 * rowstride, bytes);
+    const rsrc_t rv = make_rsrc(Vb + (size_t)k0 * rowstride, bytes);
+    unsigned char* ks = smem + stage * STAGE_B;
 #pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int u = tid + kThreads * i;
-      const int kk = k0 + u / DC, dc = u % DC;
-      u32x4 r = {0u, 0u, 0u, 0u};
-      if (kk < g.kv_stop) r = *(const u32x4*)(Kb + (size_t)kk * kv_row + dc * 8);
-      kreg[i] = r;
-    }
-    if (tid < V_UNITS) {
-      const int dc = tid % DC, kq = tid / DC;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int kk = k0 + 4 * kq + j;
-        u32x4 r = {0u, 0u, 0u, 0u};
-        if (kk < g.kv_stop) r = *(const u32x4*)(Vb + (size_t)kk * kv_row + dc * 8);
-        vreg[j] = r;
-      }
+    for (int j = 0; j < T::NLD; ++j) {
+      const int r0 = 16 * w + T::RPI * j;
+      buffer_load_lds16(rk, ks + r0 * ROWB, voffK[j]);
+      buffer_load_lds16(rv, ks + TILE_B + r0 * ROWB, voffV[j]);
     }
   };
 
-  auto store_tile = [&](int buf) {
-    uint16_t* kl = k_lds[buf];
-#pragma unroll
-    for (int i = 0; i < K_PER_T; ++i) {
-      const int u = tid + kThreads * i;
-      *(u32x4*)(kl + (u / DC) * KS + (u % DC) * 8) = kreg[i];
-    }
-    if (tid < V_UNITS) {
-      uint16_t* vl = v_lds[buf];
-      const int dc = tid % DC, kq = tid / DC;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int dw = e >> 1;
-        u32x2 pk;
-        if (e & 1) {
-          pk[0] = pack_hi_halves(vreg[0][dw], vreg[1][dw]);
-          pk[1] = pack_hi_halves(vreg[2][dw], vreg[3][dw]);
-        } else {
-          pk[0] = pack_lo_halves(vreg[0][dw], vreg[1][dw]);
-          pk[1] = pack_lo_halves(vreg[2][dw], vreg[3][dw]);
-        }
-        *(u32x2*)(vl + (dc * 8 + e) * VS + 4 * kq) = pk;
-      }
-    }
-  };
-
-  auto compute = [&](int t, int buf) {
+  auto compute = [&](int t, int stage) {
     const int k0 = t * BK;
     if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
-    const uint16_t* kl = k_lds[buf];
-    const uint16_t* vl = v_lds[buf];
+    const unsigned char* ks = smem + stage * STAGE_B;
+    const unsigned char* vs = ks + TILE_B;
 
     // S^T[key][query] = K Q^T
     f32x16 s[BK / 32];
@@ -214,7 +229,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
       s[kb] = f32x16{};
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 kf = as_bf16x8(*(const u32x4*)(kl + (kb * 32 + col) * KS + 16 * st + 8 * half));
+        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
         s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
       }
     }
@@ -251,25 +266,28 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx * cx);
-    const float corr = fast_exp2(m_run - m_new);
-    m_run = m_new;
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[kb][r], s[kb][r + 1]));
+    const float mc = xor32_max(mx) * cx;
+    if (wave_any(mc > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mc);
+      const float corr = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+    }
     float rs = 0.f;
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_new));
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_run));
         rs += p;
         s[kb][r] = p;
       }
-    l_run = fmaf(l_run, corr, rs);
-#pragma unroll
-    for (int i = 0; i < D / 32; ++i)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+    l_run += rs;
 
     // P^T as the B operand, 16 keys per MFMA step c:
     // slot j <-> key 16c + 8*(j/4) + 4*half + j%4 (registers 8*(c%2)+j of block c/2).
@@ -282,30 +300,26 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
         pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
       pf[c] = as_bf16x8(pk);
     }
-    // O^T[d][query] += V^T P^T; the A operand reads the same key order from V^T.
+    // O^T[d][query] += V^T P^T; A operand = V^T rows 32*db.., keys in P's slot order,
+    // from two transposing reads (keys 16c + 4*half + [0,4) and 16c + 8 + 4*half + [0,4)).
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
 #pragma unroll
       for (int c = 0; c < BK / 16; ++c) {
-        const uint16_t* vp = vl + (db * 32 + col) * VS + 16 * c + 4 * half;
-        const u32x2 lo = *(const u32x2*)vp;
-        const u32x2 hi = *(const u32x2*)(vp + 8);
+        const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + offV[db]);
+        const u32x2 hi = lds_read_tr16(vs + (16 * c + 8) * ROWB + offV[db]);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
         acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
       }
     }
   };
 
-  if (n_tiles > 0) {
-    load_tile(0);
-    store_tile(0);
-  }
-  __syncthreads();
+  if (n_tiles > 0) issue(0, 0);
   for (int t = 0; t < n_tiles; ++t) {
-    if (t + 1 < n_tiles) load_tile(t + 1);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t have landed in LDS
+    __syncthreads();                // ... every wave's; and stage (t+1)&1 is free
+    if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
     compute(t, t & 1);
-    if (t + 1 < n_tiles) store_tile((t + 1) & 1);
-    __syncthreads();
   }
 
   const float l_tot = xor32_sum(l_run);

@@ -85,3 +85,38 @@ __device__ __forceinline__ T ldg_or_zero(const T* p, bool ok) {
 }
 
 }  // namespace pjx
+
+namespace pjx {
+
+// ---------------------------------------------------------------------------
+// Buffer resources, buffer -> LDS loads and the transposing LDS read (gfx950).
+// ---------------------------------------------------------------------------
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef uint16_t b16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+
+// Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+}
+
+// Each lane loads 16 bytes at voffset; lane l's bytes land at lds_wave + 16*l
+// (lds_wave must be the same for every lane of the wave).
+__device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void* lds_wave, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16,
+                                           voffset, 0, 0, 0);
+}
+
+// ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
+// i%4 of the 8-byte words addressed by lanes i/4, i/4+4, i/4+8, i/4+12 (in
+// that order).  Pointing lane s at row (s/4), 16-bit columns 4*(s%4)..+3 of a
+// row-major tile hands lane i column i of 4 consecutive rows: a transposed
+// 4 x 16 block.  (Lane layout measured on MI355X.)
+__device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
+  s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  return __builtin_bit_cast(u32x2, v);
+}
+
+__device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
+
+}  // namespace pjx
