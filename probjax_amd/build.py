@@ -27,6 +27,10 @@ HIPCC_FLAGS = [
     "-fPIC",
     "-Wall",
     "-Wno-unused-result",
+    # NaN inputs still propagate (through exp2, the row sums and the outputs);
+    # this only drops the canonicalising moves the compiler puts around every
+    # fmaxf of the row-max reductions.
+    "-fno-honor-nans",
     # Packed-fp32 VALU forms are disabled for every kernel of this library.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
 ]

@@ -140,10 +140,18 @@ template <int D, bool BIAS>
 __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
   using T = Bf16Tile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE_B];
+  // Two stages as distinct LDS objects: the compiler can then prove that the
+  // buffer->LDS loads in flight for one stage do not alias reads of the other
+  // (one array indexed by stage would make it wait for those loads first).
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
 
-  const BlockGeom g = block_geom(a);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  // Wave index and the wave's first row as wave-uniform (scalar) values, so
+  // that branches on them are scalar branches.
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  g.qw = __builtin_amdgcn_readfirstlane(g.qw);
   const int col = lane & 31, half = lane >> 5;
   const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
   const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
@@ -201,13 +209,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   const int n_tiles = (g.kv_stop + BK - 1) / BK;
   const int q_last_w = g.qw + 31;
 
-  auto issue = [&](int t, int stage) {
+  auto issue = [&](int t, unsigned char* ks) {
     const int k0 = t * BK;
     const int nvalid = min(BK, g.kv_stop - k0);
     const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
     const rsrc_t rk = make_rsrc(Kb + (size_t)k0 * rowstride, bytes);
     const rsrc_t rv = make_rsrc(Vb + (size_t)k0 * rowstride, bytes);
-    unsigned char* ks = smem + stage * STAGE_B;
 #pragma unroll
     for (int j = 0; j < T::NLD; ++j) {
       const int r0 = 16 * w + T::RPI * j;
@@ -216,10 +223,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     }
   };
 
-  auto compute = [&](int t, int stage) {
+  auto compute = [&](int t, const unsigned char* ks) {
     const int k0 = t * BK;
     if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
-    const unsigned char* ks = smem + stage * STAGE_B;
     const unsigned char* vs = ks + TILE_B;
 
     // S^T[key][query] = K Q^T
@@ -251,15 +257,16 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
                            (g.qw + 31 >= g.q_hi);
     if (need_mask) {
+      // Key k0 + 4*half + o (o = kb*32 + 8*(r/4) + r%4) is kept iff o <= lim.
+      const int base = k0 + 4 * half;
+      int lim = g.kv_end - 1 - base;
+      if (a.causal) lim = min(lim, g.qi - base);
+      if (!row_ok) lim = -1;
 #pragma unroll
-      for (int kb = 0; kb < BK / 32; ++kb) {
+      for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = k0 + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const bool keep = row_ok && kk < g.kv_end && (!a.causal || kk <= g.qi);
-          if (!keep) s[kb][r] = -INFINITY;
-        }
-      }
+        for (int r = 0; r < 16; ++r)
+          if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
     }
 
     float mx = -INFINITY;
@@ -314,12 +321,21 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     }
   };
 
-  if (n_tiles > 0) issue(0, 0);
-  for (int t = 0; t < n_tiles; ++t) {
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads of tile t have landed in LDS
-    __syncthreads();                // ... every wave's; and stage (t+1)&1 is free
-    if (t + 1 < n_tiles) issue(t + 1, (t + 1) & 1);
-    compute(t, t & 1);
+  // Tile t lives in stage t % 2.  At the top of each step: this wave's loads of
+  // tile t have landed (waitcnt), then every wave's have and every wave is done
+  // reading the other stage (barrier), so tile t+1's loads can go there while
+  // tile t is computed.
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
   }
 
   const float l_tot = xor32_sum(l_run);
