@@ -14,10 +14,13 @@ import numpy as np
 def round_bf16(x):
     """Round float32 values to the nearest bfloat16 (RNE); returns float32."""
     x = np.ascontiguousarray(x, dtype=np.float32)
-    u = x.view(np.uint32).astype(np.uint64)
-    lsb = (u >> np.uint64(16)) & np.uint64(1)
-    r = ((u + np.uint64(0x7FFF) + lsb) >> np.uint64(16)) << np.uint64(16)
-    out = (r & np.uint64(0xFFFFFFFF)).astype(np.uint32).view(np.float32).copy()
+    u = x.view(np.uint32)
+    # u + 0x7FFF + lsb stays below 2^32 for every non-NaN bit pattern (the
+    # largest, -inf/-max, is 0xFF800000 + 0x8000); NaNs are restored below.
+    r = u + np.uint32(0x7FFF)
+    r += (u >> np.uint32(16)) & np.uint32(1)
+    r &= np.uint32(0xFFFF0000)
+    out = r.view(np.float32)
     nan = np.isnan(x)
     if nan.any():
         out[nan] = np.nan

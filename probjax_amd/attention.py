@@ -1,0 +1,416 @@
+"""probjax.nn's fused-attention API served by the MI355X (gfx950) HIP kernels.
+
+The functions keep probjax's names, argument meanings, defaults and error
+messages for the fused-attention path, on torch tensors resident on a ROCm
+device (torch provides the HBM buffers and the stream; the arithmetic is the
+HIP library behind ``include/probjax_hip.h``):
+
+* ``hip_attention_or_none`` -- a route with the protocol of probjax's
+  ``cudnn_attention_or_none`` / ``mosaic_attention_or_none``
+  (probjax/nn/layers/attention_device.py:165-237): inputs ``[B, T, H, D]``,
+  returns the output, or ``None`` to fall through; ``force=True`` skips the
+  device table and the environment switch;
+* ``flex_attention`` / ``dot_product_attention`` -- the dispatchers
+  (layers/attention.py:1205-1319, 1426-1759) with ``implementation="hip"``
+  (or ``None`` = the device table) in place of the Triton/cuDNN/Mosaic
+  choices; default ``sm_scale = 1/sqrt(D)``;
+* ``mha`` -- the kernel API (pallas_kernels/kernels/attention.py:2692-2984),
+  default ``sm_scale = 1.0``, split-KV decoding chosen by ``use_splitkv``
+  (:2653-2689) extended to ``KVLenMask``;
+* ``splitkv_forward`` -- kernels/attention_splitkv.py:137-250;
+* ``mla`` -- kernels/latent_attention.py:636-766, absorbed form (``wk = wv =
+  None``), default ``sm_scale = 1/sqrt(qk_head_dim)``.
+
+There is no CPU or library fallback: a call the kernels cannot compute
+exactly raises ``ValueError`` (forced paths) or returns ``None`` (the route),
+and a missing kernel library raises ``NativeLibraryError``.
+
+Device table: the route is on by default on gfx950 devices; set
+``PROBJAX_ATTENTION_HIP=0`` to turn the default route off (forced calls still
+run), mirroring ``PROBJAX_ATTENTION_CUDNN`` / ``PROBJAX_ATTENTION_MOSAIC``.
+"""
+
+from __future__ import annotations
+
+import functools
+import math
+import os
+
+import torch
+
+from . import hip_attention as hip
+from .masks import LoweredMask, lower_bias, lower_mask
+
+HIP_ARCH = "gfx950"
+FLASH_HEAD_DIMS = (64, 128)
+DECODE_HEAD_DIMS = (64, 128)
+DECODE_MAX_ROWS = 16
+MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
+
+# Split-KV decode thresholds (probjax kernels/attention.py:2649-2650).
+_SPLITKV_MAX_Q_LEN = 64
+_SPLITKV_MIN_KV_LEN = 1024
+
+
+def _env_off(name: str) -> bool:
+    """attention_device.py:67-68."""
+    return os.environ.get(name, "1").strip().lower() in ("0", "false", "no", "off")
+
+
+@functools.lru_cache(maxsize=None)
+def _device_arch(index: int) -> str:
+    return torch.cuda.get_device_properties(index).gcnArchName.split(":")[0]
+
+
+def hip_device(t) -> bool:
+    """``t`` lives on a gfx950 ROCm device."""
+    if not isinstance(t, torch.Tensor) or t.device.type != "cuda":
+        return False
+    return _device_arch(t.device.index if t.device.index is not None else 0) == HIP_ARCH
+
+
+def device_table_enabled() -> bool:
+    return not _env_off("PROBJAX_ATTENTION_HIP") and not _env_off("PROBJAX_ATTENTION_DEVICE_DEFAULTS")
+
+
+# ---------------------------------------------------------------------------
+# Eligibility
+# ---------------------------------------------------------------------------
+
+def _lengths_tensor(kv_lengths, batch, device):
+    L = torch.as_tensor(kv_lengths, device=device).reshape(-1)
+    if L.numel() != batch:
+        return None
+    return L.to(torch.int32)
+
+
+def _decode_plan(query, key, value, lm: LoweredMask, bias_t):
+    """Arguments of the split-KV decode for this call, or None."""
+    if bias_t is not None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+        return None
+    if query.dtype != torch.bfloat16:
+        return None
+    B, l_q, h_q, d = query.shape
+    h_kv = key.shape[2]
+    if d not in DECODE_HEAD_DIMS or (h_q // h_kv) * l_q > DECODE_MAX_ROWS:
+        return None
+    return dict(kv_lengths=lm.kv_lengths)
+
+
+def _flash_plan(query, key, value, lm: LoweredMask, bias_t):
+    """Arguments of the flash forward for this call, or None."""
+    if query.dtype not in (torch.bfloat16, torch.float32):
+        return None
+    B, l_q, h_q, d = query.shape
+    if d not in FLASH_HEAD_DIMS:
+        return None
+    if bias_t is not None:
+        l_k = key.shape[1]
+        if bias_t.ndim != 4 or tuple(bias_t.shape[-2:]) != (l_q, l_k):
+            return None
+        if bias_t.shape[0] not in (1, B) or bias_t.shape[1] not in (1, h_q):
+            return None
+    return dict(causal=lm.causal, kv_lengths=lm.kv_lengths, bias=bias_t,
+                q_valid=lm.q_valid, kv_valid=lm.kv_valid)
+
+
+def _eligible(query, key, value, *, mask, bias, dropout_rate):
+    """(lowered mask, bias tensor) when the kernels compute the call exactly."""
+    if dropout_rate > 0.0:
+        return None
+    if query.ndim != 4 or key.ndim != 4 or value.ndim != 4:
+        return None
+    if not (query.dtype == key.dtype == value.dtype):
+        return None
+    if not (hip_device(query) and key.device == query.device and value.device == query.device):
+        return None
+    B, l_q, h_q, d = query.shape
+    if key.shape[0] != B or value.shape != key.shape or key.shape[-1] != d or h_q % key.shape[2]:
+        return None
+    lm = lower_mask(mask)
+    if lm is None:
+        return None
+    if lm.kv_lengths is not None:
+        L = _lengths_tensor(lm.kv_lengths, B, query.device)
+        if L is None:
+            return None
+        lm.kv_lengths = L
+    bias_t = lower_bias(bias)
+    if bias_t is False:
+        return None
+    if bias_t is not None:
+        bias_t = bias_t.to(device=query.device, dtype=torch.float32)
+    return lm, bias_t
+
+
+def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: float,
+                split_kv: bool | None) -> bool:
+    if split_kv is False:
+        return False
+    if q.ndim != 4 or k.ndim != 4 or dropout_rate > 0 or has_bias:
+        return False
+    if lm is None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+        return False
+    if q.dtype != torch.bfloat16 or q.shape[-1] not in DECODE_HEAD_DIMS:
+        return False
+    if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or (q.shape[2] // k.shape[2]) * q.shape[1] > DECODE_MAX_ROWS:
+        return False
+    if split_kv:
+        return True
+    return q.shape[1] <= _SPLITKV_MAX_Q_LEN and k.shape[1] >= _SPLITKV_MIN_KV_LEN
+
+
+def use_splitkv(q, k, *, mask=None, bias=None, dropout_rate: float = 0.0,
+                split_kv: bool | None = None) -> bool:
+    """Whether ``mha`` runs the split-KV decode for these inputs.
+
+    probjax's rule (kernels/attention.py:2653-2689): never with
+    ``split_kv=False``; only exact cases (no bias, no dropout); ``True``
+    forces it when exact; ``None`` picks it for ``Lq <= 64`` and
+    ``Lkv >= 1024``.  The HIP decode is also exact with a ``KVLenMask`` (keys
+    past each length are skipped), so a length mask does not disable it here;
+    it needs bf16, head_dim 64/128 and ``(Hq/Hkv)*Lq <= 16``.
+    """
+    return _splitkv_ok(q, k, lower_mask(mask), bias is not None, dropout_rate, split_kv)
+
+
+def _run(query, key, value, lm, bias_t, sm_scale, split_kv):
+    if _splitkv_ok(query, key, lm, bias_t is not None, 0.0, split_kv):
+        plan = _decode_plan(query, key, value, lm, bias_t)
+        if plan is not None:
+            return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, **plan)
+    plan = _flash_plan(query, key, value, lm, bias_t)
+    if plan is None:
+        return None
+    return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, **plan)
+
+
+# ---------------------------------------------------------------------------
+# Route (selector seam)
+# ---------------------------------------------------------------------------
+
+def hip_attention_or_none(query, key, value, *, mask, bias, dropout_rate: float,
+                          sm_scale: float, force: bool = False):
+    """HIP fused attention when the device table routes this call there.
+
+    Inputs are ``[B, T, H, D]`` (K/V may have fewer heads, GQA).  Returns the
+    output, or None to fall through (``force=True``: skip the device table and
+    the environment switch, only check that the kernels compute the call
+    exactly).
+    """
+    if not force and not device_table_enabled():
+        return None
+    e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=dropout_rate)
+    if e is None:
+        return None
+    lm, bias_t = e
+    return _run(query, key, value, lm, bias_t, float(sm_scale), None)
+
+
+# ---------------------------------------------------------------------------
+# Kernel API
+# ---------------------------------------------------------------------------
+
+def _gqa_group(hq: int, hkv: int) -> int:
+    if hkv <= 0 or hq % hkv:
+        raise ValueError(f"number of query heads ({hq}) must be a multiple of KV heads ({hkv})")
+    return hq // hkv
+
+
+def mha(q, k, v, mask=None, bias=None, rng=None, sm_scale: float = 1.0, *,
+        dropout_rate: float = 0.0, split_kv: bool | None = None, **unused_tuning):
+    """Multi-head attention (probjax ``mha``): ``q [B, Lq, Hq, D]``,
+    ``k/v [B, Lk, Hkv, D]`` -> ``[B, Lq, Hq, D]``.
+
+    ``sm_scale`` defaults to 1.0 as in probjax.  Tiling arguments of the Pallas
+    API (``block_sizes``, ``num_warps``, ...) are accepted and ignored: the HIP
+    kernels choose their tiles.  Raises ``ValueError`` for calls the kernels
+    cannot compute exactly (dropout, masks/biases other than those in
+    ``probjax_amd.masks``, unsupported dtype or head_dim).
+    """
+    del rng, unused_tuning
+    _gqa_group(q.shape[-2], k.shape[-2])
+    if v.shape[-2] != k.shape[-2]:
+        raise ValueError(
+            f"key and value need the same number of heads, got {k.shape[-2]} and {v.shape[-2]}."
+        )
+    e = _eligible(q, k, v, mask=mask, bias=bias, dropout_rate=dropout_rate)
+    out = None if e is None else _run(q, k, v, e[0], e[1], float(sm_scale), split_kv)
+    if out is None:
+        raise ValueError(_unsupported_message(q, k, mask, bias, dropout_rate))
+    return out
+
+
+def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
+    why = []
+    if not hip_device(q):
+        why.append(f"tensors must be on a {HIP_ARCH} ROCm device (got {getattr(q, 'device', None)})")
+    if dropout_rate > 0:
+        why.append("dropout is not supported")
+    if lower_mask(mask) is None:
+        why.append(f"mask {type(mask).__name__} is not supported")
+    if lower_bias(bias) is False:
+        why.append(f"bias {type(bias).__name__} is not supported")
+    if getattr(q, "dtype", None) not in (torch.bfloat16, torch.float32):
+        why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp32)")
+    if q.ndim == 4 and q.shape[-1] not in FLASH_HEAD_DIMS:
+        why.append(f"head_dim {q.shape[-1]} is not supported {FLASH_HEAD_DIMS}")
+    detail = "; ".join(why) or "unsupported shape combination"
+    return f"the HIP attention kernels cannot compute this call exactly: {detail}"
+
+
+def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
+                    block_k: int = 64, return_lse: bool = False, kv_lengths=None,
+                    **unused_tuning):
+    """Split-KV ("flash-decoding") forward (probjax ``splitkv_forward``,
+    kernels/attention_splitkv.py:137-250): ``q [B, Lq, Hq, D]`` bf16,
+    ``k/v [B, Lkv, Hkv, D]``; ``(Hq/Hkv)*Lq <= 16``.
+
+    ``num_splits`` maps to KV chunks of ``ceil(Lkv / num_splits)`` keys rounded
+    up to 128 (``None``: the kernel's own choice).  ``kv_lengths`` ([B]) is the
+    KVLenMask extension.  With ``return_lse`` also returns the natural-log LSE
+    ``[B, Hq, Lq]`` (attention_splitkv.py:248-250; ``+inf`` for empty rows).
+    """
+    del block_k, unused_tuning
+    _gqa_group(q.shape[-2], k.shape[-2])
+    chunk = 0
+    if num_splits is not None:
+        if num_splits < 1:
+            raise ValueError(f"num_splits must be >= 1, got {num_splits}")
+        per = -(-k.shape[1] // num_splits)
+        chunk = max(128, -(-per // 128) * 128)
+    return hip.splitkv_decode(q, k, v, sm_scale=float(sm_scale), kv_lengths=kv_lengths,
+                              chunk=chunk, return_lse=return_lse)
+
+
+def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
+        sm_scale: float | None = None, dropout_rate: float = 0.0, v_dim: int | None = None,
+        **unused_tuning):
+    """Attention of ``q`` over a shared latent ``cache`` (probjax ``mla``,
+    kernels/latent_attention.py:636-766), absorbed form ``K = V = cache``.
+
+    ``q [B, Q, H, R]``, ``cache [B, S, R]`` -> ``[B, Q, H, R]`` (or the first
+    ``v_dim`` columns, which is all a caller that multiplies by ``W_UV`` of
+    width ``v_dim`` needs).  ``mask``: ``None`` / ``NoMask`` / ``KVLenMask``.
+    Materialised mode (``wk``/``wv`` given) and biases raise ``ValueError``.
+    """
+    del rng, unused_tuning
+    if q.ndim != 4:
+        raise ValueError(f"q must be rank 4 [B,Q,H,D], got shape {tuple(q.shape)}")
+    if cache.ndim != 3:
+        raise ValueError(f"cache must be rank 3 [B,S,R], got shape {tuple(cache.shape)}")
+    if q.shape[0] != cache.shape[0]:
+        raise ValueError(f"batch mismatch: q has {q.shape[0]}, cache has {cache.shape[0]}")
+    if (wk is None) != (wv is None):
+        raise ValueError(
+            "provide both wk and wv (materialized) or neither (absorbed); "
+            "mixing the two is not supported"
+        )
+    if wk is None and q.shape[-1] != cache.shape[-1]:
+        raise ValueError(
+            "absorbed mode (wk=None) requires qk_head_dim == kv_lora_rank "
+            f"({q.shape[-1]} != {cache.shape[-1]})"
+        )
+    if wk is not None:
+        raise ValueError("the HIP latent-attention kernel takes the absorbed form (wk = wv = None)")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    if bias is not None or dropout_rate > 0:
+        raise ValueError("the HIP latent-attention kernel takes no bias or dropout")
+    lm = lower_mask(mask)
+    if lm is None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+        raise ValueError(f"the HIP latent-attention kernel takes None / NoMask / KVLenMask, got {type(mask).__name__}")
+    if not hip_device(q):
+        raise ValueError(f"the HIP latent-attention kernel needs tensors on a {HIP_ARCH} ROCm device")
+    return hip.mla_decode(q, cache, sm_scale=float(sm_scale), v_dim=v_dim, kv_lengths=lm.kv_lengths)
+
+
+# ---------------------------------------------------------------------------
+# Dispatchers (probjax.nn.layers.attention)
+# ---------------------------------------------------------------------------
+
+def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
+                   dropout_rate: float = 0.0, broadcast_dropout: bool = False,
+                   deterministic=True, dtype=None, precision=None, module=None,
+                   sm_scale: float | None = None, enable_gqa: bool = False,
+                   split_kv: bool | None = None, implementation: str | None = None,
+                   **unused_tuning):
+    """Fused softmax attention with mask/bias objects (probjax
+    ``flex_attention``, layers/attention.py:1426-1759).
+
+    ``implementation``: ``None`` (the device table: the HIP route on gfx950
+    unless ``PROBJAX_ATTENTION_HIP=0``) or ``"hip"`` (forced; ``ValueError``
+    when the kernels cannot compute the call exactly).  Rank-3 inputs get a
+    leading batch axis; ``sm_scale`` defaults to ``1/sqrt(D)``.
+    """
+    del dropout_rng, broadcast_dropout, precision, module, unused_tuning
+    if dtype is not None:
+        query, key, value = (x.to(dtype) for x in (query, key, value))
+    if (query.dtype != key.dtype) or (query.dtype != value.dtype):
+        raise ValueError(
+            f"Expected query, key, and value to have the same dtype, "
+            f"but got query.dtype: {query.dtype}, key.dtype: {key.dtype}, "
+            f"and value.dtype: {value.dtype} instead."
+        )
+    if (query.ndim < 3) or (key.ndim < 3) or (value.ndim < 3):
+        raise ValueError(
+            f"Expected query, key, and value to all be at least 3 dimensional, but got query.ndim: "
+            f"{query.ndim}, key.ndim: {key.ndim}, and value.ndim: {value.ndim} instead."
+        )
+    if (not enable_gqa) and query.shape[-2] != key.shape[-2]:
+        raise ValueError(
+            f"Expect query and key/value to have the same number of heads "
+            f"but got Hq={query.shape[-2]} and Hkv={key.shape[-2]}. "
+            f"Try setting enable_gqa=True for GQA."
+        )
+    if enable_gqa and query.shape[-2] % key.shape[-2] != 0:
+        raise ValueError(
+            f"Expect number of query heads to be a multiple of kv heads for GQA "
+            f"but got Hq={query.shape[-2]} and Hkv={key.shape[-2]}."
+        )
+    if implementation not in (None, "hip"):
+        raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
+    if sm_scale is None:
+        sm_scale = 1.0 / math.sqrt(query.shape[-1])
+    squeeze = query.ndim == 3
+    if squeeze:
+        query, key, value = query[None], key[None], value[None]
+    active_dropout = dropout_rate if not deterministic and dropout_rate > 0 else 0.0
+    out = None
+    e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=active_dropout)
+    if e is not None and (implementation == "hip" or device_table_enabled()):
+        out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv)
+    if out is None:
+        raise ValueError(
+            f"implementation={implementation!r}: "
+            + _unsupported_message(query, key, mask, bias, active_dropout)
+            + ("" if implementation == "hip" or device_table_enabled()
+               else " (the HIP route is switched off by PROBJAX_ATTENTION_HIP=0)")
+        )
+    return out[0] if squeeze else out
+
+
+def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
+                          dropout_rate: float = 0.0, broadcast_dropout: bool = False,
+                          deterministic=True, dtype=None, precision=None, module=None,
+                          sm_scale: float | None = None, enable_gqa: bool = False,
+                          implementation: str | None = None):
+    """Softmax attention with Flax ``dot_product_attention`` semantics (probjax
+    layers/attention.py:1205-1319) on the HIP kernels: leading batch dims are
+    flattened, K/V may have fewer heads (GQA), ``sm_scale`` defaults to
+    ``1/sqrt(D)``.  ``implementation`` in ``(None, "hip")``.
+    """
+    if implementation not in (None, "hip"):
+        raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
+    if isinstance(mask, torch.Tensor) or isinstance(bias, torch.Tensor):
+        raise ValueError(
+            "array masks/biases are not taken by the HIP kernels; pass mask/bias objects "
+            "(CausalMask, KVLenMask, QKVLengthMask, DenseBias)"
+        )
+    batch_shape = query.shape[:-3]
+    flat = [x.reshape((-1,) + tuple(x.shape[-3:])) for x in (query, key, value)]
+    out = flex_attention(*flat, mask=mask, bias=bias, dropout_rng=dropout_rng,
+                         dropout_rate=dropout_rate, deterministic=deterministic, dtype=dtype,
+                         sm_scale=sm_scale, enable_gqa=enable_gqa or query.shape[-2] != key.shape[-2],
+                         implementation=implementation)
+    return out.reshape(tuple(batch_shape) + tuple(out.shape[-3:]))

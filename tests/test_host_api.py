@@ -1,0 +1,176 @@
+"""Host-side logic of the probjax-API mirror (no GPU needed).
+
+Restates the reference's dispatch tests where they apply to this path:
+``use_splitkv`` only for exact cases (probjax tests/test_attention_gqa_splitkv.py:
+224-232), route functions returning None to fall through and forced backends
+raising ValueError (tests/test_attention_device_defaults.py:25-59), the
+argument checks of ``flex_attention`` / ``mla``.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from probjax_amd import attention as A
+from probjax_amd import masks as M
+
+
+def _qkv(b=1, lq=1, lk=2048, hq=4, hkv=2, d=128, dtype=torch.bfloat16):
+    return (torch.zeros(b, lq, hq, d, dtype=dtype), torch.zeros(b, lk, hkv, d, dtype=dtype),
+            torch.zeros(b, lk, hkv, d, dtype=dtype))
+
+
+def test_lower_mask_table():
+    assert M.lower_mask(None) == M.LoweredMask()
+    assert M.lower_mask(M.NoMask()) == M.LoweredMask()
+    assert M.lower_mask(M.CausalMask()).causal
+    lm = M.lower_mask(M.CausalMask() & M.KVLenMask([3, 4]))
+    assert lm.causal and list(lm.kv_lengths) == [3, 4]
+    lm = M.lower_mask(M.QKVLengthMask(5, 7) & M.QKVLengthMask(6, 3))
+    assert (lm.q_valid, lm.kv_valid) == (5, 3)
+    assert M.lower_mask(M.CausalMask() | M.KVLenMask([1])) is None  # OR is not an AND of kernel masks
+
+
+def test_lower_mask_accepts_foreign_objects_by_name():
+    class CausalMask:  # noqa: D401 - stands for probjax's own class
+        pass
+
+    class KVLenMask:
+        def __init__(self, L):
+            self.kv_lengths = L
+
+    assert M.lower_mask(CausalMask()).causal
+    assert M.lower_mask(KVLenMask([2])).kv_lengths == [2]
+
+    class LocalWindowMask:
+        pass
+
+    assert M.lower_mask(LocalWindowMask()) is None
+
+
+def test_lower_bias():
+    b = torch.zeros(1, 2, 3, 4)
+    assert M.lower_bias(None) is None
+    assert M.lower_bias(M.DenseBias(b)) is b
+    assert M.lower_bias(object()) is False
+    with pytest.raises(ValueError):
+        M.DenseBias(torch.zeros(3, 4))
+
+
+def test_compose_two_stateful_raises():
+    with pytest.raises(ValueError, match="Cannot compose two stateful masks"):
+        M.ComposeMask("and", M.KVLenMask([1]), M.KVLenMask([2]))
+
+
+def test_use_splitkv_only_for_exact_cases():
+    q, k, _ = _qkv()
+    assert not A.use_splitkv(q, k, split_kv=False)
+    assert not A.use_splitkv(q, k, mask=M.CausalMask(), split_kv=True)
+    assert not A.use_splitkv(q, k, dropout_rate=0.1, split_kv=True)
+    assert not A.use_splitkv(q, k, bias=M.DenseBias(torch.zeros(1, 1, 1, 2048)), split_kv=True)
+    assert A.use_splitkv(q, k)                                  # Lq <= 64, Lkv >= 1024
+    assert A.use_splitkv(q, k, mask=M.KVLenMask([5]))           # exact with lengths too
+    q2, k2, _ = _qkv(lk=512)
+    assert not A.use_splitkv(q2, k2) and A.use_splitkv(q2, k2, split_kv=True)
+    q3, k3, _ = _qkv(lq=100)
+    assert not A.use_splitkv(q3, k3)
+    q4, k4, _ = _qkv(hq=64, hkv=2)                              # 32 rows per KV head
+    assert not A.use_splitkv(q4, k4, split_kv=True)
+    q5, k5, _ = _qkv(dtype=torch.float32)
+    assert not A.use_splitkv(q5, k5)
+
+
+def test_route_falls_through_off_device():
+    q, k, v = _qkv()
+    assert A.hip_attention_or_none(q, k, v, mask=None, bias=None, dropout_rate=0.0, sm_scale=0.1) is None
+    assert A.hip_attention_or_none(q, k, v, mask=None, bias=None, dropout_rate=0.0, sm_scale=0.1,
+                                   force=True) is None
+
+
+def test_route_respects_env_switch(monkeypatch):
+    q, k, v = _qkv()
+    monkeypatch.setenv("PROBJAX_ATTENTION_HIP", "0")
+    assert not A.device_table_enabled()
+    assert A.hip_attention_or_none(q, k, v, mask=None, bias=None, dropout_rate=0.0, sm_scale=0.1) is None
+    monkeypatch.setenv("PROBJAX_ATTENTION_HIP", "1")
+    assert A.device_table_enabled()
+
+
+def test_eligibility_rejects_without_touching_a_device(monkeypatch):
+    """Shapes/dtypes/masks the kernels do not take make the route fall through."""
+    monkeypatch.setattr(A, "hip_device", lambda t: True)
+    q, k, v = _qkv()
+    assert A._eligible(q, k, v, mask=None, bias=None, dropout_rate=0.1) is None
+    assert A._eligible(q, k, v, mask=M.CausalMask() | M.NoMask(), bias=None, dropout_rate=0.0) is None
+    assert A._eligible(q, k, v, mask=None, bias=object(), dropout_rate=0.0) is None
+    assert A._eligible(q, k, v[:, :5], mask=None, bias=None, dropout_rate=0.0) is None
+    assert A._eligible(q, k, v, mask=M.KVLenMask([1, 2]), bias=None, dropout_rate=0.0) is None  # B = 1
+    lm, b = A._eligible(q, k, v, mask=M.KVLenMask([7]), bias=None, dropout_rate=0.0)
+    assert lm.kv_lengths.dtype == torch.int32 and b is None
+    q16 = q.to(torch.float16)
+    assert A._flash_plan(q16, k, v, M.LoweredMask(), None) is None
+    q96 = torch.zeros(1, 4, 4, 96, dtype=torch.bfloat16)
+    assert A._flash_plan(q96, q96, q96, M.LoweredMask(), None) is None
+
+
+def test_flex_attention_argument_checks():
+    q, k, v = _qkv(hq=4, hkv=2)
+    with pytest.raises(ValueError, match="same dtype"):
+        A.flex_attention(q, k.float(), v)
+    with pytest.raises(ValueError, match="at least 3 dimensional"):
+        A.flex_attention(q[0, 0], k, v)
+    with pytest.raises(ValueError, match="enable_gqa=True"):
+        A.flex_attention(q, k, v)
+    q3, k3, v3 = _qkv(hq=3, hkv=2)
+    with pytest.raises(ValueError, match="multiple of kv heads"):
+        A.flex_attention(q3, k3, v3, enable_gqa=True)
+    with pytest.raises(ValueError, match="implementation must be"):
+        A.flex_attention(q, k, v, enable_gqa=True, implementation="triton")
+    # off a gfx950 device the forced route refuses (no CPU fallback)
+    with pytest.raises(ValueError, match="cannot compute this call exactly"):
+        A.flex_attention(q, k, v, enable_gqa=True, implementation="hip")
+
+
+def test_mha_and_mla_refuse_off_device():
+    q, k, v = _qkv()
+    with pytest.raises(ValueError, match="ROCm device"):
+        A.mha(q, k, v)
+    _, k3, v3 = _qkv(hkv=3)
+    with pytest.raises(ValueError, match="multiple of KV heads"):
+        A.mha(q, k3, v3)
+    qm = torch.zeros(2, 1, 16, 576, dtype=torch.bfloat16)
+    c = torch.zeros(2, 64, 576, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        A.mla(qm, c)
+    with pytest.raises(ValueError, match="rank 4"):
+        A.mla(qm[0], c)
+    with pytest.raises(ValueError, match="batch mismatch"):
+        A.mla(qm, c[:1])
+    with pytest.raises(ValueError, match="both wk and wv"):
+        A.mla(qm, c, wk=torch.zeros(16, 576, 576))
+    with pytest.raises(ValueError, match="qk_head_dim == kv_lora_rank"):
+        A.mla(qm[..., :512], c)
+
+
+def test_dot_product_attention_refuses_array_masks():
+    q, k, v = _qkv()
+    with pytest.raises(ValueError, match="array masks"):
+        A.dot_product_attention(q, k, v, mask=torch.ones(1, 1, 1, 2048, dtype=torch.bool))
+
+
+def test_splitkv_forward_num_splits_to_chunk(monkeypatch):
+    seen = {}
+
+    def fake(q, k, v, *, sm_scale, kv_lengths, chunk, return_lse):
+        seen["chunk"] = chunk
+        return q
+
+    monkeypatch.setattr(A.hip, "splitkv_decode", fake)
+    q, k, v = _qkv(lk=1000)
+    A.splitkv_forward(q, k, v, sm_scale=0.1, num_splits=3)
+    assert seen["chunk"] == 384  # ceil(1000/3) = 334 -> 3 x 128
+    A.splitkv_forward(q, k, v, sm_scale=0.1)
+    assert seen["chunk"] == 0
+    with pytest.raises(ValueError):
+        A.splitkv_forward(q, k, v, sm_scale=0.1, num_splits=0)
+    assert np.isclose(A._SPLITKV_MIN_KV_LEN, 1024)
