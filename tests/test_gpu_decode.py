@@ -23,6 +23,9 @@ BF16_TOL = 2e-2
         (4, 1, 1500, 16, 1, 128, [0, 1, 129, 1500], 256),  # empty / single-key rows, 16 rows
         (1, 3, 2000, 20, 4, 64, [1999], 512),     # 15 rows, ragged tail per wave
         (3, 1, 8192, 32, 8, 128, [8192, 512, 7777], 0),
+        (4, 1, 8192, 8, 2, 128, [1, 2, 3, 0], 128),      # chunks past every length: empty partials
+        (16, 1, 300, 8, 2, 64, [7, 300, 1, 150, 299, 2, 64, 65, 0, 33, 120, 17, 280, 5, 9, 211], 128),
+        (2, 1, 5000, 16, 4, 128, [5000, 4999], 0),
     ],
 )
 def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, chunk):
