@@ -27,9 +27,8 @@
 namespace pjx {
 
 constexpr int kDecThreads = 256;
-constexpr int kTile = 64;       // keys per tile (16 per wave)
+constexpr int kTile = 64;       // keys per latent tile (16 per wave)
 constexpr int kRows = 16;       // query rows per MFMA column block
-constexpr int kSStride = kTile + 4;  // score tile row stride (floats)
 
 struct DecodeArgs {
   const uint16_t* q;
@@ -96,6 +95,27 @@ __device__ __forceinline__ void emit_row_elem(const DecodeArgs& a, int b, int g,
       a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : INFINITY;
   } else {
     a.ws_o[(part * a.rows + r) * a.dv + d] = O;
+    if (d == 0) {
+      a.ws_ml[(part * a.rows + r) * 2] = M;
+      a.ws_ml[(part * a.rows + r) * 2 + 1] = Ls;
+    }
+  }
+}
+
+// emit_row_elem for 4 consecutive dims d..d+3 (d a multiple of 4).
+__device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g, int r, int d,
+                                              size_t part, bool final_out, float M, float Ls,
+                                              f32x4 O) {
+  if (final_out) {
+    int t, h;
+    row_to_head(a, g, r, t, h);
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    const u32x2 pk = {pack_bf16x2(O[0] * inv, O[1] * inv), pack_bf16x2(O[2] * inv, O[3] * inv)};
+    *(u32x2*)(a.o + ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + d) = pk;
+    if (a.lse && d == 0)
+      a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : INFINITY;
+  } else {
+    *(f32x4*)(a.ws_o + (part * a.rows + r) * a.dv + d) = O;
     if (d == 0) {
       a.ws_ml[(part * a.rows + r) * 2] = M;
       a.ws_ml[(part * a.rows + r) * 2 + 1] = Ls;
@@ -310,35 +330,98 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
   }
 }
 
-// D: q.k dims; NDT: 16-wide output-dim tiles per wave (DV = 64*NDT);
-// SHARED: V is the first DV dims of K (absorbed MLA).
-template <int D, int NDT, bool SHARED>
-__global__ __launch_bounds__(kDecThreads) void decode_chunk_kernel(DecodeArgs a) {
-  constexpr int DV = 64 * NDT;
-  constexpr int KSTEPS = D / 32;
-  constexpr int VT = kTile + 8;  // V^T row stride (bf16): 144 B rows keep b128 reads aligned
-  static_assert(DV <= D || !SHARED, "shared V must be a prefix of K");
-  static_assert(D % 32 == 0, "head dim");
+// ---------------------------------------------------------------------------
+// Latent (MLA) decode: K = V = one shared latent cache row of D dims per key,
+// the first DV dims acting as values.  One workgroup = one (chunk, batch)
+// item; the two LDS stages (2 x 64 keys x 2D bytes) leave room for one
+// workgroup per CU.
+//   * Each 64-key tile is contiguous in HBM (64 rows x 2D bytes) and is copied
+//     HBM -> LDS with buffer->LDS loads, 1 KiB per wave instruction; the next
+//     tile is in flight while the current one is computed.
+//   * Wave w owns keys [16w, 16w+16) of every tile and keeps its own online
+//     softmax: S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (K rows from LDS,
+//     Q^T in registers), then O^T += V^T P^T with v_mfma_f32_16x16x16_bf16,
+//     whose B operand is the score accumulator as it stands and whose A
+//     operand (V^T) comes from the same LDS tile through ds_read_b64_tr_b16.
+//     The latent row is read from HBM once and from LDS twice.
+//   * The four waves' (max, sum, O) are combined in LDS at the end.
+// LDS rows keep their 16-byte columns XOR-swizzled per row (within aligned
+// groups of 8 or 16 columns), so that 16 lanes reading one column of 16 rows
+// (K fragments) and 32 lanes reading two columns of 8 rows (transposing V
+// reads) touch distinct banks.
+// ---------------------------------------------------------------------------
+template <int D>
+struct LatentTile {
+  static constexpr int BK = 64;                    // keys per tile
+  static constexpr int ROWB = 2 * D;               // bytes per latent row
+  static constexpr int NC = D / 8;                 // 16-byte columns per row
+  static constexpr int STAGE_B = BK * ROWB;        // bytes per stage
+  static constexpr int NLD = STAGE_B / (4 * 1024);  // 1 KiB loads per wave per tile
+  static constexpr int GRP = (NC % 16 == 0) ? 16 : 8;  // swizzle group (columns)
+  static_assert(NC % 8 == 0 && STAGE_B % 4096 == 0, "latent tile shape");
+  // Row r's column XOR.  Row r starts at 16-byte bank unit (r*NC) % 16, which
+  // is 0 when NC % 16 == 0 and 8*(r&1) when NC % 16 == 8; the XOR below makes
+  // (start unit) ^ (column ^ swz(r)) distinct over any 16 consecutive rows, and
+  // over any 8 rows for an aligned column pair.
+  __device__ static int swz(int r) {
+    return GRP == 16 ? (((r & 7) << 1) | ((r >> 3) & 1)) : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
+  }
+};
 
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[DV * VT];
-  __shared__ __attribute__((aligned(16))) float s_lds[kRows * kSStride];
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
 
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+// Workgroup barrier for the buffer->LDS ring.  __syncthreads() carries a
+// workgroup release fence, which waits for every outstanding vector memory
+// operation of the wave -- including the next tile's loads, still in flight by
+// design.  Here the waits are explicit instead: this wave's LDS reads are
+// complete (lgkmcnt(0)) and the caller has waited for the loads whose data
+// the other waves will read (vmcnt); the wavefront-scope fences only keep the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+template <int D, int DV>
+__global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a) {
+  using T = LatentTile<D>;
+  constexpr int BK = T::BK, ROWB = T::ROWB, NLD = T::NLD, GRP = T::GRP;
+  constexpr int KSTEPS = D / 32;  // 32-dim k-steps of Q.K
+  constexpr int SPG = GRP / 4;    // k-steps per swizzle group
+  constexpr int NDT = DV / 16;    // 16-dim output tiles, all held by every wave
+  constexpr int DPG = GRP / 2;    // output tiles per swizzle group
+  static_assert(DV % 64 == 0 && DV <= D, "value dims are a prefix of the latent row");
+  static_assert(KSTEPS % SPG == 0 && NDT % DPG == 0, "swizzle groups");
+  // The combine at the end puts 2 waves' O (16 rows x DV floats each) in each stage.
+  static_assert(2 * kRows * DV * 4 <= T::STAGE_B, "combine scratch fits");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[T::STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[T::STAGE_B];
+  __shared__ float red_ml[4 * kRows * 2];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int chunk_id = blockIdx.x % a.nch;
-  const int bg = blockIdx.x / a.nch;
-  const int b = bg / a.G, g = bg % a.G;
+  const int chunk_id = blockIdx.x / a.B;
+  const int b = blockIdx.x % a.B;
   const int L = seq_len(a, b);
   const int c0 = chunk_id * a.chunk;
-  if (c0 >= L) return;  // whole workgroup exits: nothing past the length is read
+  if (c0 >= L) return;  // the whole workgroup: nothing past the length is read
   const int c1 = min(c0 + a.chunk, L);
+  const int n_tiles = (c1 - c0 + BK - 1) / BK;
 
-  // Q as the B operand: lane holds row c16, dims 32*s + 8*q4 + [0,8).
+  // Q^T as the B operand: lane holds query row c16, dims 32*s + 8*q4 + [0,8).
   bf16x8 qf[KSTEPS];
   {
     const bool rv = c16 < a.rows;
     int t = 0, h = 0;
-    if (rv) row_to_head(a, g, c16, t, h);
+    if (rv) row_to_head(a, 0, c16, t, h);
     const uint16_t* qrow = a.q + ((size_t)(b * a.Lq + t) * a.Hq + h) * D;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
@@ -347,205 +430,243 @@ __global__ __launch_bounds__(kDecThreads) void decode_chunk_kernel(DecodeArgs a)
       qf[s] = as_bf16x8(r);
     }
   }
-  const size_t kv_tok = (size_t)a.G * D;
-  const uint16_t* Kb = a.k + ((size_t)b * a.Lk * a.G + g) * D;
-  const uint16_t* Vb = SHARED ? Kb : a.v + ((size_t)b * a.Lk * a.G + g) * D;
+  const unsigned char* Kb = (const unsigned char*)a.k + (size_t)b * a.Lk * ROWB;
+
+  // Buffer->LDS sources: load j of wave w fills 16-byte LDS unit
+  // p = (NLD*w + j)*64 + lane = row*NC + slot with global column slot ^ swz(row).
+  uint32_t voff[NLD];
+#pragma unroll
+  for (int j = 0; j < NLD; ++j) {
+    const int p = (NLD * w + j) * 64 + lane, r = p / T::NC, slot = p % T::NC;
+    voff[j] = r * ROWB + 16 * (slot ^ T::swz(r));
+  }
+  // K fragment of k-step s: row 16w + c16, column 4s + q4, i.e. group s / SPG,
+  // column 4*(s % SPG) + q4 within it.
+  uint32_t offK[SPG];
+  {
+    const int r = 16 * w + c16;
+#pragma unroll
+    for (int e = 0; e < SPG; ++e) offK[e] = r * ROWB + 16 * ((4 * e + q4) ^ T::swz(r));
+  }
+  // Transposing V^T read for output tile dt (dims 16*dt + [0,16), keys
+  // 16w + 4*q4 + [0,4)): lane s of each 16-lane group points at row
+  // 16w + 4*q4 + s/4, dims 16*dt + 4*(s%4) + [0,4).
+  uint32_t offV[DPG];
+  {
+    const int r = 16 * w + 4 * q4 + (c16 >> 2);
+#pragma unroll
+    for (int e = 0; e < DPG; ++e)
+      offV[e] = r * ROWB + 16 * ((2 * e + ((c16 & 3) >> 1)) ^ T::swz(r)) + 8 * (c16 & 1);
+  }
 
   f32x4 acc[NDT];
 #pragma unroll
   for (int i = 0; i < NDT; ++i) acc[i] = f32x4{};
   float m_run = kMaxInit, l_run = 0.f;
 
-  for (int k0 = c0; k0 < c1; k0 += kTile) {
-    // ---- phase 1: S^T for keys [k0 + 16w, +16), V^T into LDS ----
-    const int key = k0 + 16 * w + c16;
-    const bool kin = key < c1;
-    const uint16_t* krow = Kb + (size_t)(kin ? key : 0) * kv_tok;
-    u32x4 kf[KSTEPS];
+  auto issue = [&](int t, unsigned char* ks) {
+    const int k0 = c0 + t * BK;
+    // Rows at or past c1 read as 0; a tile past the chunk reads nothing.
+    // (readfirstlane: the clamp is computed on the vector unit, and a vector
+    // operand of the buffer descriptor would need a waterfall loop.)
+    const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(BK, c1 - k0)) * ROWB);
+    const rsrc_t rs = make_rsrc(Kb + (size_t)k0 * ROWB, bytes);
 #pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) {
-      u32x4 r = {0u, 0u, 0u, 0u};
-      if (kin) r = *(const u32x4*)(krow + 32 * s + 8 * q4);
-      kf[s] = r;
-    }
-    u32x4 vf[SHARED ? 1 : DV / 32];
-    if constexpr (!SHARED) {
-      const uint16_t* vrow = Vb + (size_t)(kin ? key : 0) * kv_tok;
-#pragma unroll
-      for (int s = 0; s < DV / 32; ++s) {
-        u32x4 r = {0u, 0u, 0u, 0u};
-        if (kin) r = *(const u32x4*)(vrow + 32 * s + 8 * q4);
-        vf[s] = r;
-      }
-    }
-    f32x4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < KSTEPS; ++s) sacc = mfma16x16x32(as_bf16x8(kf[s]), qf[s], sacc);
-    // C layout: lane holds row c16, keys 16w + 4*q4 + r.
-    *(f32x4*)(&s_lds[c16 * kSStride + 16 * w + 4 * q4]) = sacc;
-    // V^T[d][key - k0]
-    {
-      const int kc = 16 * w + c16;
-#pragma unroll
-      for (int s = 0; s < DV / 32; ++s) {
-        const u32x4 src = SHARED ? kf[s] : vf[SHARED ? 0 : s];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const int d = 32 * s + 8 * q4 + 2 * j;
-          vt_lds[d * VT + kc] = (uint16_t)(src[j] & 0xffffu);
-          vt_lds[(d + 1) * VT + kc] = (uint16_t)(src[j] >> 16);
-        }
-      }
-    }
-    __syncthreads();
+    for (int j = 0; j < NLD; ++j) buffer_load_lds16(rs, ks + (NLD * w + j) * 1024, voff[j]);
+  };
 
-    // ---- phase 2: softmax over the 64-key tile, then O^T += V^T P^T ----
-    float p[2][8];
+  auto compute = [&](int t, const unsigned char* ks) {
+    const int k0 = c0 + t * BK;
+    // s[r] = S^T[key k0 + 16w + 4*q4 + r][row c16]
+    f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const f32x4 lo = *(const f32x4*)(&s_lds[c16 * kSStride + 32 * c + 8 * q4]);
-      const f32x4 hi = *(const f32x4*)(&s_lds[c16 * kSStride + 32 * c + 8 * q4 + 4]);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        p[c][j] = lo[j];
-        p[c][4 + j] = hi[j];
-      }
+    for (int st = 0; st < KSTEPS; ++st) {
+      const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + offK[st % SPG] + 16 * GRP * (st / SPG)));
+      s = mfma16x16x32(kf, qf[st], s);
     }
-    if (k0 + kTile > c1) {
+    if (k0 + BK > c1) {
+      const int lim = c1 - (k0 + 16 * w + 4 * q4);
 #pragma unroll
-      for (int c = 0; c < 2; ++c)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          if (k0 + 32 * c + 8 * q4 + j >= c1) p[c][j] = -INFINITY;
+      for (int r = 0; r < 4; ++r)
+        if (r >= lim) s[r] = -INFINITY;
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int j = 0; j < 8; ++j) mx = fmaxf(mx, p[c][j]);
+    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
     mx = xor16_max(mx);
-    mx = xor32_max(mx);
-    const float m_new = fmaxf(m_run, mx * a.cx);
-    const float corr = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float rs = 0.f;
-    bf16x8 pf[2];
+    const float mc = xor32_max(mx) * a.cx;
+    if (wave_any(mc > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mc);
+      const float corr = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= corr;
 #pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      u32x4 pk;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const float e0 = fast_exp2(fmaf(p[c][2 * j], a.cx, -m_new));
-        const float e1 = fast_exp2(fmaf(p[c][2 * j + 1], a.cx, -m_new));
-        rs += e0 + e1;
-        pk[j] = pack_bf16x2(e0, e1);
-      }
-      pf[c] = as_bf16x8(pk);
+      for (int i = 0; i < NDT; ++i) acc[i] *= corr;
     }
-    l_run = fmaf(l_run, corr, rs);
+    float p[4];
 #pragma unroll
-    for (int i = 0; i < NDT; ++i) {
-      acc[i] *= corr;
-      const int dt = w * NDT + i;
+    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(fmaf(s[r], a.cx, -m_run));
+    l_run += (p[0] + p[1]) + (p[2] + p[3]);
+    const u32x2 pk = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    const s16x4 pb = __builtin_bit_cast(s16x4, pk);
 #pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const u32x4 av = *(const u32x4*)(&vt_lds[(dt * 16 + c16) * VT + 32 * c + 8 * q4]);
-        acc[i] = mfma16x16x32(as_bf16x8(av), pf[c], acc[i]);
-      }
+    for (int dt = 0; dt < NDT; ++dt) {
+      const u32x2 av = lds_read_tr16(ks + offV[dt % DPG] + 16 * GRP * (dt / DPG));
+      acc[dt] = mfma16x16x16(__builtin_bit_cast(s16x4, av), pb, acc[dt]);
     }
-    __syncthreads();
+  };
+
+  // Tile t lives in stage t % 2.  Before computing tile t: this wave's loads
+  // of it have landed (vmcnt counts loads in issue order and only tile t+1's
+  // may still be pending), then the barrier makes every wave's loads visible.
+  // After computing it, a barrier lets tile t+2 be loaded into the same stage.
+  // Every path issues the same sequence of loads (tiles past the chunk are
+  // empty) and the loop has no early exit, so the compiler can tell that at
+  // each read of a stage the NLD most recent loads target the other stage,
+  // and adds no wait of its own.
+  // Prologue: Q's loads are waited for while tile 0 is in flight, so that no
+  // load into registers is pending at the loop (the compiler would otherwise
+  // wait for every outstanding load, tile 1's included, before entering it).
+  __builtin_amdgcn_sched_barrier(0);
+  issue(0, smem0);
+  wait_vmcnt<NLD>();
+  issue(1, smem1);
+  for (int t = 0; t < n_tiles; t += 2) {
+    wait_vmcnt<NLD>();
+    stage_barrier();
+    compute(t, smem0);
+    stage_barrier();
+    issue(t + 2, smem0);
+    wait_vmcnt<NLD>();
+    stage_barrier();
+    if (t + 1 < n_tiles) compute(t + 1, smem1);
+    stage_barrier();
+    issue(t + 3, smem1);
   }
 
-  // ---- this chunk's result: final output if it covers the sequence ----
+  // ---- combine the four waves: O^T in LDS, float4 columns XOR-swizzled by row ----
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
-  const size_t part = (size_t)bg * a.nch + chunk_id;
-  const bool final_out = c0 == 0 && L <= a.chunk;
-  if (c16 < a.rows) {
+  wait_vmcnt<0>();  // the trailing (empty) tile loads still write LDS
+  __syncthreads();  // every wave is done with both stages
+  {
+    // Waves 0, 1 write stage 0, waves 2, 3 stage 1 (a branch, not a pointer
+    // select, keeps every LDS access tied to one array for the compiler).
+    auto put = [&](unsigned char* st) {
+      float* ro = (float*)st + (w & 1) * kRows * DV;
 #pragma unroll
-    for (int i = 0; i < NDT; ++i) {
-      const int d0 = (w * NDT + i) * 16 + 4 * q4;
-      if (d0 < a.dv) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) emit_row_elem(a, b, g, c16, d0 + j, part, final_out, m_run, l_run, acc[i][j]);
-      }
+      for (int dt = 0; dt < NDT; ++dt)
+        *(f32x4*)(ro + c16 * DV + 4 * ((4 * dt + q4) ^ c16)) = acc[dt];  // O[row c16][16dt + 4q4 + r]
+    };
+    if (w < 2) put(smem0); else put(smem1);
+    if (q4 == 0) {
+      red_ml[(w * kRows + c16) * 2] = m_run;
+      red_ml[(w * kRows + c16) * 2 + 1] = l_run;
     }
+  }
+  __syncthreads();
+  const size_t part = (size_t)b * a.nch + chunk_id;
+  const bool final_out = c0 == 0 && L <= a.chunk;
+  constexpr int NQ = DV / 4;  // float4 columns per row
+  for (int idx = tid; idx < kRows * NQ; idx += kDecThreads) {
+    const int r = idx / NQ, u = idx % NQ;
+    if (r >= a.rows) break;
+    float mw[4], M = kMaxInit;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      mw[ww] = red_ml[(ww * kRows + r) * 2];
+      M = fmaxf(M, mw[ww]);
+    }
+    float Ls = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = fast_exp2(mw[ww] - M);
+      Ls = fmaf(wt, red_ml[(ww * kRows + r) * 2 + 1], Ls);
+      const float* ro = (const float*)(ww < 2 ? smem0 : smem1) + (ww & 1) * kRows * DV;
+      O += wt * *(const f32x4*)(ro + r * DV + 4 * (u ^ (r & 15)));
+    }
+    emit_row_quad(a, b, 0, r, 4 * u, part, final_out, M, Ls, O);
   }
 }
 
 // Exact merge of the chunk partials of one (batch, group, query row):
 // M = max_c m_c, O = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c
-// (attention_splitkv.py:236-245, with unnormalised partials).  Sequences that
-// fit one chunk were finished by the chunk kernel; empty sequences (length 0,
-// no chunk ran) get a zero output and LSE = +inf (attention_xla.py:417-420).
-__global__ __launch_bounds__(128) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int kMaxBatch = 512;  // chunk weights staged in LDS per pass
-  __shared__ float wts[kMaxBatch];
-  __shared__ float red[2][4];
-  const int bg = blockIdx.x / a.rows;
-  const int r = blockIdx.x % a.rows;
+// (attention_splitkv.py:236-245, with unnormalised partials).  One thread per
+// 4 output dims.  The partials are taken in batches of kMergeBatch chunks whose
+// loads (m, l and 4 dims of O per chunk) are all issued before any is used, so
+// a batch costs one memory round trip (the first one overlapping the length
+// load); batches are combined online (running max, rescaled sums).  Sequences that fit one chunk were finished by the
+// chunk kernel; empty sequences (length 0, no chunk ran) get a zero output and
+// LSE = +inf (attention_xla.py:417-420).
+constexpr int kMergeThreads = 128;
+constexpr int kMergeBatch = 16;
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs a) {
+  const int nq = a.dv / 4;
+  const long gid = (long)blockIdx.x * kMergeThreads + threadIdx.x;
+  const long item = gid / nq;
+  const int u = (int)(gid % nq);
+  if (item >= (long)a.B * a.G * a.rows) return;
+  const int bg = (int)(item / a.rows), r = (int)(item % a.rows);
   const int b = bg / a.G, g = bg % a.G;
-  const int L = seq_len(a, b);
-  const int n = (L + a.chunk - 1) / a.chunk;
-  if (n == 1) return;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const size_t base = (size_t)bg * a.nch;
-  const float* ml = a.ws_ml + (base * a.rows + r) * 2;  // chunk c at ml[c * rows * 2]
+  const float* ml = a.ws_ml + (base * a.rows + r) * 2;  // chunk c at ml[c * ml_stride]
   const size_t ml_stride = (size_t)a.rows * 2;
-  // Global max of the chunk maxima.
-  float M = kMaxInit;
-  for (int c = tid; c < n; c += 128) M = fmaxf(M, ml[c * ml_stride]);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) M = fmaxf(M, __shfl_xor(M, o));
-  if (lane == 0) red[0][w] = M;
-  __syncthreads();
-  M = fmaxf(red[0][0], red[0][1]);
-  int t, h;
-  row_to_head(a, g, r, t, h);
-  uint16_t* orow = a.o + ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv;
-  const float* po = a.ws_o + (base * a.rows + r) * a.dv;  // chunk c at po[c * rows * dv]
+  const float* po = a.ws_o + (base * a.rows + r) * a.dv + 4 * u;  // chunk c at po[c * o_stride]
   const size_t o_stride = (size_t)a.rows * a.dv;
-  float num[5] = {0.f, 0.f, 0.f, 0.f, 0.f};  // dv <= 640 over 128 threads
-  float den = 0.f;
-  for (int cb = 0; cb < n; cb += kMaxBatch) {
-    const int cn = min(kMaxBatch, n - cb);
-    __syncthreads();
-    for (int c = tid; c < cn; c += 128) {
-      const float wt = fast_exp2(ml[(size_t)(cb + c) * ml_stride] - M);
-      wts[c] = wt;
-      den = fmaf(wt, ml[(size_t)(cb + c) * ml_stride + 1], den);
-    }
-    __syncthreads();
+  // The sequence length is needed only after the first batch's loads are
+  // issued: partial addresses are clamped to the workspace's a.nch chunks,
+  // and slots at or past this sequence's chunk count n (never written by this
+  // call) are dropped by selects, so whatever they hold cannot leak in.
+  // (A buffer load of the length: unconditional, so nothing waits for it
+  // before the partial loads; without lengths the buffer is empty.)
+  const int len_raw = (int)__builtin_amdgcn_raw_buffer_load_b32(
+      make_rsrc(a.lengths, a.lengths ? (uint32_t)a.B * 4u : 0u), b * 4, 0, 0);
+  float M = kMaxInit, den = 0.f;
+  f32x4 num = {0.f, 0.f, 0.f, 0.f};
+  float mv[kMergeBatch], lv[kMergeBatch];
+  f32x4 ov[kMergeBatch];
+  auto load_batch = [&](int c0) {
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-      const int d = tid + 128 * i;
-      if (d < a.dv) {
-        const float* p = po + (size_t)cb * o_stride + d;
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, acc3 = 0.f;
-        int c = 0;
-        for (; c + 4 <= cn; c += 4) {
-          acc0 = fmaf(wts[c], p[(size_t)c * o_stride], acc0);
-          acc1 = fmaf(wts[c + 1], p[(size_t)(c + 1) * o_stride], acc1);
-          acc2 = fmaf(wts[c + 2], p[(size_t)(c + 2) * o_stride], acc2);
-          acc3 = fmaf(wts[c + 3], p[(size_t)(c + 3) * o_stride], acc3);
-        }
-        for (; c < cn; ++c) acc0 = fmaf(wts[c], p[(size_t)c * o_stride], acc0);
-        num[i] += (acc0 + acc1) + (acc2 + acc3);
+    for (int i = 0; i < kMergeBatch; ++i) {
+      const size_t c = (size_t)min(c0 + i, a.nch - 1);
+      mv[i] = ml[c * ml_stride];
+      lv[i] = ml[c * ml_stride + 1];
+      ov[i] = *(const f32x4*)(po + c * o_stride);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the batch ahead of the arithmetic
+  };
+  auto add_batch = [&](int c0, int n) {
+    float bm = M;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i)
+      if (c0 + i < n) bm = fmaxf(bm, mv[i]);
+    const float sc = fast_exp2(M - bm);
+    M = bm;
+    den *= sc;
+    num *= sc;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; ++i) {
+      if (c0 + i < n) {
+        const float wt = fast_exp2(mv[i] - M);
+        den = fmaf(wt, lv[i], den);
+        num += wt * ov[i];
       }
     }
+  };
+  load_batch(0);
+  const int L = a.lengths ? min(a.Lk, max(len_raw, 0)) : a.Lk;  // as seq_len
+  const int n = (L + a.chunk - 1) / a.chunk;
+  if (n == 1) return;  // the chunk kernel wrote this row's output
+  add_batch(0, n);
+  for (int c0 = kMergeBatch; c0 < n; c0 += kMergeBatch) {
+    load_batch(c0);
+    add_batch(c0, n);
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) den += __shfl_xor(den, o);
-  if (lane == 0) red[1][w] = den;
-  __syncthreads();
-  den = red[1][0] + red[1][1];
+  int t, h;
+  row_to_head(a, g, r, t, h);
   const float inv = den > 0.f ? 1.f / den : 0.f;
-#pragma unroll
-  for (int i = 0; i < 5; ++i) {
-    const int d = tid + 128 * i;
-    if (d < a.dv) orow[d] = __builtin_bit_cast(uint16_t, (__bf16)(num[i] * inv));
-  }
-  if (a.lse && tid == 0)
+  const u32x2 pk = {pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
+  *(u32x2*)(a.o + ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + 4 * u) = pk;
+  if (a.lse && u == 0)
     a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = den > 0.f ? (M + __log2f(den)) * kLn2 : INFINITY;
 }
 
@@ -591,7 +712,9 @@ static int run_decode(K kernel, DecodeArgs& a, void* workspace, size_t ws_bytes,
   hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kDecThreads), 0, stream, a);
   int rc = check_launch(name);
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)(a.B * a.G * a.rows)), dim3(128), 0, stream, a);
+  const long merge_threads = (long)a.B * a.G * a.rows * (a.dv / 4);
+  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((merge_threads + kMergeThreads - 1) / kMergeThreads)),
+                     dim3(kMergeThreads), 0, stream, a);
   return check_launch(name);
 }
 
@@ -660,9 +783,9 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   a.dv = (int)v_dim; a.cx = sm_scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (batch == 0) return PJX_OK;
-  if (rank == 576 && v_dim == 512) return run_decode(decode_chunk_kernel<576, 8, true>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 576 && v_dim == 576) return run_decode(decode_chunk_kernel<576, 9, true>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 512 && v_dim == 512) return run_decode(decode_chunk_kernel<512, 8, true>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 128 && v_dim == 128) return run_decode(decode_chunk_kernel<128, 2, true>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
+  if (rank == 576 && v_dim == 512) return run_decode(mla_decode_kernel<576, 512>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
+  if (rank == 576 && v_dim == 576) return run_decode(mla_decode_kernel<576, 576>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
+  if (rank == 512 && v_dim == 512) return run_decode(mla_decode_kernel<512, 512>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
+  if (rank == 128 && v_dim == 128) return run_decode(mla_decode_kernel<128, 128>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
   return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
 }

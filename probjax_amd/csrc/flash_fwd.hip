@@ -119,7 +119,6 @@ __device__ __forceinline__ f32x4 load_bias4(const float* row, int kk, int Lk) {
 // normalised output is the same softmax: O / l with l accumulated against the
 // same reference max.
 // ---------------------------------------------------------------------------
-constexpr float kRescaleLog2 = 8.0f;
 
 template <int D>
 struct Bf16Tile {

@@ -119,4 +119,15 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
 
 __device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
 
+// v_mfma_f32_16x16x16_bf16: A lane l holds A[l%16][4*(l/16)+j], j<4;
+// B lane l holds B[4*(l/16)+j][l%16]; C as for 16x16x32.
+__device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+// Lazy softmax rescale: the running max used for exponentiation is raised
+// only when a row's new max exceeds it by more than this (log2 units), so P
+// stays <= 2^kRescaleLog2 and the O rescale runs on few tiles.
+constexpr float kRescaleLog2 = 8.0f;
+
 }  // namespace pjx

@@ -48,16 +48,37 @@ def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, ch
     assert max_abs(lse[fin], want_lse[fin]) <= 1e-3
 
 
-@pytest.mark.parametrize("v_dim", [512, 576])
-def test_mla_decode_matches_oracle(device, v_dim):
+@pytest.mark.parametrize(
+    "b,lq,h,s,r,dv,lengths,chunk",
+    [
+        (2, 1, 16, 700, 576, 512, None, 0),
+        (2, 1, 16, 700, 576, 576, None, 0),
+        (3, 1, 16, 1000, 576, 512, [1, 63, 1000], 192),     # 3-tile chunks, partial last tiles
+        (4, 1, 8, 513, 576, 512, [0, 64, 65, 513], 64),      # empty sequence, one-tile chunks, 8 rows
+        (2, 2, 4, 300, 512, 512, [300, 129], 128),           # Lq = 2: rows fold as t*H + h
+        (2, 1, 16, 2000, 512, 512, None, 0),
+        (2, 1, 16, 777, 128, 128, [777, 5], 0),
+        (1, 1, 16, 4096, 576, 512, [4096], 8192),            # one chunk: the chunk kernel writes the output
+        (5, 1, 3, 257, 576, 576, [257, 256, 2, 128, 129], 128),  # 3 rows
+    ],
+)
+def test_mla_decode_matches_oracle(device, b, lq, h, s, r, dv, lengths, chunk):
     import torch
     from probjax_amd.hip_attention import mla_decode
 
-    b, h, s, r = 2, 16, 700, 576
-    q, cache = (oracle.round_bf16(x) for x in rng_normal(11, (b, 1, h, r), (b, s, r)))
+    q, cache = (oracle.round_bf16(x) for x in rng_normal(11, (b, lq, h, r), (b, s, r)))
     scale = 1.0 / math.sqrt(192)
-    want = oracle.xla_mla(q, cache, sm_scale=scale)[..., :v_dim]
-    got = mla_decode(to_dev(q, device, torch.bfloat16), to_dev(cache, device, torch.bfloat16),
-                     sm_scale=scale, v_dim=v_dim)
+    mask = None if lengths is None else oracle.KVLenMask(np.array(lengths, np.int32))
+    shared = cache[:, :, None, :]
+    want, want_lse = oracle.xla_attention(q, shared, shared, mask=mask, sm_scale=scale, strategy="tiled",
+                                          return_lse=True)
+    want = want[..., :dv]
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    got, lse = mla_decode(to_dev(q, device, torch.bfloat16), to_dev(cache, device, torch.bfloat16),
+                          sm_scale=scale, v_dim=dv, kv_lengths=L, chunk=chunk, return_lse=True)
     torch.cuda.synchronize()
     assert max_abs(to_np(got), want) <= BF16_TOL
+    lse = to_np(lse)
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
+    fin = np.isfinite(want_lse)
+    assert max_abs(lse[fin], want_lse[fin]) <= 1e-3
