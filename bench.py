@@ -8,6 +8,10 @@ forward at B=4, H=16, L=4096, D=128 (``configs[1]``).  One step = one
 TFLOP/s with the reference's FLOP convention ``4*B*H*Lq*Lk*D``, halved for
 causal (probjax docs/scripts/benchmark_gpu_attention.py:179-187).
 
+Each workload first runs untimed for ``--settle`` seconds (default 0.5) so that
+the GPU clocks reach their sustained level, then W warmup steps, then the K
+timed steps.
+
 The other configurations are measured the same way after the headline and
 reported under ``"configs"`` (decode and MLA as HBM GB/s of the bytes the
 algorithm must move: valid K/V + q + o; bias configs include the bias once).
@@ -43,8 +47,10 @@ METRIC = "flash-attn fwd TFLOP/s (% bf16 MFMA peak); split-KV decode HBM GB/s (%
 def _parse():
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
-    p.add_argument("--steps", type=int, default=20)
-    p.add_argument("--warmup", type=int, default=5)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--settle", type=float, default=0.5, metavar="SECONDS",
+                   help="untimed clock-settling run of each workload before its warmup steps")
     p.add_argument("--no-cpu-baseline", action="store_true",
                    help="skip the timed CPU oracle leg")
     p.add_argument("--only", default="",
@@ -174,11 +180,28 @@ def make_c5(dev, gen):
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
 
 
-def _time(fn, steps, warmup):
+def _settle(fn, seconds):
+    """Untimed clock settling: run the workload for `seconds` of wall time.
+
+    MI355X raises its clocks over the first tens of milliseconds of sustained
+    load; a C2 step measured after 5 warmup calls reads ~25% slower than
+    after 200.  Settling before the W warmup steps makes the K timed steps
+    the steady state whatever W the caller passes."""
+    import torch
+
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        for _ in range(8):
+            fn()
+        torch.cuda.synchronize()
+
+
+def _time(fn, steps, warmup, settle_s=0.0):
     """Wall time of `steps` back-to-back calls between device syncs, and the
     per-call average from HIP events recorded on the launch stream."""
     import torch
 
+    _settle(fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
@@ -286,7 +309,7 @@ def main():
     head = None
     for key in only:
         w = MAKERS[key](dev, gen)
-        wall_ms, ev_ms = _time(w["fn"], args.steps, args.warmup)
+        wall_ms, ev_ms = _time(w["fn"], args.steps, args.warmup, args.settle)
         tflops, gbs, frac = _rates(w, ev_ms)
         row = {"workload": w["name"], "ms": round(ev_ms, 5), "wall_ms": round(wall_ms, 5),
                "tflops": round(tflops, 2), "gbs": round(gbs, 1),
@@ -302,6 +325,7 @@ def main():
         torch.cuda.empty_cache()
 
     out = {"metric": METRIC, "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "settle_s": args.settle,
            "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
            "data": "synthetic (torch.randn N(0,1) on device, seed 0)"}
     if head is not None:

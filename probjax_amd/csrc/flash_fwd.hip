@@ -17,10 +17,11 @@
 // O^T = V^T P^T straight from registers (the lane layout of S^T's C operand is
 // the B-operand layout of the next MFMA up to a key permutation that V^T's
 // A operand reproduces), so the per-row rescale and 1/l are lane-local too.
-// K tiles are stored row-major in LDS; V tiles are transposed into LDS once
-// per tile (bf16) so that the A operand of P.V is two 8-byte LDS reads.
-// LDS is double-buffered with register prefetch: the global loads of tile
-// t+1 are in flight while tile t is computed; one barrier per tile.
+// bf16: K and V tiles go HBM -> LDS by buffer loads that write LDS directly,
+// both stored row-major; the A operand of P.V (V^T) comes from transposing
+// LDS reads of the row-major V tile.  fp32: tiles are staged through
+// registers.  Either way LDS holds two tiles, the loads of tile t+1 are in
+// flight while tile t is computed, and there is one barrier per tile.
 //
 // Grid: one workgroup per (q tile, batch, head), ordered heaviest causal
 // q-tile first (longest-processing-time order), and batch*head fastest so
