@@ -368,27 +368,6 @@ struct LatentTile {
   }
 };
 
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier for the buffer->LDS ring.  __syncthreads() carries a
-// workgroup release fence, which waits for every outstanding vector memory
-// operation of the wave -- including the next tile's loads, still in flight by
-// design.  Here the waits are explicit instead: this wave's LDS reads are
-// complete (lgkmcnt(0)) and the caller has waited for the loads whose data
-// the other waves will read (vmcnt); the wavefront-scope fences only keep the
-// compiler from moving LDS accesses across the barrier.
-__device__ __forceinline__ void stage_barrier() {
-  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
 template <int D, int DV>
 __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a) {
   using T = LatentTile<D>;

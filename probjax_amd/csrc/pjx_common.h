@@ -102,9 +102,10 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
 
 // Each lane loads 16 bytes at voffset; lane l's bytes land at lds_wave + 16*l
 // (lds_wave must be the same for every lane of the wave).
-__device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void* lds_wave, uint32_t voffset) {
+__device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void* lds_wave, uint32_t voffset,
+                                                  uint32_t soffset = 0) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16,
-                                           voffset, 0, 0, 0);
+                                           voffset, soffset, 0, 0);
 }
 
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
@@ -123,6 +124,27 @@ __device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ba
 // B lane l holds B[4*(l/16)+j][l%16]; C as for 16x16x32.
 __device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  // gfx9 s_waitcnt: vmcnt[3:0] | expcnt[6:4] | lgkmcnt[11:8] | vmcnt[5:4] << 14.
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier for the buffer->LDS ring.  __syncthreads() carries a
+// workgroup release fence, which waits for every outstanding vector memory
+// operation of the wave -- including the next tile's loads, still in flight by
+// design.  Here the waits are explicit instead: this wave's LDS reads are
+// complete (lgkmcnt(0)) and the caller has waited for the loads whose data
+// the other waves will read (vmcnt); the wavefront-scope fences only keep the
+// compiler from moving LDS accesses across the barrier.
+__device__ __forceinline__ void stage_barrier() {
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0)
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
 // Lazy softmax rescale: the running max used for exponentiation is raised

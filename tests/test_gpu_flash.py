@@ -92,6 +92,40 @@ def test_flash_bias_kvlen(device, dtype_name):
     assert max_abs(to_np(got), want) <= (F32_TOL if dtype_name == "f32" else BF16_TOL)
 
 
+@pytest.mark.parametrize(
+    "b,lq,lk,hq,hkv,d,causal,bias_bh,lengths",
+    [
+        (1, 300, 520, 4, 2, 64, False, (1, 1), None),           # partial tiles, rows past Lq, GQA, broadcast bias
+        (2, 200, 200, 2, 2, 128, True, (2, 2), [150, 200]),     # D=128 ring, causal + lengths, full bias
+        (1, 1024, 1024, 2, 2, 64, False, (1, 2), [1000]),       # 16 tiles: the 3-stage ring wraps, ragged end
+        (1, 512, 192, 2, 2, 64, True, (1, 2), None),            # exactly 3 tiles
+        (2, 130, 262, 2, 2, 64, True, (1, 2), [262, 5]),        # Lk % 4 != 0: bias through registers
+        (1, 64, 4096, 2, 1, 128, False, (1, 2), [4000]),        # long rows, one query tile
+    ],
+)
+def test_flash_bf16_bias_matches_oracle(device, b, lq, lk, hq, hkv, d, causal, bias_bh, lengths):
+    import torch
+
+    q, k, v = (oracle.round_bf16(x) for x in _inputs(5, b, lq, lk, hq, hkv, d))
+    (bias,) = rng_normal(6, (*bias_bh, lq, lk), scale=0.5)
+    scale = 1.0 / math.sqrt(d)
+    masks = [oracle.CausalMask()] if causal else []
+    if lengths is not None:
+        masks.append(oracle.KVLenMask(np.array(lengths, np.int32)))
+    mask = None if not masks else (masks[0] if len(masks) == 1 else oracle.ComposeMask("and", *masks))
+    want, want_lse = oracle.xla_attention(q, k, v, mask=mask, bias=oracle.DenseBias(bias), sm_scale=scale,
+                                          return_lse=True)
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    got, lse = _flash(*(to_dev(x, device, torch.bfloat16) for x in (q, k, v)), sm_scale=scale, causal=causal,
+                      kv_lengths=L, bias=to_dev(bias, device, torch.float32), return_lse=True)
+    torch.cuda.synchronize()
+    assert max_abs(to_np(got), want) <= BF16_TOL
+    lse = to_np(lse)
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
+    fin = np.isfinite(want_lse)
+    assert max_abs(lse[fin], want_lse[fin]) <= 1e-2
+
+
 def test_flash_fully_masked_rows_are_zero_and_masked_keys_exact(device):
     import torch
 
