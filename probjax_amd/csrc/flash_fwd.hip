@@ -544,6 +544,198 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
 }
 
 // ---------------------------------------------------------------------------
+// fp32, small grids: the key range of one 32-row query block is split over
+// the 8 waves of a workgroup, so a problem with few query tiles still spreads
+// over many SIMDs (the fp32 MFMA rate makes one wave's pass over all keys the
+// critical path otherwise).  Wave w takes 32-key blocks w, w+NW, w+2NW, ...;
+// each block's K half-rows and V columns are loaded from global memory
+// straight into the MFMA operand registers (the next block's loads are in
+// flight while one is computed), so no LDS staging is needed.  Each wave
+// keeps its own online softmax; the partial (max, sum, O) are combined in LDS
+// at the end.  NW = 8 waves for D = 64; D = 128 uses 4 (one per SIMD): its
+// double-buffered operand blocks need more than the 256 registers of two
+// waves per SIMD.  Products and softmax are those of flash_fwd_f32_kernel
+// (v_mfma_f32_32x32x2f32, keys as MFMA rows).
+// ---------------------------------------------------------------------------
+template <int D>
+constexpr int split_waves() { return D == 128 ? 4 : 8; }
+
+template <int D, bool BIAS>
+__global__ __launch_bounds__(64 * split_waves<D>(), 1) void flash_fwd_f32_split_kernel(FlashArgs a) {
+  constexpr int NW = split_waves<D>();
+  constexpr int DH = D / 2;          // floats per half row
+  constexpr int OS = D + 4;          // combine row stride (floats)
+  __shared__ __attribute__((aligned(16))) float red_o[NW * 32 * OS];
+  __shared__ float red_ml[NW * 32 * 2];
+
+  // Workgroup -> (32-row query block, batch, head); batch*head fastest.
+  const int BH = a.B * a.Hq;
+  const int bh = blockIdx.x % BH;
+  const int qb = blockIdx.x / BH;
+  const int b = bh / a.Hq, h = bh % a.Hq, hkv = h / (a.Hq / a.Hkv);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int qw = qb * 32;
+  const int qi = qw + col;
+  const int q_hi = min(a.Lq, a.q_valid);
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  int kv_stop = kv_end;
+  if (qw >= q_hi) kv_stop = 0;
+  else if (a.causal) kv_stop = min(kv_stop, min(qw + 32, q_hi));
+  const int nkb = (kv_stop + 31) / 32;
+  const bool row_in = qi < a.Lq;
+  const bool row_ok = qi < q_hi;
+  const size_t kv_row = (size_t)a.Hkv * D;
+  const float* Kb = (const float*)a.k + ((size_t)b * a.Lk * a.Hkv + hkv) * D;
+  const float* Vb = (const float*)a.v + ((size_t)b * a.Lk * a.Hkv + hkv) * D;
+
+  float qf[DH];
+  {
+    const float* qrow = (const float*)a.q + ((size_t)(b * a.Lq + (row_in ? qi : 0)) * a.Hq + h) * D + half * DH;
+#pragma unroll
+    for (int s = 0; s < DH / 4; ++s) {
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+      if (row_in) r = *(const f32x4*)(qrow + 4 * s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) qf[4 * s + j] = r[j];
+    }
+  }
+  const float* brow = nullptr;
+  if constexpr (BIAS)
+    brow = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride + (size_t)(row_in ? qi : 0) * a.Lk;
+  const bool bias_vec = (a.Lk & 3) == 0;
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  float m_run = kMaxInit, l_run = 0.f;
+
+  // Operand registers of one 32-key block: K half row of key k0 + col (dims
+  // half*D/2 + [0, D/2)); V column db*32 + col at the 16 keys of slot r
+  // (key k0 + 8*(r/4) + 4*half + r%4).  Keys at or past kv_stop read 0.
+  struct Block {
+    float k[DH];
+    float v[D / 32][16];
+  };
+  auto load = [&](int kbk, Block& blk) {
+    const int k0 = kbk * 32;
+    const int kk = k0 + col;
+    const bool kin = kbk < nkb && kk < kv_stop;
+    const float* kp = Kb + (size_t)(kin ? kk : 0) * kv_row + half * DH;
+#pragma unroll
+    for (int s = 0; s < DH / 4; ++s) {
+      f32x4 r = {0.f, 0.f, 0.f, 0.f};
+      if (kin) r = *(const f32x4*)(kp + 4 * s);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) blk.k[4 * s + j] = r[j];
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      const bool vin = kbk < nkb && key < kv_stop;
+      const float* vp = Vb + (size_t)(vin ? key : 0) * kv_row + col;
+#pragma unroll
+      for (int db = 0; db < D / 32; ++db) blk.v[db][r] = vin ? vp[db * 32] : 0.f;
+    }
+  };
+  auto compute = [&](int kbk, const Block& blk) {
+    const int k0 = kbk * 32;
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int st = 0; st < DH; ++st) s = mfma32x32x2f32(blk.k[st], qf[st], s);
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const int kk = k0 + 8 * gq + 4 * half;
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[4 * gq + j] = fmaf(s[4 * gq + j], a.scale, bv[j]);
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int kk = k0 + 8 * (r >> 2) + 4 * half + (r & 3);
+      const bool keep = row_ok && kk < kv_end && (!a.causal || kk <= qi);
+      if (!keep) s[r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) mx = fmaxf(mx, s[r]);
+    mx = xor32_max(mx);
+    const float m_new = fmaxf(m_run, mx * cx);
+    const float corr = fast_exp2(m_run - m_new);
+    m_run = m_new;
+    float rs = 0.f;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const float p = fast_exp2(fmaf(s[r], cx, -m_new));
+      rs += p;
+      s[r] = p;
+    }
+    l_run = fmaf(l_run, corr, rs);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i) acc[i] *= corr;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[db] = mfma32x32x2f32(blk.v[db][r], s[r], acc[db]);
+  };
+
+  // This wave's blocks w, w+NW, ... (a wave may have none: it then combines
+  // an empty partial).
+  Block cur, nxt;
+  load(w, cur);
+  for (int kbk = w; kbk < nkb; kbk += NW) {
+    load(kbk + NW, nxt);
+    compute(kbk, cur);
+    cur = nxt;
+  }
+
+  // ---- combine the NW partials in LDS ----
+  l_run = xor32_sum(l_run);
+  {
+    float* ro = red_o + (size_t)w * 32 * OS;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq)
+        *(f32x4*)(ro + col * OS + db * 32 + 8 * gq + 4 * half) =
+            f32x4{acc[db][4 * gq], acc[db][4 * gq + 1], acc[db][4 * gq + 2], acc[db][4 * gq + 3]};
+    if (half == 0) {
+      red_ml[(w * 32 + col) * 2] = m_run;
+      red_ml[(w * 32 + col) * 2 + 1] = l_run;
+    }
+  }
+  __syncthreads();
+  constexpr int NQ = D / 4;
+  for (int idx = tid; idx < 32 * NQ; idx += 64 * NW) {
+    const int r = idx / NQ, u = idx % NQ;
+    const int q = qw + r;
+    float M = kMaxInit;
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) M = fmaxf(M, red_ml[(ww * 32 + r) * 2]);
+    float L = 0.f;
+    f32x4 O = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ww = 0; ww < NW; ++ww) {
+      const float wt = fast_exp2(red_ml[(ww * 32 + r) * 2] - M);
+      L = fmaf(wt, red_ml[(ww * 32 + r) * 2 + 1], L);
+      O += wt * *(const f32x4*)(red_o + (size_t)(ww * 32 + r) * OS + 4 * u);
+    }
+    if (q < a.Lq) {
+      const float inv = L > 0.f ? 1.f / L : 0.f;
+      *(f32x4*)((float*)a.o + ((size_t)(b * a.Lq + q) * a.Hq + h) * D + 4 * u) = O * inv;
+      if (a.lse && u == 0)
+        a.lse[((size_t)b * a.Hq + h) * a.Lq + q] = L > 0.f ? (M + __log2f(L)) * kLn2 : INFINITY;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
 // bf16 path with a dense fp32 bias, streamed through LDS.  The bias is the
 // bulk of the bytes (4 B per score against 4*D bytes of K/V per key shared by
 // 128 queries), so the kernel is a streaming kernel: each stage of an NS-deep
@@ -821,6 +1013,15 @@ static int launch(K kernel, const FlashArgs& a, hipStream_t stream) {
   return check_launch("pjx_flash_fwd");
 }
 
+// The fp32 split kernel: one workgroup per 32-row query block.
+template <int D, typename K>
+static int launch_split(K kernel, const FlashArgs& a, hipStream_t stream) {
+  const long blocks = (long)((a.Lq + 31) / 32) * a.B * a.Hq;
+  if (blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: grid too large");
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(64 * split_waves<D>()), 0, stream, a);
+  return check_launch("pjx_flash_fwd");
+}
+
 }  // namespace pjx
 
 using namespace pjx;
@@ -876,6 +1077,16 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
     }
     if (ring) return launch(flash_fwd_bf16_bias_ring_kernel<64>, a, s);
     return hb ? launch(flash_fwd_bf16_kernel<64, true>, a, s) : launch(flash_fwd_bf16_kernel<64, false>, a, s);
+  }
+  // fp32 with fewer 128-row workgroups than CUs: split each query block's
+  // keys over several waves (latency-bound sizes, like the reference's CPU
+  // case).
+  if ((long)a.n_qtiles * batch * q_heads < 256) {
+    if (head_dim == 128)
+      return hb ? launch_split<128>(flash_fwd_f32_split_kernel<128, true>, a, s)
+                : launch_split<128>(flash_fwd_f32_split_kernel<128, false>, a, s);
+    return hb ? launch_split<64>(flash_fwd_f32_split_kernel<64, true>, a, s)
+              : launch_split<64>(flash_fwd_f32_split_kernel<64, false>, a, s);
   }
   if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true>, a, s) : launch(flash_fwd_f32_kernel<128, false>, a, s);
   return hb ? launch(flash_fwd_f32_kernel<64, true>, a, s) : launch(flash_fwd_f32_kernel<64, false>, a, s);

@@ -36,6 +36,10 @@ def _inputs(seed, b, lq, lk, hq, hkv, d):
         (2, 300, 300, 2, 2, 64, True),   # ragged
         (1, 200, 333, 4, 2, 128, False),  # GQA, unaligned
         (1, 130, 130, 2, 1, 128, True),
+        # >= 256 query tiles of 128 rows: the one-pass fp32 kernel (the cases
+        # above split each query block's keys over several waves)
+        (1, 1024, 1024, 32, 8, 64, True),
+        (1, 640, 700, 64, 64, 128, False),
     ],
 )
 def test_flash_f32_matches_oracle(device, b, lq, lk, hq, hkv, d, causal):
