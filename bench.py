@@ -57,6 +57,9 @@ def _parse():
                    help="comma list of configs to run (C1..C5); default all")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (counter calibration) and exit")
+    p.add_argument("--gemm-calibration", type=int, default=0, metavar="N",
+                   help="only time a library bf16 GEMM N x N x N (torch.matmul -> hipBLASLt), the "
+                        "practical MFMA ceiling on this box, and exit")
     return p.parse_args()
 
 
@@ -72,6 +75,19 @@ def copy_calibration(mib, reps=5):
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_calibration_bytes_each_way": n * 4, "reps": reps}), flush=True)
+
+
+def gemm_calibration(n, settle_s, steps=10):
+    """A library bf16 GEMM (torch.matmul, hipBLASLt) after clock settling:
+    the MFMA rate a plain GEMM sustains within this box's power limit."""
+    import torch
+
+    a = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    b = torch.randn(n, n, device="cuda", dtype=torch.bfloat16)
+    fn = lambda: torch.matmul(a, b)  # noqa: E731
+    wall_ms, ev_ms = _time(fn, steps, 2, settle_s)
+    print(json.dumps({"gemm_calibration": f"bf16 {n}x{n}x{n}", "ms": round(ev_ms, 4),
+                      "tflops": round(2 * n ** 3 / (ev_ms * 1e-3) / 1e12, 1)}), flush=True)
 
 
 # ---------------------------------------------------------------------------
@@ -296,6 +312,9 @@ def main():
         sys.exit(1)
     if args.copy_calibration:
         copy_calibration(args.copy_calibration)
+        return
+    if args.gemm_calibration:
+        gemm_calibration(args.gemm_calibration, args.settle)
         return
     from probjax_amd import native
 
