@@ -36,6 +36,16 @@ HIPCC_FLAGS = [
 ]
 
 
+# Extra flags for single sources.  flash_bias_ring.hip: its LDS ring leaves one
+# wave per SIMD, and at that occupancy the compiler would put the MFMA
+# accumulators in AGPRs and copy every score out of them for the softmax;
+# forcing the VGPR form of the MFMAs keeps the scores where the softmax reads
+# them (the kernel fits in 256 VGPRs).
+FILE_FLAGS = {
+    "flash_bias_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -44,7 +54,7 @@ def hipcc() -> str:
 
 
 def _compile(src: Path, obj: Path) -> str:
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *FILE_FLAGS.get(src.name, []), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     out = "\n".join(
         line for line in (res.stdout + res.stderr).splitlines() if "packed-fp32-ops" not in line
