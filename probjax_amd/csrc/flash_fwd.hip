@@ -23,6 +23,10 @@
 // registers.  Either way LDS holds two tiles, the loads of tile t+1 are in
 // flight while tile t is computed, and there is one barrier per tile.
 //
+// This file also holds the fp32 kernel for small grids (each query block's
+// keys split over the waves of a workgroup) and pjx_flash_fwd, which picks
+// the kernel; the bf16 dense-bias kernel is in flash_bias_ring.hip.
+//
 // Grid: one workgroup per (q tile, batch, head), ordered heaviest causal
 // q-tile first (longest-processing-time order), and batch*head fastest so
 // that every q-tile of one (batch, head) lands on the same XCD (workgroups are
