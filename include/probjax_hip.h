@@ -72,6 +72,41 @@ int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* 
                   void* stream);
 
 /*
+ * Bytes of workspace pjx_flash_bwd needs: two fp32 values per query row
+ * (delta = sum_d o*do and the base-2 LSE), 8 * batch * q_heads * q_len.
+ */
+size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_len);
+
+/*
+ * Flash-attention backward: dq, dk, dv of pjx_flash_fwd's output.  Replaces
+ * the Pallas backward of `mha` (probjax/nn/pallas_kernels/kernels/
+ * attention.py: _preprocess_backward_kernel 853-867, mha_backward_kernel
+ * 909-1160, _mha_backward_raw 3505-3560 with the GQA group sums 2123-2128):
+ *
+ *   delta = sum_d o*do;  p = exp(s - lse);  ds = p * (do.v^T - delta) * sm_scale
+ *   dv = sum_q bf16(p)^T do,  dk = sum_q bf16(ds)^T q,  dq = sum_k bf16(ds) k
+ *
+ * with s the forward's score (sm_scale * q.k + bias, masked keys excluded)
+ * and fp32 accumulation; dk/dv sum the query heads of each KV head's group.
+ * The dense bias gets no gradient (the reference's custom VJP returns zeros
+ * for it, attention.py:3262-3263).
+ *
+ * Arguments as pjx_flash_fwd, plus: o the forward output, dout [B, Lq, Hq, D]
+ * the output gradient, lse the forward's natural-log LSE [B, Hq, Lq] (+inf
+ * rows contribute nothing); dq [B, Lq, Hq, D], dk and dv [B, Lk, Hkv, D]
+ * (fully written, zeros where no valid score reaches).  workspace: at least
+ * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.
+ * dtype: PJX_DTYPE_BF16.  head_dim in {64, 128}.
+ */
+int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                  const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                  void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
+                  const float* bias, int64_t bias_batch, int64_t bias_heads, int64_t batch,
+                  int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                  int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
+                  float sm_scale, void* stream);
+
+/*
  * Bytes of workspace pjx_splitkv_decode / pjx_mla_decode need for these sizes
  * (partial outputs and log-sum-exp terms of every KV chunk).
  *   rows   -- query rows per (batch, kv head): (Hq/Hkv)*Lq for GQA decode,

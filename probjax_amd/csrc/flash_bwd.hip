@@ -1,0 +1,595 @@
+// Flash-attention backward for gfx950 (bf16 inputs, fp32 accumulation).
+//
+// Replaces the Pallas backward of probjax's `mha`:
+//   _preprocess_backward_kernel (probjax/nn/pallas_kernels/kernels/attention.py:853-867)
+//   mha_backward_kernel         (:909-1160; scan #1 dK/dV :989-1052, scan #2 dQ :1089-1150)
+//   _mha_backward_raw           (:3505-3560; GQA group sums :2123-2128)
+// with the math of those kernels:
+//   delta = sum_d o * do;  p = exp2(s * log2e - lse * log2e);  dp = do . v^T
+//   ds = p * (dp - delta) * sm_scale
+//   dv = sum_q bf16(p)^T do,  dk = sum_q bf16(ds)^T q,  dq = sum_k bf16(ds) k.
+// s is the forward's score: sm_scale * q.k [+ bias], masked keys excluded.
+// lse is the forward's natural-log residual (+inf for rows without a valid
+// key: p = 0 there, so those rows contribute nothing).
+//
+// Two kernels on the caller's stream:
+//   flash_bwd_dq_kernel   -- one workgroup per (128-query tile, batch, head),
+//     as the forward: K/V tiles of 64 keys stream HBM -> LDS; S^T = K Q^T and
+//     dP^T = V dO^T with keys as MFMA rows, so each lane holds one query's
+//     column and its lse / delta are one register each; dQ^T += K^T dS^T with
+//     K^T read by transposing LDS reads.  It also computes delta for its rows
+//     (o and dO are read once, for dO^T) and writes delta and lse*log2e to
+//     the workspace for the second kernel.
+//   flash_bwd_dkdv_kernel -- one workgroup per (128-key tile, batch, KV head),
+//     each wave owns 32 keys whose K^T and V^T stay in registers; Q and dO
+//     tiles of 64 queries of every query head of the group stream through
+//     LDS.  S = Q K^T and dP = dO V^T put queries on the MFMA rows, so P and
+//     dS in registers are directly the B operands of dV^T += dO^T P and
+//     dK^T += Q^T dS (dO^T and Q^T by transposing LDS reads).  The group's
+//     query heads accumulate in fp32 before the single rounding to bf16.
+//
+// LDS tiles (both kernels) are row-major [row][dim] with 16-byte chunks
+// XOR-swizzled so that both reads of a tile are free of bank conflicts: the
+// 16-byte reads of one chunk column over 16 consecutive rows, and the
+// transposing 8-byte reads of 4 aligned rows x 4 consecutive chunks.
+#include "flash_common.h"
+
+namespace pjx {
+
+struct FlashBwdArgs {
+  FlashArgs f;        // q, k, v, o (forward output), lse, masks, bias, sizes
+  const void* dout;   // dO [B, Lq, Hq, D]
+  float* delta;       // workspace [B, Hq, Lq]
+  float* lse2;        // workspace [B, Hq, Lq]: lse * log2e
+  void* dq;
+  void* dk;
+  void* dv;
+};
+
+constexpr int kBKV = 128;  // keys per dK/dV workgroup (32 per wave)
+constexpr int kBQs = 64;   // queries per dK/dV LDS stage
+
+template <int D>
+struct BwdTile {
+  static constexpr int ROWS = 64;            // rows per tile
+  static constexpr int ROWB = D * 2;         // bytes per row
+  static constexpr int NC = D / 8;           // 16-byte chunks per row
+  static constexpr int TILE_B = ROWS * ROWB;
+  static constexpr int RPI = 64 / NC;        // rows per 1 KiB wave load
+  static constexpr int NLD = (ROWS / 4) / RPI;  // loads per wave per tensor per tile
+  // Bijective over any 16 consecutive rows (16-byte column reads), and the
+  // 4 rows of an aligned group differ in the chunk bits above the 4-chunk
+  // block of a transposing read (D=128: bits 3:2; D=64 with two rows per bank
+  // line: bit 2 between rows of equal parity).
+  __device__ static int swz(int r) {
+    return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+  }
+};
+
+// Per-lane LDS byte offsets of a tile's two read patterns.
+template <int D>
+struct BwdOffsets {
+  using T = BwdTile<D>;
+  uint32_t row[D / 16];   // A = X[row][dim]: row `col` of a 32-row block, dims 16*s + 8*half
+  uint32_t tlo[D / 32];   // A = X^T: transposing reads, rows 4*half + s16/4 of a 16-row step
+  uint32_t thi[D / 32];   // ... and rows 8 + 4*half + s16/4
+  __device__ void init(int lane) {
+    const int col = lane & 31, half = lane >> 5;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) row[s] = col * T::ROWB + 16 * ((2 * s + half) ^ T::swz(col));
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int r = 4 * half + s16 / 4;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int chunk = 4 * db + 2 * (grp & 1) + ((s16 & 3) >> 1);
+      tlo[db] = r * T::ROWB + 16 * (chunk ^ T::swz(r)) + 8 * (s16 & 1);
+      thi[db] = (r + 8) * T::ROWB + 16 * (chunk ^ T::swz(r + 8)) + 8 * (s16 & 1);
+    }
+  }
+};
+
+// A operand X^T (dims 32*db.., 16 rows starting at row0 in slot order
+// 8*(j/4) + 4*half + j%4) from a row-major tile.
+template <int D>
+__device__ __forceinline__ bf16x8 read_t(const unsigned char* tile, int row0, uint32_t lo, uint32_t hi) {
+  const unsigned char* p = tile + row0 * BwdTile<D>::ROWB;
+  const u32x2 a = lds_read_tr16(p + lo);
+  const u32x2 b = lds_read_tr16(p + hi);
+  const u32x4 v = {a[0], a[1], b[0], b[1]};
+  return as_bf16x8(v);
+}
+
+// Registers of a 32x32 C block as the B operand of the next product:
+// k-step c (16 rows) holds registers 8c .. 8c+7, rounded to bf16.
+__device__ __forceinline__ bf16x8 pack_step(const f32x16& x, int c) {
+  u32x4 pk;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(x[8 * c + 2 * j], x[8 * c + 2 * j + 1]);
+  return as_bf16x8(pk);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// ---------------------------------------------------------------------------
+// dQ (and delta): one workgroup per (128-query tile, batch, head).
+// ---------------------------------------------------------------------------
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  using T = BwdTile<D>;
+  constexpr int BK = T::ROWS, ROWB = T::ROWB, TILE_B = T::TILE_B;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[2 * TILE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[2 * TILE_B];
+
+  BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  g.qw = __builtin_amdgcn_readfirstlane(g.qw);
+  const int col = lane & 31, half = lane >> 5;
+  const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
+  const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
+  const unsigned char* Vb = (const unsigned char*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
+  const bool row_in = g.qi < a.Lq;
+  const bool row_ok = g.qi < g.q_hi;
+
+  // Q^T and dO^T as B operands (lane: query `col`, dims 16*s + 8*half + [0,8)),
+  // and delta = sum_d o*do of this query over both halves.
+  bf16x8 qf[D / 16], dof[D / 16];
+  float dsum = 0.f;
+  {
+    const size_t roff = ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
+    const uint16_t* qrow = (const uint16_t*)a.q + roff;
+    const uint16_t* drow = (const uint16_t*)ba.dout + roff;
+    const uint16_t* orow = (const uint16_t*)a.o + roff;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      u32x4 rq = {0u, 0u, 0u, 0u}, rd = rq, ro = rq;
+      if (row_in) {
+        rq = *(const u32x4*)(qrow + 16 * s + 8 * half);
+        rd = *(const u32x4*)(drow + 16 * s + 8 * half);
+        ro = *(const u32x4*)(orow + 16 * s + 8 * half);
+      }
+      qf[s] = as_bf16x8(rq);
+      dof[s] = as_bf16x8(rd);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dsum = fmaf(bf16_lo(ro[j]), bf16_lo(rd[j]), fmaf(bf16_hi(ro[j]), bf16_hi(rd[j]), dsum));
+    }
+  }
+  const float delta = xor32_sum(dsum);
+  float lse2 = 0.f;
+  const size_t lidx = ((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi;
+  if (row_in) {
+    lse2 = a.lse[lidx] * kLog2e;
+    if (half == 0) {
+      ba.delta[lidx] = delta;
+      ba.lse2[lidx] = lse2;
+    }
+  }
+  const float* brow = nullptr;
+  if constexpr (BIAS) {
+    brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
+           (size_t)(row_in ? g.qi : 0) * a.Lk;
+  }
+  const bool bias_vec = (a.Lk & 3) == 0;
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+
+  uint32_t voff[T::NLD];
+#pragma unroll
+  for (int j = 0; j < T::NLD; ++j) {
+    const int r = 16 * w + T::RPI * j + lane / T::NC, slot = lane % T::NC;
+    voff[j] = r * rowstride + 16 * (slot ^ T::swz(r));
+  }
+  BwdOffsets<D> off;
+  off.init(lane);
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+
+  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int q_last_w = g.qw + 31;
+
+  auto issue = [&](int t, unsigned char* ks) {
+    const int k0 = t * BK;
+    const int nvalid = min(BK, g.kv_stop - k0);
+    const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
+    const rsrc_t rk = make_rsrc(Kb + (size_t)k0 * rowstride, bytes);
+    const rsrc_t rv = make_rsrc(Vb + (size_t)k0 * rowstride, bytes);
+#pragma unroll
+    for (int j = 0; j < T::NLD; ++j) {
+      const int r0 = 16 * w + T::RPI * j;
+      buffer_load_lds16(rk, ks + r0 * ROWB, voff[j]);
+      buffer_load_lds16(rv, ks + TILE_B + r0 * ROWB, voff[j]);
+    }
+  };
+
+  auto compute = [&](int t, const unsigned char* ks) {
+    const int k0 = t * BK;
+    if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    const unsigned char* vs = ks + TILE_B;
+
+    // S^T[key][query] = K Q^T and dP^T = V dO^T; register r of block kb holds
+    // key k0 + kb*32 + 8*(r/4) + 4*half + r%4 of query `col`.
+    f32x16 s[BK / 32], dp[BK / 32];
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb) {
+      s[kb] = f32x16{};
+      dp[kb] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + off.row[st]));
+        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+      }
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 vf = as_bf16x8(*(const u32x4*)(vs + kb * 32 * ROWB + off.row[st]));
+        dp[kb] = mfma32x32x16(vf, dof[st], dp[kb]);
+      }
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
+        }
+    }
+    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                           (g.qw + 31 >= g.q_hi);
+    if (need_mask) {
+      const int base = k0 + 4 * half;
+      int lim = g.kv_end - 1 - base;
+      if (a.causal) lim = min(lim, g.qi - base);
+      if (!row_ok) lim = -1;
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
+    }
+    // dS^T = P^T (dP^T - delta) * scale, rounded to bf16 as the B operand.
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
+        s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
+      }
+    bf16x8 dsf[BK / 16];
+#pragma unroll
+    for (int c = 0; c < BK / 16; ++c) dsf[c] = pack_step(s[c >> 1], c & 1);
+    // dQ^T[d][query] += K^T dS^T
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int c = 0; c < BK / 16; ++c)
+        acc[db] = mfma32x32x16(read_t<D>(ks, 16 * c, off.tlo[db], off.thi[db]), dsf[c], acc[db]);
+  };
+
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
+  }
+
+  if (row_in) {
+    uint16_t* drow = (uint16_t*)ba.dq + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2 pk;
+        pk[0] = pack_bf16x2(acc[db][4 * gq], acc[db][4 * gq + 1]);
+        pk[1] = pack_bf16x2(acc[db][4 * gq + 2], acc[db][4 * gq + 3]);
+        *(u32x2*)(drow + db * 32 + 8 * gq + 4 * half) = pk;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV: one workgroup per (128-key tile, batch, KV head).
+// ---------------------------------------------------------------------------
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  using T = BwdTile<D>;
+  constexpr int ROWB = T::ROWB, TILE_B = T::TILE_B;
+  static_assert(T::ROWS == kBQs, "one Q / dO tile per stage");
+  // Per stage: Q tile, dO tile, then each wave's own copy of the stage's
+  // lse*log2e and delta (64 floats each).
+  constexpr int SMALL_B = 2 * kBQs * 4;
+  constexpr int STAGE_B = 2 * TILE_B + 4 * SMALL_B;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int BH = a.B * a.Hkv;
+  const int bh = blockIdx.x % BH;
+  const int k0 = (blockIdx.x / BH) * kBKV;
+  const int b = bh / a.Hkv, hkv = bh % a.Hkv;
+  const int G = a.Hq / a.Hkv;
+  const int kw = k0 + 32 * w;
+  const int key = kw + col;
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  const int q_hi = min(a.Lq, a.q_valid);
+  // Queries that can see a key of this tile: causal rows start at k0.
+  const int q_begin = a.causal ? (k0 / kBQs) * kBQs : 0;
+  const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + kBQs - 1) / kBQs : 0;
+  const int n_tiles = G * n_qt;
+
+  // K^T and V^T as B operands: lane holds key `key`, dims 16*s + 8*half + [0,8).
+  bf16x8 kf[D / 16], vf[D / 16];
+  {
+    const bool kin = key < a.Lk;
+    const size_t koff = ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * D;
+    const uint16_t* krow = (const uint16_t*)a.k + koff;
+    const uint16_t* vrow = (const uint16_t*)a.v + koff;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      u32x4 rk = {0u, 0u, 0u, 0u}, rv = rk;
+      if (kin) {
+        rk = *(const u32x4*)(krow + 16 * s + 8 * half);
+        rv = *(const u32x4*)(vrow + 16 * s + 8 * half);
+      }
+      kf[s] = as_bf16x8(rk);
+      vf[s] = as_bf16x8(rv);
+    }
+  }
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const uint32_t rowstride = (uint32_t)a.Hq * D * 2;
+
+  uint32_t voff[T::NLD];
+#pragma unroll
+  for (int j = 0; j < T::NLD; ++j) {
+    const int r = 16 * w + T::RPI * j + lane / T::NC, slot = lane % T::NC;
+    voff[j] = r * rowstride + 16 * (slot ^ T::swz(r));
+  }
+  BwdOffsets<D> off;
+  off.init(lane);
+
+  f32x16 acck[D / 32], accv[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    acck[i] = f32x16{};
+    accv[i] = f32x16{};
+  }
+
+  auto tile_head = [&](int t) { return hkv * G + t / n_qt; };
+  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * kBQs; };
+
+  auto issue = [&](int t, unsigned char* st) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    const int nvalid = min(kBQs, a.Lq - q0);
+    const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
+    const size_t roff = ((size_t)(b * a.Lq + q0) * a.Hq + h) * ROWB;
+    const rsrc_t rq = make_rsrc((const unsigned char*)a.q + roff, bytes);
+    const rsrc_t rd = make_rsrc((const unsigned char*)ba.dout + roff, bytes);
+#pragma unroll
+    for (int j = 0; j < T::NLD; ++j) {
+      const int r0 = 16 * w + T::RPI * j;
+      buffer_load_lds16(rq, st + r0 * ROWB, voff[j]);
+      buffer_load_lds16(rd, st + TILE_B + r0 * ROWB, voff[j]);
+    }
+    const size_t loff = ((size_t)b * a.Hq + h) * a.Lq + q0;
+    const rsrc_t rl = make_rsrc(ba.lse2 + loff, (uint32_t)nvalid * 4);
+    const rsrc_t rdl = make_rsrc(ba.delta + loff, (uint32_t)nvalid * 4);
+    unsigned char* small = st + 2 * TILE_B + w * SMALL_B;
+    buffer_load_lds4(rl, small, 4 * lane);
+    buffer_load_lds4(rdl, small + kBQs * 4, 4 * lane);
+  };
+
+  auto compute = [&](int t, const unsigned char* st) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    const unsigned char* qs = st;
+    const unsigned char* dos = st + TILE_B;
+    const float* lsm = (const float*)(st + 2 * TILE_B + w * SMALL_B);
+    const float* dlm = lsm + kBQs;
+    const float* bbase = nullptr;
+    if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
+#pragma unroll
+    for (int qb = 0; qb < kBQs / 32; ++qb) {
+      const int qs0 = q0 + 32 * qb;
+      if (qs0 >= q_hi || kw >= kv_end) continue;
+      if (a.causal && qs0 + 31 < kw) continue;  // every query before this wave's first key
+
+      // S[query][key] = Q K^T: register r holds query qs0 + 8*(r/4) + 4*half + r%4
+      // of key `key`.
+      f32x16 s = f32x16{};
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        const bf16x8 qf = as_bf16x8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[k]));
+        s = mfma32x32x16(qf, kf[k], s);
+      }
+      if constexpr (BIAS) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qr = qs0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const float bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
+          s[r] = fmaf(s[r], a.scale, bv);
+        }
+      }
+      const bool need_mask = (a.causal && qs0 < kw + 31) || (kw + 32 > kv_end) || (qs0 + 32 > q_hi);
+      if (need_mask) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int qr = qs0 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool keep = key < kv_end && qr < q_hi && (!a.causal || qr >= key);
+          if (!keep) s[r] = -INFINITY;
+        }
+      }
+      // P, and dV^T[d][key] += dO^T P
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 l4 = *(const f32x4*)(lsm + 32 * qb + 8 * gq + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[4 * gq + j] = fast_exp2(fmaf(s[4 * gq + j], cx, -l4[j]));
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 pf = pack_step(s, c);
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+          accv[db] = mfma32x32x16(read_t<D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
+      }
+      // dP = dO V^T; dS = P (dP - delta) * scale; dK^T[d][key] += Q^T dS
+      f32x16 dp = f32x16{};
+#pragma unroll
+      for (int k = 0; k < D / 16; ++k) {
+        const bf16x8 df = as_bf16x8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[k]));
+        dp = mfma32x32x16(df, vf[k], dp);
+      }
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        const f32x4 d4 = *(const f32x4*)(dlm + 32 * qb + 8 * gq + 4 * half);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s[4 * gq + j] = s[4 * gq + j] * (dp[4 * gq + j] - d4[j]) * a.scale;
+      }
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bf16x8 dsf = pack_step(s, c);
+#pragma unroll
+        for (int db = 0; db < D / 32; ++db)
+          acck[db] = mfma32x32x16(read_t<D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
+      }
+    }
+  };
+
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
+  }
+
+  // dK, dV rows of this lane's key (zeros for keys past the valid length).
+  if (key < a.Lk) {
+    const size_t koff = ((size_t)(b * a.Lk + key) * a.Hkv + hkv) * D;
+    uint16_t* dkrow = (uint16_t*)ba.dk + koff;
+    uint16_t* dvrow = (uint16_t*)ba.dv + koff;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2 pk, pv;
+        pk[0] = pack_bf16x2(acck[db][4 * gq], acck[db][4 * gq + 1]);
+        pk[1] = pack_bf16x2(acck[db][4 * gq + 2], acck[db][4 * gq + 3]);
+        pv[0] = pack_bf16x2(accv[db][4 * gq], accv[db][4 * gq + 1]);
+        pv[1] = pack_bf16x2(accv[db][4 * gq + 2], accv[db][4 * gq + 3]);
+        *(u32x2*)(dkrow + db * 32 + 8 * gq + 4 * half) = pk;
+        *(u32x2*)(dvrow + db * 32 + 8 * gq + 4 * half) = pv;
+      }
+  }
+}
+
+template <typename K>
+static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
+  const long blocks = (long)a.f.n_qtiles * a.f.B * a.f.Hq;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  return check_launch("pjx_flash_bwd (dq)");
+}
+
+template <typename K>
+static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
+  const long blocks = (long)((a.f.Lk + kBKV - 1) / kBKV) * a.f.B * a.f.Hkv;
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  return check_launch("pjx_flash_bwd (dk, dv)");
+}
+
+// dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
+// dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
+template <int D>
+static int run_bwd(const FlashBwdArgs& a, bool hb, hipStream_t s) {
+  if (a.f.Lq > 0) {
+    const int rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false>, a, s);
+    if (rc != PJX_OK) return rc;
+  }
+  if (a.f.Lk == 0) return PJX_OK;
+  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<D, true>, a, s) : launch_dkdv(flash_bwd_dkdv_kernel<D, false>, a, s);
+}
+
+}  // namespace pjx
+
+using namespace pjx;
+
+extern "C" size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_len) {
+  if (batch <= 0 || q_heads <= 0 || q_len <= 0) return 0;
+  return (size_t)(2 * batch * q_heads * q_len) * sizeof(float);
+}
+
+extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
+                             const void* dout, const float* lse, void* dq, void* dk, void* dv,
+                             void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
+                             const float* bias, int64_t bias_batch, int64_t bias_heads,
+                             int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
+                             int64_t kv_heads, int64_t head_dim, int64_t q_valid, int64_t kv_valid,
+                             int causal, float sm_scale, void* stream) {
+  clear_error();
+  if (dtype != PJX_DTYPE_BF16)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16");
+  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q, k, v, o, dout, lse, dq, dk, dv must be non-null");
+  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: negative or zero size");
+  if (q_heads % kv_heads != 0)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q_heads must be a multiple of kv_heads");
+  if (head_dim != 64 && head_dim != 128)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128");
+  if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sm_scale must be > 0");
+  if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
+  const int64_t elems = std::max(batch * q_len * q_heads, batch * kv_len * kv_heads) * head_dim;
+  if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30) ||
+      (int64_t)q_heads * head_dim * 2 * 64 > 0xffffffffLL)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sizes out of range");
+  if (batch == 0 || (q_len == 0 && kv_len == 0)) return PJX_OK;
+  const size_t need = pjx_flash_bwd_workspace_size(batch, q_heads, q_len);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(PJX_ERR_WORKSPACE, "pjx_flash_bwd: workspace missing or smaller than pjx_flash_bwd_workspace_size()");
+
+  FlashBwdArgs ba;
+  FlashArgs& a = ba.f;
+  a.q = q; a.k = k; a.v = v; a.o = const_cast<void*>(o); a.lse = const_cast<float*>(lse);
+  a.kv_lengths = kv_lengths;
+  a.bias = bias;
+  a.bias_hstride = (bias && bias_heads != 1) ? q_len * kv_len : 0;
+  a.bias_bstride = (bias && bias_batch != 1) ? bias_heads * q_len * kv_len : 0;
+  a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len;
+  a.Hq = (int)q_heads; a.Hkv = (int)kv_heads;
+  a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
+  a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
+  a.causal = causal ? 1 : 0;
+  a.scale = sm_scale;
+  a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
+  if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL ||
+      (long)((kv_len + kBKV - 1) / kBKV) * batch * kv_heads > 0x7fffffffL)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: grid too large");
+  ba.dout = dout;
+  ba.delta = (float*)workspace;
+  ba.lse2 = ba.delta + batch * q_heads * q_len;
+  ba.dq = dq; ba.dk = dk; ba.dv = dv;
+  hipStream_t s = (hipStream_t)stream;
+  const bool hb = bias != nullptr;
+  return head_dim == 128 ? run_bwd<128>(ba, hb, s) : run_bwd<64>(ba, hb, s);
+}

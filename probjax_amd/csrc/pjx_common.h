@@ -108,6 +108,12 @@ __device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void* lds_wave, uint
                                            voffset, soffset, 0, 0);
 }
 
+// Each lane loads 4 bytes at voffset; lane l's bytes land at lds_wave + 4*l.
+__device__ __forceinline__ void buffer_load_lds4(rsrc_t r, void* lds_wave, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 4,
+                                           voffset, 0, 0, 0);
+}
+
 // ds_read_b64_tr_b16: within each group of 16 lanes, lane i receives element
 // i%4 of the 8-byte words addressed by lanes i/4, i/4+4, i/4+8, i/4+12 (in
 // that order).  Pointing lane s at row (s/4), 16-bit columns 4*(s%4)..+3 of a

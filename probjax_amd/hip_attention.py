@@ -103,6 +103,56 @@ def flash_attention_fwd(
     return (o, lse) if return_lse else o
 
 
+def flash_attention_bwd(
+    q, k, v, o, do, lse, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
+    q_valid: int | None = None, kv_valid: int | None = None, workspace=None,
+):
+    """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``.
+
+    ``o`` and ``lse`` are the forward's output and natural-log LSE; ``do`` the
+    output gradient.  Masks, bias and scale must be the forward's.  bf16 only.
+    """
+    dev = _on_device(q, k, v, o, do, lse, bias)
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
+        raise ValueError("q, k, v must be [B, T, H, D]")
+    B, Lq, Hq, D = q.shape
+    _, Lk, Hkv, Dk = k.shape
+    if k.shape != v.shape or k.shape[0] != B or Dk != D:
+        raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
+    if o.shape != q.shape or do.shape != q.shape or tuple(lse.shape) != (B, Hq, Lq):
+        raise ValueError("o and do must be shaped like q and lse [B, Hq, Lq]")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype == do.dtype == torch.bfloat16):
+        raise ValueError("the HIP attention backward takes bfloat16 q, k, v, o, do")
+    if Hq % Hkv:
+        raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
+    if D not in (64, 128):
+        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if not sm_scale > 0:
+        raise ValueError("sm_scale must be > 0")
+    q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))
+    lse = lse.to(torch.float32).contiguous()
+    bb = bh = 1
+    if bias is not None:
+        if bias.ndim != 4 or tuple(bias.shape[-2:]) != (Lq, Lk):
+            raise ValueError(f"bias must be [1|B, 1|H, {Lq}, {Lk}], got {tuple(bias.shape)}")
+        bb, bh = bias.shape[:2]
+        if bb not in (1, B) or bh not in (1, Hq):
+            raise ValueError(f"bias {tuple(bias.shape)} does not broadcast to B={B}, H={Hq}")
+        bias = bias.to(torch.float32).contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    lib = native.load()
+    ws = _workspace(int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq)), dev, workspace)
+    rc = lib.pjx_flash_bwd(
+        native.PJX_DTYPE_BF16, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
+        _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
+        Lq if q_valid is None else int(q_valid), Lk if kv_valid is None else int(kv_valid),
+        int(bool(causal)), float(sm_scale), _stream(dev),
+    )
+    native.check(rc)
+    return dq, dk, dv
+
+
 def decode_workspace_bytes(batch, groups, rows, kv_len, v_dim, chunk=0) -> int:
     return int(native.load().pjx_decode_workspace_size(batch, groups, rows, kv_len, v_dim, chunk))
 
