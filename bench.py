@@ -15,6 +15,9 @@ timed steps.
 The other configurations are measured the same way after the headline and
 reported under ``"configs"`` (decode and MLA as HBM GB/s of the bytes the
 algorithm must move: valid K/V + q + o; bias configs include the bias once).
+``C2B`` is the backward of the headline workload (one ``pjx_flash_bwd`` call)
+and ``C2FB`` forward + backward, both as TFLOP/s with the reference
+benchmark's FlashAttention convention (fwd+bwd = 3.5x the forward's FLOPs).
 
 ``cpu_baseline`` times the numpy restatement of probjax's XLA CPU path
 (``oracle.xla_attention``, 256x256 tiles with causal tile skipping) on one
@@ -54,7 +57,8 @@ def _parse():
     p.add_argument("--no-cpu-baseline", action="store_true",
                    help="skip the timed CPU oracle leg")
     p.add_argument("--only", default="",
-                   help="comma list of configs to run (C1..C5); default all")
+                   help="comma list of configs to run (C1..C5, C2B = backward, C2FB = "
+                        "forward+backward); default all")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (counter calibration) and exit")
     p.add_argument("--gemm-calibration", type=int, default=0, metavar="N",
@@ -193,7 +197,60 @@ def make_c5(dev, gen):
                 kernel="decode_chunk_kernel<576,8,true>")
 
 
-MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5}
+def _c2_train_inputs(dev, gen):
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 4, 4096, 16, 128
+    q, k, v, do = (_randn((B, L, H, D), gen, dev, torch.bfloat16) for _ in range(4))
+    o, lse = flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True, return_lse=True)
+    return B, L, H, D, q, k, v, do, o, lse
+
+
+def make_c2b(dev, gen):
+    """Backward of the headline forward: one pjx_flash_bwd call (dq, dk, dv).
+
+    FLOPs by the FlashAttention convention of the reference's benchmark
+    (docs/scripts/benchmark_gpu_attention.py:179-187: fwd+bwd = 3.5x fwd, so
+    bwd = 2.5x fwd); the kernels execute 3.5x fwd (S and dP are recomputed
+    for dQ)."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_bwd
+
+    B, L, H, D, q, k, v, do, o, lse = _c2_train_inputs(dev, gen)
+    ws = torch.empty(8 * B * H * L, dtype=torch.uint8, device=dev)
+    flop = 2.5 * 4 * B * H * L * L * D / 2
+    nbytes = 2 * B * L * H * D * 2 * 4 + B * H * L * 4  # q,k,v,o,do + dq,dk,dv + lse
+    fn = lambda: flash_attention_bwd(q, k, v, o, do, lse, sm_scale=1 / math.sqrt(D), causal=True,  # noqa: E731
+                                     workspace=ws)
+    return dict(name="C2 causal bwd bf16 B=4 H=16 L=4096 D=128 (dq, dk, dv)", fn=fn, flop=flop,
+                bytes=nbytes, bound="mfma", dtype="bf16",
+                kernel="flash_bwd_dq_kernel<128,false> + flash_bwd_dkdv_kernel<128,false>")
+
+
+def make_c2fb(dev, gen):
+    """Forward (with LSE) + backward, the reference benchmark's fwd_bwd mode
+    (3.5x the forward's FLOPs)."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_bwd, flash_attention_fwd
+
+    B, L, H, D, q, k, v, do, _, _ = _c2_train_inputs(dev, gen)
+    ws = torch.empty(8 * B * H * L, dtype=torch.uint8, device=dev)
+    sc = 1 / math.sqrt(D)
+
+    def fn():
+        o, lse = flash_attention_fwd(q, k, v, sm_scale=sc, causal=True, return_lse=True)
+        return flash_attention_bwd(q, k, v, o, do, lse, sm_scale=sc, causal=True, workspace=ws)
+
+    flop = 3.5 * 4 * B * H * L * L * D / 2
+    nbytes = 2 * B * L * H * D * 2 * 5 + B * H * L * 4
+    return dict(name="C2 causal fwd+bwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop,
+                bytes=nbytes, bound="mfma", dtype="bf16",
+                kernel="flash_fwd_bf16_kernel<128,false> + flash_bwd_*<128,false>")
+
+
+MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
+          "C2B": make_c2b, "C2FB": make_c2fb}
 
 
 def _settle(fn, seconds):

@@ -17,6 +17,10 @@ HIP library behind ``include/probjax_hip.h``):
 * ``mha`` -- the kernel API (pallas_kernels/kernels/attention.py:2692-2984),
   default ``sm_scale = 1.0``, split-KV decoding chosen by ``use_splitkv``
   (:2653-2689) extended to ``KVLenMask``;
+* gradients -- when q, k or v requires grad, the flash path (and the split-KV
+  primal) runs as a ``torch.autograd.Function`` whose backward is the HIP
+  backward (probjax's custom VJP of ``mha``, :3188-3266; no cotangent for
+  mask/bias data);
 * ``splitkv_forward`` -- kernels/attention_splitkv.py:137-250;
 * ``mla`` -- kernels/latent_attention.py:636-766, absorbed form (``wk = wv =
   None``), default ``sm_scale = 1/sqrt(qk_head_dim)``.
@@ -46,6 +50,7 @@ FLASH_HEAD_DIMS = (64, 128)
 DECODE_HEAD_DIMS = (64, 128)
 DECODE_MAX_ROWS = 16
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
+BACKWARD_DTYPES = (torch.bfloat16,)  # dtypes pjx_flash_bwd takes
 
 # Split-KV decode thresholds (probjax kernels/attention.py:2649-2650).
 _SPLITKV_MAX_Q_LEN = 64
@@ -174,15 +179,57 @@ def use_splitkv(q, k, *, mask=None, bias=None, dropout_rate: float = 0.0,
     return _splitkv_ok(q, k, lower_mask(mask), bias is not None, dropout_rate, split_kv)
 
 
+class _AttentionFunction(torch.autograd.Function):
+    """Differentiable HIP attention, the custom VJP of probjax's ``mha``
+    (kernels/attention.py:3188-3266): the forward keeps ``(q, k, v, out,
+    lse)`` as residuals and the backward is ``pjx_flash_bwd``.  Mask and bias
+    data get no cotangent, as in the reference (:3262-3263): the bias tensor
+    is an argument of the kernels, not an input of this function."""
+
+    @staticmethod
+    def forward(ctx, query, key, value, run_fwd, bwd_kwargs):
+        out, lse = run_fwd(query, key, value)
+        ctx.save_for_backward(query, key, value, out, lse)
+        ctx.bwd_kwargs = bwd_kwargs
+        return out
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, k, v, o, lse = ctx.saved_tensors
+        dq, dk, dv = hip.flash_attention_bwd(q, k, v, o, dout, lse, **ctx.bwd_kwargs)
+        return dq, dk, dv, None, None
+
+
+def _needs_grad(*ts) -> bool:
+    return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
+
+
 def _run(query, key, value, lm, bias_t, sm_scale, split_kv):
+    grad = _needs_grad(query, key, value)
+    if grad and query.dtype not in BACKWARD_DTYPES:
+        return None
     if _splitkv_ok(query, key, lm, bias_t is not None, 0.0, split_kv):
         plan = _decode_plan(query, key, value, lm, bias_t)
         if plan is not None:
-            return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, **plan)
+            if not grad:
+                return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, **plan)
+            # Split-KV primal, regular backward (probjax splitkv_attention,
+            # kernels/attention_splitkv.py:253-272).
+            return _AttentionFunction.apply(
+                query, key, value,
+                lambda q, k, v: hip.splitkv_decode(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
+                dict(sm_scale=sm_scale, kv_lengths=plan["kv_lengths"]),
+            )
     plan = _flash_plan(query, key, value, lm, bias_t)
     if plan is None:
         return None
-    return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, **plan)
+    if not grad:
+        return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, **plan)
+    return _AttentionFunction.apply(
+        query, key, value,
+        lambda q, k, v: hip.flash_attention_fwd(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
+        dict(sm_scale=sm_scale, **plan),
+    )
 
 
 # ---------------------------------------------------------------------------
@@ -253,6 +300,8 @@ def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
         why.append(f"bias {type(bias).__name__} is not supported")
     if getattr(q, "dtype", None) not in (torch.bfloat16, torch.float32):
         why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp32)")
+    if _needs_grad(q, k) and getattr(q, "dtype", None) not in BACKWARD_DTYPES:
+        why.append(f"gradients need {BACKWARD_DTYPES} inputs (got {getattr(q, 'dtype', None)})")
     if q.ndim == 4 and q.shape[-1] not in FLASH_HEAD_DIMS:
         why.append(f"head_dim {q.shape[-1]} is not supported {FLASH_HEAD_DIMS}")
     detail = "; ".join(why) or "unsupported shape combination"
