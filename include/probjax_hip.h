@@ -96,7 +96,8 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * rows contribute nothing); dq [B, Lq, Hq, D], dk and dv [B, Lk, Hkv, D]
  * (fully written, zeros where no valid score reaches).  workspace: at least
  * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.
- * dtype: PJX_DTYPE_BF16.  head_dim in {64, 128}.
+ * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 (all fp32 products, no roundings).
+ * head_dim in {64, 128}.
  */
 int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,

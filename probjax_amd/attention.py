@@ -50,7 +50,7 @@ FLASH_HEAD_DIMS = (64, 128)
 DECODE_HEAD_DIMS = (64, 128)
 DECODE_MAX_ROWS = 16
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
-BACKWARD_DTYPES = (torch.bfloat16,)  # dtypes pjx_flash_bwd takes
+BACKWARD_DTYPES = (torch.bfloat16, torch.float32)  # dtypes pjx_flash_bwd takes
 
 # Split-KV decode thresholds (probjax kernels/attention.py:2649-2650).
 _SPLITKV_MAX_Q_LEN = 64

@@ -1,4 +1,4 @@
-// Flash-attention backward for gfx950 (bf16 inputs, fp32 accumulation).
+// Flash-attention backward for gfx950 (bf16 or fp32 inputs, fp32 accumulation).
 //
 // Replaces the Pallas backward of probjax's `mha`:
 //   _preprocess_backward_kernel (probjax/nn/pallas_kernels/kernels/attention.py:853-867)
@@ -503,6 +503,390 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
   }
 }
 
+// ---------------------------------------------------------------------------
+// fp32 path: v_mfma_f32_32x32x2f32 (full fp32 products) for every product.
+// One MFMA step contracts two indices, one per wave half.  Products whose
+// contraction runs over the head dim take half rows (half 0: dims s, half 1:
+// dims D/2 + s) as in the fp32 forward; products whose contraction runs over
+// keys or queries take the pair (register r, half 0), (r, half 1) of a 32x32
+// C block as the two indices, so their A operand is one float of a row-major
+// tile.  Tiles are staged through registers into LDS rows padded to D + 4
+// floats (16-byte reads of 16 consecutive rows hit distinct banks).
+// ---------------------------------------------------------------------------
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  constexpr int BK = (D == 128) ? 32 : 64;
+  constexpr int KS = D + 4;
+  constexpr int DC = D / 4;
+  constexpr int PER_T = BK * DC / kThreads;
+  static_assert(PER_T >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float k_lds[2][BK * KS];
+  __shared__ __attribute__((aligned(16))) float v_lds[2][BK * KS];
+
+  const BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int col = lane & 31, half = lane >> 5;
+  const size_t kv_row = (size_t)a.Hkv * D;
+  const float* Kb = (const float*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const float* Vb = (const float*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * D;
+  const bool row_in = g.qi < a.Lq;
+  const bool row_ok = g.qi < g.q_hi;
+
+  float qf[D / 2], dof[D / 2];
+  float dsum = 0.f;
+  {
+    const size_t roff = ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D + half * (D / 2);
+    const float* qrow = (const float*)a.q + roff;
+    const float* drow = (const float*)ba.dout + roff;
+    const float* orow = (const float*)a.o + roff;
+#pragma unroll
+    for (int s = 0; s < D / 8; ++s) {
+      f32x4 rq = {0.f, 0.f, 0.f, 0.f}, rd = rq, ro = rq;
+      if (row_in) {
+        rq = *(const f32x4*)(qrow + 4 * s);
+        rd = *(const f32x4*)(drow + 4 * s);
+        ro = *(const f32x4*)(orow + 4 * s);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        qf[4 * s + j] = rq[j];
+        dof[4 * s + j] = rd[j];
+        dsum = fmaf(ro[j], rd[j], dsum);
+      }
+    }
+  }
+  const float delta = xor32_sum(dsum);
+  float lse2 = 0.f;
+  const size_t lidx = ((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi;
+  if (row_in) {
+    lse2 = a.lse[lidx] * kLog2e;
+    if (half == 0) {
+      ba.delta[lidx] = delta;
+      ba.lse2[lidx] = lse2;
+    }
+  }
+  const float* brow = nullptr;
+  if constexpr (BIAS) {
+    brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
+           (size_t)(row_in ? g.qi : 0) * a.Lk;
+  }
+  const bool bias_vec = (a.Lk & 3) == 0;
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int q_last_w = g.qw + 31;
+
+  f32x4 kreg[PER_T], vreg[PER_T];
+  auto load_tile = [&](int t) {
+    const int k0 = t * BK;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      const int kk = k0 + u / DC, dc = u % DC;
+      f32x4 rk = {0.f, 0.f, 0.f, 0.f}, rv = rk;
+      if (kk < g.kv_stop) {
+        rk = *(const f32x4*)(Kb + (size_t)kk * kv_row + dc * 4);
+        rv = *(const f32x4*)(Vb + (size_t)kk * kv_row + dc * 4);
+      }
+      kreg[i] = rk;
+      vreg[i] = rv;
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      *(f32x4*)(&k_lds[buf][(u / DC) * KS + (u % DC) * 4]) = kreg[i];
+      *(f32x4*)(&v_lds[buf][(u / DC) * KS + (u % DC) * 4]) = vreg[i];
+    }
+  };
+
+  auto compute = [&](int t, int buf) {
+    const int k0 = t * BK;
+    if (a.causal && k0 > q_last_w) return;
+    const float* kl = k_lds[buf];
+    const float* vl = v_lds[buf];
+    f32x16 s[BK / 32], dp[BK / 32];
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb) {
+      s[kb] = f32x16{};
+      dp[kb] = f32x16{};
+      const float* kp = kl + (kb * 32 + col) * KS + half * (D / 2);
+      const float* vp = vl + (kb * 32 + col) * KS + half * (D / 2);
+#pragma unroll
+      for (int st4 = 0; st4 < D / 8; ++st4) {
+        const f32x4 kf = *(const f32x4*)(kp + 4 * st4);
+        const f32x4 vf = *(const f32x4*)(vp + 4 * st4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s[kb] = mfma32x32x2f32(kf[j], qf[4 * st4 + j], s[kb]);
+          dp[kb] = mfma32x32x2f32(vf[j], dof[4 * st4 + j], dp[kb]);
+        }
+      }
+    }
+    if constexpr (BIAS) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int gq = 0; gq < 4; ++gq) {
+          const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+          for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
+        }
+    }
+    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                           (g.qw + 31 >= g.q_hi);
+    if (need_mask) {
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = k0 + kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const bool keep = row_ok && kk < g.kv_end && (!a.causal || kk <= g.qi);
+          if (!keep) s[kb][r] = -INFINITY;
+        }
+    }
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
+        s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
+      }
+    // dQ^T[d][query] += K^T dS^T: step (kb, r) contracts keys (r, half 0/1).
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int key = kb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          acc[db] = mfma32x32x2f32(kl[key * KS + db * 32 + col], s[kb][r], acc[db]);
+        }
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    compute(t, t & 1);
+    if (t + 1 < n_tiles) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  if (row_in) {
+    float* drow = (float*)ba.dq + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        f32x4 v;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) v[j] = acc[db][4 * gq + j];
+        *(f32x4*)(drow + db * 32 + 8 * gq + 4 * half) = v;
+      }
+  }
+}
+
+template <int D, bool BIAS>
+__global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  constexpr int BQ = 32;  // queries per stage (one 32-query step)
+  constexpr int KS = D + 4;
+  constexpr int DC = D / 4;
+  constexpr int PER_T = BQ * DC / kThreads;
+  static_assert(PER_T >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) float q_lds[2][BQ * KS];
+  __shared__ __attribute__((aligned(16))) float d_lds[2][BQ * KS];
+  __shared__ __attribute__((aligned(16))) float ld_lds[2][2 * BQ];  // lse*log2e, delta
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int col = lane & 31, half = lane >> 5;
+  const int BH = a.B * a.Hkv;
+  const int bh = blockIdx.x % BH;
+  const int k0 = (blockIdx.x / BH) * kBKV;
+  const int b = bh / a.Hkv, hkv = bh % a.Hkv;
+  const int G = a.Hq / a.Hkv;
+  const int kw = k0 + 32 * w;
+  const int key = kw + col;
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  const int q_hi = min(a.Lq, a.q_valid);
+  const int q_begin = a.causal ? (k0 / BQ) * BQ : 0;
+  const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + BQ - 1) / BQ : 0;
+  const int n_tiles = G * n_qt;
+
+  float kf[D / 2], vf[D / 2];
+  {
+    const bool kin = key < a.Lk;
+    const size_t koff = ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * D + half * (D / 2);
+    const float* krow = (const float*)a.k + koff;
+    const float* vrow = (const float*)a.v + koff;
+#pragma unroll
+    for (int s = 0; s < D / 8; ++s) {
+      f32x4 rk = {0.f, 0.f, 0.f, 0.f}, rv = rk;
+      if (kin) {
+        rk = *(const f32x4*)(krow + 4 * s);
+        rv = *(const f32x4*)(vrow + 4 * s);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        kf[4 * s + j] = rk[j];
+        vf[4 * s + j] = rv[j];
+      }
+    }
+  }
+  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const size_t q_row = (size_t)a.Hq * D;
+
+  f32x16 acck[D / 32], accv[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) {
+    acck[i] = f32x16{};
+    accv[i] = f32x16{};
+  }
+
+  f32x4 qreg[PER_T], dreg[PER_T];
+  float lreg = 0.f;
+  auto tile_head = [&](int t) { return hkv * G + t / n_qt; };
+  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * BQ; };
+  auto load_tile = [&](int t) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    const float* Qb = (const float*)a.q + ((size_t)b * a.Lq * a.Hq + h) * D;
+    const float* Db = (const float*)ba.dout + ((size_t)b * a.Lq * a.Hq + h) * D;
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      const int qq = q0 + u / DC, dc = u % DC;
+      f32x4 rq = {0.f, 0.f, 0.f, 0.f}, rd = rq;
+      if (qq < a.Lq) {
+        rq = *(const f32x4*)(Qb + (size_t)qq * q_row + dc * 4);
+        rd = *(const f32x4*)(Db + (size_t)qq * q_row + dc * 4);
+      }
+      qreg[i] = rq;
+      dreg[i] = rd;
+    }
+    lreg = 0.f;
+    if (tid < 2 * BQ) {
+      const int qq = q0 + (tid % BQ);
+      const size_t li = ((size_t)b * a.Hq + h) * a.Lq + qq;
+      if (qq < a.Lq) lreg = tid < BQ ? ba.lse2[li] : ba.delta[li];
+    }
+  };
+  auto store_tile = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < PER_T; ++i) {
+      const int u = tid + kThreads * i;
+      *(f32x4*)(&q_lds[buf][(u / DC) * KS + (u % DC) * 4]) = qreg[i];
+      *(f32x4*)(&d_lds[buf][(u / DC) * KS + (u % DC) * 4]) = dreg[i];
+    }
+    if (tid < 2 * BQ) ld_lds[buf][tid] = lreg;
+  };
+
+  auto compute = [&](int t, int buf) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    if (q0 >= q_hi || kw >= kv_end) return;
+    if (a.causal && q0 + BQ - 1 < kw) return;  // every query before this wave's first key
+    const float* ql = q_lds[buf];
+    const float* dl = d_lds[buf];
+    const float* lsm = ld_lds[buf];
+    // S[query][key] = Q K^T and dP = dO V^T; register r holds query
+    // q0 + 8*(r/4) + 4*half + r%4 of key `key`.
+    f32x16 s = f32x16{}, dp = f32x16{};
+    {
+      const float* qp = ql + col * KS + half * (D / 2);
+      const float* dpp = dl + col * KS + half * (D / 2);
+#pragma unroll
+      for (int st4 = 0; st4 < D / 8; ++st4) {
+        const f32x4 qv = *(const f32x4*)(qp + 4 * st4);
+        const f32x4 dv4 = *(const f32x4*)(dpp + 4 * st4);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          s = mfma32x32x2f32(qv[j], kf[4 * st4 + j], s);
+          dp = mfma32x32x2f32(dv4[j], vf[4 * st4 + j], dp);
+        }
+      }
+    }
+    if constexpr (BIAS) {
+      const float* bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = q0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const float bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
+        s[r] = fmaf(s[r], a.scale, bv);
+      }
+    }
+    const bool need_mask = (a.causal && q0 < kw + 31) || (kw + 32 > kv_end) || (q0 + BQ > q_hi);
+    if (need_mask) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qr = q0 + 8 * (r >> 2) + 4 * half + (r & 3);
+        const bool keep = key < kv_end && qr < q_hi && (!a.causal || qr >= key);
+        if (!keep) s[r] = -INFINITY;
+      }
+    }
+    f32x16 ds;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
+      const float p = fast_exp2(fmaf(s[r], cx, -lsm[qi]));
+      s[r] = p;
+      ds[r] = p * (dp[r] - lsm[BQ + qi]) * a.scale;
+    }
+    // dV^T[d][key] += dO^T P and dK^T[d][key] += Q^T dS: step r contracts
+    // queries (r, half 0/1).
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
+        accv[db] = mfma32x32x2f32(dl[qi * KS + db * 32 + col], s[r], accv[db]);
+        acck[db] = mfma32x32x2f32(ql[qi * KS + db * 32 + col], ds[r], acck[db]);
+      }
+  };
+
+  if (n_tiles > 0) {
+    load_tile(0);
+    store_tile(0);
+  }
+  __syncthreads();
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 1 < n_tiles) load_tile(t + 1);
+    compute(t, t & 1);
+    if (t + 1 < n_tiles) store_tile((t + 1) & 1);
+    __syncthreads();
+  }
+
+  if (key < a.Lk) {
+    const size_t koff = ((size_t)(b * a.Lk + key) * a.Hkv + hkv) * D;
+    float* dkrow = (float*)ba.dk + koff;
+    float* dvrow = (float*)ba.dv + koff;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        f32x4 vk, vv;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          vk[j] = acck[db][4 * gq + j];
+          vv[j] = accv[db][4 * gq + j];
+        }
+        *(f32x4*)(dkrow + db * 32 + 8 * gq + 4 * half) = vk;
+        *(f32x4*)(dvrow + db * 32 + 8 * gq + 4 * half) = vv;
+      }
+  }
+}
+
 template <typename K>
 static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
   const long blocks = (long)a.f.n_qtiles * a.f.B * a.f.Hq;
@@ -520,12 +904,19 @@ static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
 // dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
 // dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
 template <int D>
-static int run_bwd(const FlashBwdArgs& a, bool hb, hipStream_t s) {
+static int run_bwd(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
-    const int rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false>, a, s);
+    int rc;
+    if (f32)
+      rc = hb ? launch_dq(flash_bwd_dq_f32_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_f32_kernel<D, false>, a, s);
+    else
+      rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false>, a, s);
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
+  if (f32)
+    return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true>, a, s)
+              : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false>, a, s);
   return hb ? launch_dkdv(flash_bwd_dkdv_kernel<D, true>, a, s) : launch_dkdv(flash_bwd_dkdv_kernel<D, false>, a, s);
 }
 
@@ -546,8 +937,8 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
                              int64_t kv_heads, int64_t head_dim, int64_t q_valid, int64_t kv_valid,
                              int causal, float sm_scale, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16)
-    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q, k, v, o, dout, lse, dq, dk, dv must be non-null");
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
@@ -561,7 +952,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
   const int64_t elems = std::max(batch * q_len * q_heads, batch * kv_len * kv_heads) * head_dim;
   if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30) ||
-      (int64_t)q_heads * head_dim * 2 * 64 > 0xffffffffLL)
+      (int64_t)q_heads * head_dim * 4 * 64 > 0xffffffffLL)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sizes out of range");
   if (batch == 0 || (q_len == 0 && kv_len == 0)) return PJX_OK;
   const size_t need = pjx_flash_bwd_workspace_size(batch, q_heads, q_len);
@@ -591,5 +982,6 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
-  return head_dim == 128 ? run_bwd<128>(ba, hb, s) : run_bwd<64>(ba, hb, s);
+  const bool f32 = dtype == PJX_DTYPE_F32;
+  return head_dim == 128 ? run_bwd<128>(ba, f32, hb, s) : run_bwd<64>(ba, f32, hb, s);
 }

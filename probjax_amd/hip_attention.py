@@ -110,7 +110,7 @@ def flash_attention_bwd(
     """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``.
 
     ``o`` and ``lse`` are the forward's output and natural-log LSE; ``do`` the
-    output gradient.  Masks, bias and scale must be the forward's.  bf16 only.
+    output gradient.  Masks, bias and scale must be the forward's.  bf16 or fp32.
     """
     dev = _on_device(q, k, v, o, do, lse, bias)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -121,8 +121,9 @@ def flash_attention_bwd(
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}, v {tuple(v.shape)}")
     if o.shape != q.shape or do.shape != q.shape or tuple(lse.shape) != (B, Hq, Lq):
         raise ValueError("o and do must be shaped like q and lse [B, Hq, Lq]")
-    if not (q.dtype == k.dtype == v.dtype == o.dtype == do.dtype == torch.bfloat16):
-        raise ValueError("the HIP attention backward takes bfloat16 q, k, v, o, do")
+    if not (q.dtype == k.dtype == v.dtype == o.dtype == do.dtype):
+        raise ValueError("q, k, v, o, do must share a dtype")
+    code = _dtype_code(q)
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
     if D not in (64, 128):
@@ -144,7 +145,7 @@ def flash_attention_bwd(
     lib = native.load()
     ws = _workspace(int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq)), dev, workspace)
     rc = lib.pjx_flash_bwd(
-        native.PJX_DTYPE_BF16, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
+        code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
         _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
         Lq if q_valid is None else int(q_valid), Lk if kv_valid is None else int(kv_valid),
         int(bool(causal)), float(sm_scale), _stream(dev),

@@ -115,3 +115,24 @@ def test_no_grad_inputs_take_the_plain_forward(device):
     out2 = A.flex_attention(tq, k, v, mask=CausalMask())
     assert out2.grad_fn is not None
     assert torch.equal(out, out2.detach())
+
+
+def test_config1_f32_grad(device):
+    """Config 1 (fp32 causal 1x512x4x64) through flex_attention with gradients,
+    against the float64 oracle: max-abs <= 1e-5 * max(1, max|ref|)."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd.masks import CausalMask
+
+    q, k, v, do = rng_normal(35, (1, 512, 4, 64), (1, 512, 4, 64), (1, 512, 4, 64), (1, 512, 4, 64))
+    tq, tk, tv = (to_dev(x, device, torch.float32).requires_grad_(True) for x in (q, k, v))
+    out = A.flex_attention(tq, tk, tv, mask=CausalMask())
+    (out * to_dev(do, device, torch.float32)).sum().backward()
+    o, lse = oracle.xla_attention(q, k, v, mask=oracle.CausalMask(), sm_scale=1 / 8, strategy="dense",
+                                  compute_dtype=np.float64, return_lse=True)
+    assert float(np.max(np.abs(to_np(out) - o))) <= 1e-5
+    want = attention_backward(q, k, v, o, do, lse, mask=oracle.CausalMask(), sm_scale=1 / 8,
+                              compute_dtype=np.float64)
+    for name, t, w in (("dq", tq, want[0]), ("dk", tk, want[1]), ("dv", tv, want[2])):
+        err = float(np.max(np.abs(to_np(t.grad).astype(np.float64) - w)))
+        assert err <= 1e-5 * max(1.0, float(np.max(np.abs(w)))), f"{name}: {err:.3e}"

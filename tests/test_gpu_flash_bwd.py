@@ -116,3 +116,46 @@ def test_flash_bwd_static_lengths(device):
         _check(to_np(g), w, name)
     assert torch.count_nonzero(got[0][:, qv:]) == 0
     assert torch.count_nonzero(got[1][:, kvv:]) == 0 and torch.count_nonzero(got[2][:, kvv:]) == 0
+
+
+F32_CASES = [
+    # B, Lq, Lk, Hq, Hkv, D, causal, lengths, bias_shape
+    (1, 512, 512, 4, 4, 64, True, None, None),          # config 1's shape
+    (2, 300, 300, 4, 2, 128, True, None, None),         # GQA, partial tiles
+    (2, 200, 333, 4, 1, 64, False, [333, 0], (2, 1)),   # per-batch bias, empty batch, Lq != Lk
+    (1, 160, 160, 2, 2, 128, False, [100], (1, 2)),
+]
+
+
+@pytest.mark.parametrize("B,Lq,Lk,Hq,Hkv,D,causal,lengths,bias_shape", F32_CASES)
+def test_flash_bwd_f32_matches_float64_oracle(device, B, Lq, Lk, Hq, Hkv, D, causal, lengths, bias_shape):
+    """fp32 gradients against the float64 oracle: max-abs <= 1e-5 * max(1, max|ref|)
+    (the fp32 bar of 1e-5, scaled by the gradients' magnitude; the fp32 oracle
+    itself sits ~2e-6 from float64 on these shapes)."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_bwd
+
+    print(f"case f32 B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D} causal={causal} "
+          f"lengths={lengths} bias={bias_shape}", flush=True)
+    q, k, v, do = rng_normal(40, (B, Lq, Hq, D), (B, Lk, Hkv, D), (B, Lk, Hkv, D), (B, Lq, Hq, D))
+    bias = None if bias_shape is None else rng_normal(41, (*bias_shape, Lq, Lk), scale=0.5)[0]
+    scale = 1.0 / math.sqrt(D)
+    mask = _mask(causal, lengths)
+    db = oracle.DenseBias(bias) if bias is not None else None
+    o, lse = oracle.xla_attention(q, k, v, mask=mask, bias=db, sm_scale=scale, strategy="dense",
+                                  compute_dtype=np.float64, return_lse=True)
+    want = attention_backward(q, k, v, o, do, lse, mask=mask, bias=db, sm_scale=scale,
+                              compute_dtype=np.float64)
+    f = torch.float32
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    bt = None if bias is None else torch.from_numpy(bias).to(device)
+    got = flash_attention_bwd(
+        to_dev(q, device, f), to_dev(k, device, f), to_dev(v, device, f), to_dev(o, device, f),
+        to_dev(do, device, f), torch.from_numpy(lse).to(device), sm_scale=scale, causal=causal,
+        kv_lengths=L, bias=bt,
+    )
+    torch.cuda.synchronize()
+    for name, g, w in zip(("dq", "dk", "dv"), got, want):
+        tol = 1e-5 * max(1.0, float(np.max(np.abs(w))))
+        err = float(np.max(np.abs(to_np(g).astype(np.float64) - w)))
+        assert err <= tol, f"{name}: max err {err:.3e} > {tol:.3e}"
