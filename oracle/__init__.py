@@ -17,13 +17,28 @@ Pinning status of each function is recorded in the module docstrings
 
 from .bf16 import round_bf16  # noqa: F401
 from .masks import (  # noqa: F401
+    BlockDiagonalCausalMask,
+    BlockDiagonalMask,
+    CausalAlibiBias,
+    CausalFromBottomRightMask,
+    CausalLocalWindowMask,
     CausalMask,
     ComposeMask,
+    ConstantBias,
     DenseBias,
+    DistanceDecayBias,
+    IdentityBias,
     KVLenMask,
+    LocalWindowMask,
     NoMask,
+    PerHeadScaleBias,
+    PrefixLMMask,
     QKVLengthMask,
+    SameSegmentMask,
+    SeqLenMask,
+    SoftCappingBias,
     SumBias,
+    SymmetricAlibiBias,
 )
 from .attention_xla import auto_strategy, xla_attention  # noqa: F401
 from .splitkv import default_num_splits, splitkv_forward  # noqa: F401

@@ -20,7 +20,9 @@ Follows ``probjax/nn/pallas_kernels/kernels/attention.py``:
   - GQA: per-query-head ``dk``/``dv`` in the input dtype, summed over each KV
     head's group in fp32 and cast (``_sum_gqa_group`` ``:2123-2128``);
   - the dense bias gets no cotangent (the custom VJP returns zeros for the
-    bias leaves, ``:3262-3263``).
+    bias leaves, ``:3262-3263``);
+  - score modifiers (soft capping, per-head scale) multiply ``ds`` by their
+    derivative at the pre-bias score (``:1051-1056``; ``grad_tile``).
 
 Rows without a valid key: the forward's natural-log LSE is ``+inf`` there
 (the XLA path's convention, ``attention_xla.py:420``), so ``p = 0`` and such
@@ -99,7 +101,9 @@ def attention_backward(
             s = qb @ kb.T
             if sm_scale != 1.0:
                 s = s * cdt(sm_scale)
+            gf = None
             if bias is not None:
+                gf = bias.grad_tile(s, b, h, 0, Lq, 0, Lk)
                 s = bias.tile_add(s, b, h, 0, Lq, 0, Lk).astype(cdt, copy=False)
             if keep is not None:
                 s = np.where(keep, s, -np.inf).astype(cdt, copy=False)
@@ -108,6 +112,8 @@ def attention_backward(
             ds = p * (dp - delta[b, h][:, None])
             if sm_scale != 1.0:
                 ds = ds * cdt(sm_scale)
+            if gf is not None:
+                ds = ds * np.asarray(gf, cdt)  # score-modifier derivative (:1051-1056)
             pc = round_bf16(p).astype(cdt) if bf16 else p
             dsc = round_bf16(ds).astype(cdt) if bf16 else ds
             dv_h[b, :, h] = pc.T @ dob

@@ -13,16 +13,29 @@ the hot path uses:
   ``:456-497``; at most one stateful child ``:359-371``)
 * ``DenseBias``      -- ``:1807-1922`` (``scores + data``; ``[B|1, H|1, Q, K]``
   broadcast over size-1 batch/head, block index map ``:1849-1858``)
-* ``SumBias``        -- ``:551-577`` (sum of additive deltas)
+* ``SumBias``        -- ``:551-577`` (sum of additive deltas; derivative 1)
+* positional masks   -- ``LocalWindowMask`` ``:651-704``, ``CausalLocalWindowMask``
+  ``:707-750``, ``CausalFromBottomRightMask`` ``:753-782``, ``PrefixLMMask``
+  ``:785-868``, ``SeqLenMask`` ``:1239-1398``
+* segment masks      -- ``SameSegmentMask`` ``:1537-1668``, ``BlockDiagonalMask``
+  ``:871-981``, ``BlockDiagonalCausalMask`` ``:984-1076``
+* score modifiers    -- ``IdentityBias`` ``:2201-2220``, ``ConstantBias``
+  ``:1781-1805``, ``CausalAlibiBias`` / ``SymmetricAlibiBias`` (slope
+  ``2^-(h+1)``, ``:2223-2255, 2355-2380``), ``DistanceDecayBias``
+  ``:2387-2414``, ``SoftCappingBias`` ``:2564-2603`` and ``PerHeadScaleBias``
+  ``:2606-2648`` with their score derivatives (``grad_tile``)
 
 The XLA reference evaluates a mask per ``(batch, head)`` on index tiles with
 its payload sliced per batch (``attention_xla.py:227-279``); ``tile_keep``
 below is that evaluation for one batch element, ``tile_add`` the bias one.
 
 Parity pinned by the reference's own known-answer tests, restated in
-``tests/test_oracle_masks.py`` (``tests/test_attention_mask_bias.py:54-68,
-130-163, 263-294`` in the reference) and by the equivalence
+``tests/test_oracle_masks.py`` (``tests/test_attention_mask_bias.py:54-209,
+263-365`` in the reference) and by the equivalence
 KVLenMask(L) == boolean key mask ``arange(S) < L`` == additive -inf bias.
+``PerHeadScaleBias``'s derivative is the modifier's own (``scales[h]``), the
+gradient of the XLA path; the Pallas kernels call ``grad`` with the batch
+index in the head slot (``kernels/attention.py:1051-1056``).
 """
 
 from __future__ import annotations
@@ -156,6 +169,140 @@ class KVLenMask(AttentionMask):
         return None
 
 
+class LocalWindowMask(AttentionMask):
+    """attention_mask_bias.py:651-704: ``-right <= q - k <= left`` (right None -> 0)."""
+
+    def __init__(self, left_window: int, right_window=None):
+        self.left_window = int(left_window)
+        self.right_window = right_window
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        d = np.asarray(q_idx)[:, None] - np.asarray(k_idx)[None, :]
+        rw = 0 if self.right_window is None else int(self.right_window)
+        return (d >= -rw) & (d <= self.left_window)
+
+
+class CausalLocalWindowMask(AttentionMask):
+    """:707-750: ``0 <= q - k <= left``."""
+
+    def __init__(self, left_window: int):
+        self.left_window = int(left_window)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        d = np.asarray(q_idx)[:, None] - np.asarray(k_idx)[None, :]
+        return (d >= 0) & (d <= self.left_window)
+
+
+class CausalFromBottomRightMask(AttentionMask):
+    """:753-782: ``q + (kv_length - q_length) >= k``."""
+
+    def __init__(self, q_length: int, kv_length: int):
+        self.q_length, self.kv_length = int(q_length), int(kv_length)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        shift = self.kv_length - self.q_length
+        return (np.asarray(q_idx)[:, None] + shift) >= np.asarray(k_idx)[None, :]
+
+
+class PrefixLMMask(AttentionMask):
+    """:785-868: ``(k < P) | (q >= k)``; ``prefix_lengths`` a scalar or ``[B]``
+    (the kernel reads one value per batch element)."""
+
+    stateful = True
+
+    def block_mask(self, q_len, kv_len, block_q, block_k):
+        return None  # per-batch data: no static tile map
+
+    def __init__(self, prefix_lengths):
+        self.prefix_lengths = np.asarray(prefix_lengths, dtype=np.int32)
+
+    def _p(self, b):
+        p = self.prefix_lengths
+        return int(p) if p.ndim == 0 else int(p.reshape(-1)[b])
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        p = self._p(0) if seg_q is None else int(np.asarray(seg_q).reshape(-1)[0])
+        q_idx, k_idx = np.asarray(q_idx), np.asarray(k_idx)
+        return (k_idx[None, :] < p) | (q_idx[:, None] >= k_idx[None, :])
+
+    def tile_keep(self, b, span_q, span_k):
+        return self(span_q, span_k, np.int32(self._p(b)))
+
+
+class SeqLenMask(AttentionMask):
+    """:1239-1398: inside the valid length ``L[b]`` full attention, outside it
+    only the diagonal: ``(q < L & k < L) | (q == k)``."""
+
+    stateful = True
+
+    def block_mask(self, q_len, kv_len, block_q, block_k):
+        return None  # per-batch data: no static tile map
+
+    def __init__(self, seq_lengths):
+        self.seq_lengths = np.asarray(seq_lengths, dtype=np.int32).reshape(-1)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        L = int(self.seq_lengths[0]) if seg_q is None else int(np.asarray(seg_q).reshape(-1)[0])
+        q_idx, k_idx = np.asarray(q_idx), np.asarray(k_idx)
+        rect = (q_idx[:, None] < L) & (k_idx[None, :] < L)
+        return rect | (q_idx[:, None] == k_idx[None, :])
+
+    def tile_keep(self, b, span_q, span_k):
+        return self(span_q, span_k, np.int32(self.seq_lengths[b]))
+
+
+class SameSegmentMask(AttentionMask):
+    """:1537-1668: ``seg_q[q] == seg_k[k]``; ids ``[B, L]`` or shared ``[L]``;
+    keys use the query ids when ``key_segment_ids`` is None."""
+
+    stateful = True
+
+    def block_mask(self, q_len, kv_len, block_q, block_k):
+        return None  # per-batch data: no static tile map
+
+    def __init__(self, query_segment_ids, key_segment_ids=None):
+        self.query_segment_ids = np.asarray(query_segment_ids, dtype=np.int32)
+        self.key_segment_ids = None if key_segment_ids is None else np.asarray(key_segment_ids, np.int32)
+
+    @staticmethod
+    def _row(ids, b):
+        return ids if ids.ndim == 1 else ids[b]
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        sq = self.query_segment_ids if seg_q is None else np.asarray(seg_q)
+        kids = self.key_segment_ids if self.key_segment_ids is not None else self.query_segment_ids
+        sk = kids if seg_k is None else np.asarray(seg_k)
+        return sq[..., :, None] == sk[..., None, :]
+
+    def tile_keep(self, b, span_q, span_k):
+        kids = self.key_segment_ids if self.key_segment_ids is not None else self.query_segment_ids
+        sq = self._row(self.query_segment_ids, b)[np.asarray(span_q)]
+        sk = self._row(kids, b)[np.asarray(span_k)]
+        return sq[:, None] == sk[None, :]
+
+
+class BlockDiagonalMask(SameSegmentMask):
+    """:871-981: same block id (the ids are segment ids)."""
+
+    def __init__(self, query_block_ids, key_block_ids=None):
+        super().__init__(query_block_ids, key_block_ids)
+
+
+class BlockDiagonalCausalMask(SameSegmentMask):
+    """:984-1076: same block id and ``q >= k``."""
+
+    def __init__(self, query_block_ids, key_block_ids=None):
+        super().__init__(query_block_ids, key_block_ids)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        same = super().__call__(q_idx, k_idx, seg_q, seg_k)
+        return same & (np.asarray(q_idx)[:, None] >= np.asarray(k_idx)[None, :])
+
+    def tile_keep(self, b, span_q, span_k):
+        same = super().tile_keep(b, span_q, span_k)
+        return same & (np.asarray(span_q)[:, None] >= np.asarray(span_k)[None, :])
+
+
 class ComposeMask(AttentionMask):
     def __init__(self, op: str, lhs: AttentionMask, rhs: AttentionMask):
         if op not in ("and", "or", "xor"):
@@ -207,7 +354,13 @@ class AttentionBias:
         return SumBias(self, other)
 
     def tile_add(self, scores, b, h, q0, bq, k0, kc):
-        raise NotImplementedError  # pragma: no cover
+        """The bias evaluated on one score tile (attention_xla.py:227-246)."""
+        return self(scores, h, np.arange(q0, q0 + bq), np.arange(k0, k0 + kc))
+
+    def grad_tile(self, scores, b, h, q0, bq, k0, kc):
+        """d(modified score)/d(score) on a tile: 1 for additive biases
+        (attention_mask_bias.py:286-298)."""
+        return np.ones_like(scores)
 
 
 class DenseBias(AttentionBias):
@@ -253,6 +406,98 @@ class DenseBias(AttentionBias):
         if b.shape[1] not in (1, num_heads):
             raise ValueError(f"Cannot broadcast bias head dim {b.shape[1]} to {num_heads}")
         return np.broadcast_to(b, (batch_size, num_heads, q_len, kv_len))
+
+
+class IdentityBias(AttentionBias):
+    """attention_mask_bias.py:2201-2227."""
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        return scores
+
+
+class ConstantBias(AttentionBias):
+    """:1781-1805: ``scores + value``."""
+
+    def __init__(self, value: float):
+        self.value = float(value)
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        return scores + np.float32(self.value)
+
+
+def alibi_slope(h: int) -> float:
+    """:2223-2227: ``2^-(h+1)``."""
+    return float(2.0 ** (-(int(h) + 1.0)))
+
+
+class CausalAlibiBias(AttentionBias):
+    """:2230-2255: ``scores - slope(h) * relu(q - k)``."""
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        d = np.maximum(np.asarray(q_idx)[:, None] - np.asarray(k_idx)[None, :], 0)
+        return scores - np.float32(alibi_slope(h_idx)) * d.astype(np.float32)
+
+
+class SymmetricAlibiBias(AttentionBias):
+    """:2355-2380: ``scores - slope(h) * |q - k|``."""
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        d = np.abs(np.asarray(q_idx)[:, None] - np.asarray(k_idx)[None, :])
+        return scores - np.float32(alibi_slope(h_idx)) * d.astype(np.float32)
+
+
+class DistanceDecayBias(AttentionBias):
+    """:2387-2414: ``scores - alpha * |q - k|``."""
+
+    def __init__(self, alpha: float = 1.0):
+        self.alpha = float(alpha)
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        d = np.abs(np.asarray(q_idx)[:, None] - np.asarray(k_idx)[None, :]).astype(np.float32)
+        return scores - np.float32(self.alpha) * d
+
+
+class SoftCappingBias(AttentionBias):
+    """:2564-2603: ``softcap * tanh(scores / softcap)``; grad ``1 - tanh^2``."""
+
+    def __init__(self, softcap: float = 20.0):
+        if softcap <= 0:
+            raise ValueError("softcap must be > 0")
+        self.softcap = float(softcap)
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        c = np.asarray(self.softcap, dtype=np.asarray(scores).dtype)
+        return c * np.tanh(scores / c)
+
+    def grad(self, scores, h_idx=None, q_idx=None, k_idx=None, data=None):
+        c = np.asarray(self.softcap, dtype=np.asarray(scores).dtype)
+        t = np.tanh(scores / c)
+        return 1.0 - t * t
+
+    def grad_tile(self, scores, b, h, q0, bq, k0, kc):
+        return self.grad(scores)
+
+
+class PerHeadScaleBias(AttentionBias):
+    """:2606-2648: ``scores * scales[h|0]``; grad ``scales[h|0]``."""
+
+    def __init__(self, scales):
+        s = np.asarray(scales, dtype=np.float32)
+        if s.ndim == 0:
+            s = s[None]
+        if s.ndim != 1:
+            raise ValueError("scales must be shape [H|1]")
+        self.scales = s
+
+    def _scale(self, h):
+        return self.scales[0 if self.scales.shape[0] == 1 else int(h)]
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        return scores * np.asarray(self._scale(h_idx), dtype=np.asarray(scores).dtype)
+
+    def grad_tile(self, scores, b, h, q0, bq, k0, kc):
+        # The modifier's derivative at head h (the XLA path's autodiff).
+        return np.full_like(scores, self._scale(h))
 
 
 class SumBias(AttentionBias):

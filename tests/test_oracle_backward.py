@@ -203,3 +203,54 @@ def test_bf16_within_reference_gradient_tolerance():
     # and the bf16 casts are really applied (not a relabelled fp32 run)
     assert any(np.max(np.abs(a - b)) > 0 for a, b in zip(g16, g32))
     assert all(np.array_equal(x, oracle.round_bf16(x)) for x in g16)
+
+
+@pytest.mark.parametrize("kind", ["softcap", "headscale", "alibi", "window", "segments", "prefix"])
+def test_backward_with_score_modifiers_and_masks_matches_torch(kind):
+    """The oracle's modifier derivatives and extended masks against torch
+    float64 autograd of the same modified-score attention."""
+    B, L, Hq, Hkv, D = 2, 10, 4, 2, 6
+    q, k, v, do = rng_normal(7, (B, L, Hq, D), (B, L, Hkv, D), (B, L, Hkv, D), (B, L, Hq, D))
+    scale = 0.5
+    mask = bias = None
+    G = Hq // Hkv
+    t = lambda x: torch.from_numpy(np.asarray(x, np.float64)).requires_grad_(True)  # noqa: E731
+    tq, tk, tv = t(q), t(k), t(v)
+    s = torch.einsum("bqhd,bkhd->bhqk", tq, tk.repeat_interleave(G, 2)) * scale
+    qi = torch.arange(L)[:, None]
+    ki = torch.arange(L)[None, :]
+    keep = torch.ones(B, 1, L, L, dtype=torch.bool)
+    if kind == "softcap":
+        bias = oracle.SoftCappingBias(1.5)
+        s = 1.5 * torch.tanh(s / 1.5)
+    elif kind == "headscale":
+        sc = np.array([0.5, 2.0, 1.0, 3.0], np.float32)
+        bias = oracle.PerHeadScaleBias(sc)
+        s = s * torch.from_numpy(sc.astype(np.float64))[None, :, None, None]
+    elif kind == "alibi":
+        bias = oracle.SymmetricAlibiBias() + oracle.ConstantBias(0.25)
+        slopes = torch.tensor([2.0 ** -(h + 1) for h in range(Hq)], dtype=torch.float64)
+        s = s - slopes[None, :, None, None] * (qi - ki).abs() + 0.25
+    elif kind == "window":
+        mask = oracle.LocalWindowMask(3, 1) & oracle.CausalFromBottomRightMask(L, L)
+        keep = keep & (((qi - ki) >= -1) & ((qi - ki) <= 3) & (qi >= ki))
+    elif kind == "segments":
+        ids = np.array([[0] * 4 + [1] * 6, [0] * 7 + [1] * 3], np.int32)
+        mask = oracle.SameSegmentMask(ids)
+        tid = torch.from_numpy(ids)
+        keep = keep & (tid[:, None, :, None] == tid[:, None, None, :])
+    elif kind == "prefix":
+        pl = np.array([3, 0], np.int32)
+        mask = oracle.PrefixLMMask(pl)
+        keep = keep & ((ki[None, None] < torch.from_numpy(pl)[:, None, None, None]) | (qi >= ki))
+    s = s.masked_fill(~keep, -math.inf)
+    p = torch.softmax(s, -1)
+    o = torch.einsum("bhqk,bkhd->bqhd", p, tv.repeat_interleave(G, 2))
+    o.backward(torch.from_numpy(np.asarray(do, np.float64)))
+    o_np, lse = oracle.xla_attention(q, k, v, mask=mask, bias=bias, sm_scale=scale, strategy="dense",
+                                     compute_dtype=np.float64, return_lse=True)
+    np.testing.assert_allclose(o_np, o.detach().numpy(), atol=1e-6)
+    got = attention_backward(q, k, v, o_np, do, lse, mask=mask, bias=bias, sm_scale=scale,
+                             compute_dtype=np.float64)
+    for g, w in zip(got, (tq.grad, tk.grad, tv.grad)):
+        np.testing.assert_allclose(g, w.numpy(), atol=2e-5, rtol=1e-5)

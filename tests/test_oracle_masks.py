@@ -135,3 +135,109 @@ def test_block_mask_matches_dense_nonempty_blocks(mask, q_len, kv_len, bq, bk):
     # the generic (evaluate every tile) fallback agrees
     np.testing.assert_array_equal(AttentionMask.block_mask(mask, q_len, kv_len, bq, bk),
                                   _block_from_dense(dense, bq, bk))
+
+
+# ---------------------------------------------------------------------------
+# Positional / segment masks and score modifiers (restated from the
+# reference's tests/test_attention_mask_bias.py:70-173, 296-365).
+# ---------------------------------------------------------------------------
+
+def test_local_window_band_and_right_none():
+    d = _idx(8)[:, None] - _idx(8)[None, :]
+    got = oracle.LocalWindowMask(left_window=2, right_window=1)(_idx(8), _idx(8))
+    np.testing.assert_array_equal(got, (d >= -1) & (d <= 2))
+    np.testing.assert_array_equal(oracle.LocalWindowMask(3, None)(_idx(8), _idx(8)),
+                                  oracle.LocalWindowMask(3, 0)(_idx(8), _idx(8)))
+
+
+def test_causal_local_window_band():
+    d = _idx(8)[:, None] - _idx(8)[None, :]
+    got = oracle.CausalLocalWindowMask(left_window=3)(_idx(8), _idx(8))
+    np.testing.assert_array_equal(got, (d >= 0) & (d <= 3))
+
+
+def test_causal_from_bottom_right_alignment():
+    got = oracle.CausalFromBottomRightMask(q_length=3, kv_length=5)(_idx(3), _idx(5))
+    np.testing.assert_array_equal(got, (_idx(3)[:, None] + 2) >= _idx(5)[None, :])
+    # last query row sees every key
+    assert got[-1].all() and got[0].sum() == 3
+
+
+def test_prefix_lm_scalar_and_per_batch():
+    got = oracle.PrefixLMMask(np.int32(2))(_idx(6), _idx(6))
+    want = (_idx(6)[None, :] < 2) | (_idx(6)[:, None] >= _idx(6)[None, :])
+    np.testing.assert_array_equal(got, want)
+    m = oracle.PrefixLMMask(np.array([1, 4], np.int32))
+    np.testing.assert_array_equal(m.tile_keep(1, _idx(6), _idx(6)),
+                                  (_idx(6)[None, :] < 4) | (_idx(6)[:, None] >= _idx(6)[None, :]))
+    assert m.block_mask(6, 6, 2, 2) is None
+
+
+def test_block_diagonal_masks():
+    q_ids = np.array([0, 0, 1, 1, 2], np.int32)
+    k_ids = np.array([0, 1, 1, 2], np.int32)
+    diag = oracle.BlockDiagonalMask(q_ids, k_ids)(_idx(5), _idx(4))
+    np.testing.assert_array_equal(diag, q_ids[:, None] == k_ids[None, :])
+    causal = oracle.BlockDiagonalCausalMask(q_ids, k_ids)(_idx(5), _idx(4))
+    np.testing.assert_array_equal(causal, (q_ids[:, None] == k_ids[None, :])
+                                  & (_idx(5)[:, None] >= _idx(4)[None, :]))
+
+
+def test_seq_len_dense():
+    lengths = np.array([2, 4, 6], np.int32)
+    m = oracle.SeqLenMask(lengths)
+    for b, L in enumerate(lengths):
+        valid = _idx(6) < L
+        want = (valid[:, None] & valid[None, :]) | np.eye(6, dtype=bool)
+        np.testing.assert_array_equal(m.tile_keep(b, _idx(6), _idx(6)), want)
+
+
+def test_same_segment_ids():
+    q_ids = np.array([0, 1, 1, 2], np.int32)
+    k_ids = np.array([1, 0, 2, 1, 2], np.int32)
+    got = oracle.SameSegmentMask(q_ids, k_ids)(_idx(4), _idx(5))
+    np.testing.assert_array_equal(got, q_ids[:, None] == k_ids[None, :])
+    # per-batch ids, keys default to the query ids
+    ids = np.array([[0, 0, 1, 1], [0, 1, 1, 1]], np.int32)
+    m = oracle.SameSegmentMask(ids)
+    np.testing.assert_array_equal(m.tile_keep(1, _idx(4), _idx(4)), ids[1][:, None] == ids[1][None, :])
+
+
+def test_bias_value_formulas():
+    scores = np.zeros((4, 4), np.float32)
+    h = 1
+    slope = 2.0 ** (-(h + 1))
+    d = _idx(4)[:, None] - _idx(4)[None, :]
+    np.testing.assert_allclose(oracle.CausalAlibiBias()(scores, h, _idx(4), _idx(4)),
+                               -slope * np.maximum(d, 0))
+    np.testing.assert_allclose(oracle.SymmetricAlibiBias()(scores, h, _idx(4), _idx(4)),
+                               -slope * np.abs(d))
+    np.testing.assert_allclose(oracle.DistanceDecayBias(alpha=0.7)(scores, h, _idx(4), _idx(4)),
+                               -0.7 * np.abs(d), rtol=1e-6)
+    np.testing.assert_array_equal(oracle.IdentityBias()(scores, h, _idx(4), _idx(4)), scores)
+    np.testing.assert_allclose(oracle.ConstantBias(0.3)(scores, h, _idx(4), _idx(4)), scores + 0.3)
+
+
+def test_soft_capping_and_grad():
+    scores = np.array([[-50.0, 0.0, 50.0]], np.float32)
+    b = oracle.SoftCappingBias(softcap=10.0)
+    out = b(scores, 0, _idx(1), _idx(3))
+    assert np.all(np.abs(out) <= 10.0 + 1e-5)
+    np.testing.assert_allclose(out, 10.0 * np.tanh(scores / 10.0))
+    g = b.grad(scores)
+    assert g.shape == scores.shape and np.all(g >= 0) and np.all(g <= 1)
+    # the derivative against central differences
+    x = np.linspace(-30, 30, 13).astype(np.float64)[None]
+    eps = 1e-5
+    num = (b(x + eps, 0, None, None) - b(x - eps, 0, None, None)) / (2 * eps)
+    np.testing.assert_allclose(b.grad(x), num, atol=1e-7)
+    with pytest.raises(ValueError):
+        oracle.SoftCappingBias(0.0)
+
+
+def test_per_head_scale():
+    scores = np.ones((2, 3), np.float32)
+    b = oracle.PerHeadScaleBias(np.array([2.0, 0.5], np.float32))
+    np.testing.assert_allclose(b(scores, 0, _idx(2), _idx(3)), 2 * scores)
+    np.testing.assert_allclose(b(scores, 1, _idx(2), _idx(3)), 0.5 * scores)
+    np.testing.assert_allclose(b.grad_tile(scores, 0, 1, 0, 2, 0, 3), 0.5 * scores)
