@@ -34,6 +34,51 @@ extern "C" {
 #define PJX_ERR_LAUNCH 2   /* the HIP runtime rejected a launch */
 #define PJX_ERR_WORKSPACE 3 /* workspace missing or too small */
 
+/*
+ * Extended masks and score modifiers of pjx_flash_fwd / pjx_flash_bwd
+ * (probjax/nn/pallas_kernels/attention_mask_bias.py).  Pass NULL for none;
+ * in a struct, window_left / window_right < 0 and NULL pointers mean absent.
+ * All device pointers; lengths and ids int32.
+ *
+ * Masks (ANDed with causal, kv_lengths and q_valid / kv_valid):
+ *   causal_shift   -- with causal != 0, key k is visible to query q iff
+ *                     k <= q + causal_shift: 0 for CausalMask (:617-648),
+ *                     Lk - Lq for CausalFromBottomRightMask (:753-782)
+ *   window_left    -- k >= q - window_left  (LocalWindowMask :651-704,
+ *   window_right   -- k <= q + window_right  CausalLocalWindowMask :707-750)
+ *   prefix_lengths -- [B]: k < P[b] or k <= q (PrefixLMMask :785-868)
+ *   seq_lengths    -- [B]: (q < L[b] and k < L[b]) or q == k (SeqLenMask
+ *                     :1239-1398)
+ *   segment_q, segment_k -- [B, Lq], [B, Lk]: ids equal (SameSegmentMask
+ *                     :1537-1668, BlockDiagonalMask :871-981; with causal
+ *                     BlockDiagonalCausalMask :984-1076)
+ * Score modifiers, on s = sm_scale * q.k in the order of SumBias (:553-582):
+ *   s' = f(s) + bias + alibi + constant, with
+ *   f(s) = softcap * tanh(s / softcap) if softcap > 0 (SoftCappingBias
+ *          :2564-2603), else s * head_scales[h] if head_scales is given
+ *          (PerHeadScaleBias :2606-2648), else s;
+ *   alibi = -alibi_slopes[h] * (alibi_symmetric ? |q - k| : max(q - k, 0))
+ *          (CausalAlibiBias :2230-2255, SymmetricAlibiBias :2355-2380,
+ *          DistanceDecayBias :2387-2414; slopes [Hq]);
+ *   constant (ConstantBias :1781-1805).
+ * The backward multiplies dS by f'(s).  softcap and head_scales exclude each
+ * other.
+ */
+typedef struct pjx_score_mods {
+  int32_t causal_shift;
+  int32_t window_left;
+  int32_t window_right;
+  const int32_t* prefix_lengths;
+  const int32_t* seq_lengths;
+  const int32_t* segment_q;
+  const int32_t* segment_k;
+  const float* alibi_slopes;
+  int32_t alibi_symmetric;
+  float softcap;
+  const float* head_scales;
+  float constant;
+} pjx_score_mods;
+
 /* Library version (major*10000 + minor*100 + patch). */
 int pjx_version(void);
 
@@ -61,6 +106,8 @@ const char* pjx_last_error(void);
  * lse: optional fp32 [B, Hq, Lq] natural-log log-sum-exp of the scores
  *   (+inf for rows without a valid key, as attention_xla.py:420); NULL skips.
  *
+ * mods: extended masks / score modifiers (pjx_score_mods) or NULL.
+ *
  * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim in {64, 128}
  * (k and v share it).  sm_scale must be > 0.
  */
@@ -69,7 +116,7 @@ int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* 
                   int64_t bias_batch, int64_t bias_heads, int64_t batch, int64_t q_len,
                   int64_t kv_len, int64_t q_heads, int64_t kv_heads, int64_t head_dim,
                   int64_t q_valid, int64_t kv_valid, int causal, float sm_scale,
-                  void* stream);
+                  const pjx_score_mods* mods, void* stream);
 
 /*
  * Bytes of workspace pjx_flash_bwd needs: two fp32 values per query row
@@ -95,7 +142,8 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * the output gradient, lse the forward's natural-log LSE [B, Hq, Lq] (+inf
  * rows contribute nothing); dq [B, Lq, Hq, D], dk and dv [B, Lk, Hkv, D]
  * (fully written, zeros where no valid score reaches).  workspace: at least
- * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.
+ * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.  mods: the
+ * forward's (pjx_score_mods) or NULL.
  * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 (all fp32 products, no roundings).
  * head_dim in {64, 128}.
  */
@@ -105,7 +153,7 @@ int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const 
                   const float* bias, int64_t bias_batch, int64_t bias_heads, int64_t batch,
                   int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                   int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
-                  float sm_scale, void* stream);
+                  float sm_scale, const pjx_score_mods* mods, void* stream);
 
 /*
  * Bytes of workspace pjx_splitkv_decode / pjx_mla_decode need for these sizes

@@ -43,7 +43,7 @@ import os
 import torch
 
 from . import hip_attention as hip
-from .masks import LoweredMask, lower_bias, lower_mask
+from .masks import LoweredBias, LoweredMask, lower_bias, lower_mask
 
 HIP_ARCH = "gfx950"
 FLASH_HEAD_DIMS = (64, 128)
@@ -89,9 +89,9 @@ def _lengths_tensor(kv_lengths, batch, device):
     return L.to(torch.int32)
 
 
-def _decode_plan(query, key, value, lm: LoweredMask, bias_t):
+def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
     """Arguments of the split-KV decode for this call, or None."""
-    if bias_t is not None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+    if lb is not None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return None
     if query.dtype != torch.bfloat16:
         return None
@@ -102,21 +102,80 @@ def _decode_plan(query, key, value, lm: LoweredMask, bias_t):
     return dict(kv_lengths=lm.kv_lengths)
 
 
-def _flash_plan(query, key, value, lm: LoweredMask, bias_t):
+def _int_tensor(x, shape, device):
+    """int32 device tensor of ``x`` broadcast to ``shape``, or None."""
+    t = torch.as_tensor(x, device=device)
+    if t.dtype.is_floating_point or t.dtype == torch.bool:
+        return None
+    try:
+        return torch.broadcast_to(t.to(torch.int32), shape).contiguous()
+    except RuntimeError:
+        return None
+
+
+def _score_mods(lm: LoweredMask, lb: LoweredBias | None, B, l_q, l_k, h_q, device):
+    """``ScoreModsArgs`` of the extended masks / modifiers (None when there
+    are none), or False when their data does not fit the call."""
+    ext_bias = lb is not None and lb.extended
+    if not lm.extended and not ext_bias:
+        return None
+    m = hip.ScoreModsArgs(causal_shift=lm.causal_shift or 0)
+    if lm.window_left is not None:
+        m.window_left = int(lm.window_left)
+    if lm.window_right is not None:
+        m.window_right = int(lm.window_right)
+    for name, val in (("prefix_lengths", lm.prefix_lengths), ("seq_lengths", lm.seq_lengths)):
+        if val is not None:
+            t = _int_tensor(torch.as_tensor(val).reshape(-1), (B,), device)
+            if t is None:
+                return False
+            setattr(m, name, t)
+    if lm.segment_q is not None:
+        kid = lm.segment_k if lm.segment_k is not None else lm.segment_q
+        sq, sk = torch.as_tensor(lm.segment_q), torch.as_tensor(kid)
+        if sq.shape[-1] != l_q or sk.shape[-1] != l_k:
+            return False  # ids per position (keys default to the query ids)
+        m.segment_q = _int_tensor(sq, (B, l_q), device)
+        m.segment_k = _int_tensor(sk, (B, l_k), device)
+        if m.segment_q is None or m.segment_k is None:
+            return False
+    if lb is not None:
+        if lb.alibi is not None:
+            if lb.alibi == "decay":
+                slopes = torch.full((h_q,), lb.alibi_alpha, dtype=torch.float32)
+            else:
+                slopes = torch.tensor([2.0 ** (-(h + 1.0)) for h in range(h_q)], dtype=torch.float32)
+            m.alibi_slopes = slopes.to(device)
+            m.alibi_symmetric = lb.alibi != "causal"
+        m.softcap = float(lb.softcap)
+        m.constant = float(lb.constant)
+        if lb.head_scales is not None:
+            hs = torch.as_tensor(lb.head_scales, dtype=torch.float32).reshape(-1)
+            if hs.numel() not in (1, h_q):
+                return False
+            m.head_scales = torch.broadcast_to(hs, (h_q,)).contiguous().to(device)
+    return m
+
+
+def _flash_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
     """Arguments of the flash forward for this call, or None."""
     if query.dtype not in (torch.bfloat16, torch.float32):
         return None
     B, l_q, h_q, d = query.shape
+    l_k = key.shape[1]
     if d not in FLASH_HEAD_DIMS:
         return None
-    if bias_t is not None:
-        l_k = key.shape[1]
-        if bias_t.ndim != 4 or tuple(bias_t.shape[-2:]) != (l_q, l_k):
+    dense = None if lb is None else lb.dense
+    if dense is not None:
+        if dense.ndim != 4 or tuple(dense.shape[-2:]) != (l_q, l_k):
             return None
-        if bias_t.shape[0] not in (1, B) or bias_t.shape[1] not in (1, h_q):
+        if dense.shape[0] not in (1, B) or dense.shape[1] not in (1, h_q):
             return None
-    return dict(causal=lm.causal, kv_lengths=lm.kv_lengths, bias=bias_t,
-                q_valid=lm.q_valid, kv_valid=lm.kv_valid)
+    mods = _score_mods(lm, lb, B, l_q, l_k, h_q, query.device)
+    if mods is False:
+        return None
+    return dict(causal=lm.causal, kv_lengths=lm.kv_lengths, bias=dense,
+                q_valid=lm.q_valid, kv_valid=lm.kv_valid, mods=mods)
 
 
 def _eligible(query, key, value, *, mask, bias, dropout_rate):
@@ -140,12 +199,12 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
         if L is None:
             return None
         lm.kv_lengths = L
-    bias_t = lower_bias(bias)
-    if bias_t is False:
+    lb = lower_bias(bias)
+    if lb is False:
         return None
-    if bias_t is not None:
-        bias_t = bias_t.to(device=query.device, dtype=torch.float32)
-    return lm, bias_t
+    if lb is not None and lb.dense is not None:
+        lb.dense = lb.dense.to(device=query.device, dtype=torch.float32)
+    return lm, lb
 
 
 def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: float,
@@ -154,7 +213,7 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if q.ndim != 4 or k.ndim != 4 or dropout_rate > 0 or has_bias:
         return False
-    if lm is None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+    if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return False
     if q.dtype != torch.bfloat16 or q.shape[-1] not in DECODE_HEAD_DIMS:
         return False
@@ -204,12 +263,12 @@ def _needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
-def _run(query, key, value, lm, bias_t, sm_scale, split_kv):
+def _run(query, key, value, lm, lb, sm_scale, split_kv):
     grad = _needs_grad(query, key, value)
     if grad and query.dtype not in BACKWARD_DTYPES:
         return None
-    if _splitkv_ok(query, key, lm, bias_t is not None, 0.0, split_kv):
-        plan = _decode_plan(query, key, value, lm, bias_t)
+    if _splitkv_ok(query, key, lm, lb is not None, 0.0, split_kv):
+        plan = _decode_plan(query, key, value, lm, lb)
         if plan is not None:
             if not grad:
                 return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, **plan)
@@ -220,7 +279,7 @@ def _run(query, key, value, lm, bias_t, sm_scale, split_kv):
                 lambda q, k, v: hip.splitkv_decode(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
                 dict(sm_scale=sm_scale, kv_lengths=plan["kv_lengths"]),
             )
-    plan = _flash_plan(query, key, value, lm, bias_t)
+    plan = _flash_plan(query, key, value, lm, lb)
     if plan is None:
         return None
     if not grad:
@@ -250,8 +309,8 @@ def hip_attention_or_none(query, key, value, *, mask, bias, dropout_rate: float,
     e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=dropout_rate)
     if e is None:
         return None
-    lm, bias_t = e
-    return _run(query, key, value, lm, bias_t, float(sm_scale), None)
+    lm, lb = e
+    return _run(query, key, value, lm, lb, float(sm_scale), None)
 
 
 # ---------------------------------------------------------------------------
@@ -367,7 +426,7 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     if bias is not None or dropout_rate > 0:
         raise ValueError("the HIP latent-attention kernel takes no bias or dropout")
     lm = lower_mask(mask)
-    if lm is None or lm.causal or lm.q_valid is not None or lm.kv_valid is not None:
+    if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         raise ValueError(f"the HIP latent-attention kernel takes None / NoMask / KVLenMask, got {type(mask).__name__}")
     if not hip_device(q):
         raise ValueError(f"the HIP latent-attention kernel needs tensors on a {HIP_ARCH} ROCm device")

@@ -2,7 +2,7 @@
 #include <stdio.h>
 #include <string.h>
 
-#include "pjx_internal.h"
+#include "flash_common.h"
 
 namespace pjx {
 
@@ -22,6 +22,55 @@ int check_launch(const char* where) {
   snprintf(buf, sizeof(buf), "%s: kernel launch failed: %s", where, hipGetErrorString(err));
   set_error(buf);
   return PJX_ERR_LAUNCH;
+}
+
+int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) {
+  ScoreMods& m = a.m;
+  m.causal_shift = 0;
+  m.win_left = m.win_right = kNoBound;
+  m.prefix = m.seqlen = m.seg_q = m.seg_k = nullptr;
+  m.alibi = nullptr;
+  m.alibi_sym = 0;
+  m.softcap = 0.f;
+  m.head_scale = nullptr;
+  m.constant = 0.f;
+  a.ext = 0;
+  if (!mods) return PJX_OK;
+  char buf[256];
+  if (mods->softcap < 0.f || mods->softcap != mods->softcap) {
+    snprintf(buf, sizeof(buf), "%s: softcap must be >= 0", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (mods->softcap > 0.f && mods->head_scales) {
+    snprintf(buf, sizeof(buf), "%s: softcap and head_scales exclude each other", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if ((mods->segment_q == nullptr) != (mods->segment_k == nullptr)) {
+    snprintf(buf, sizeof(buf), "%s: segment_q and segment_k go together", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (mods->window_left >= kNoBound || mods->window_right >= kNoBound ||
+      mods->causal_shift >= kNoBound || mods->causal_shift <= -kNoBound) {
+    snprintf(buf, sizeof(buf), "%s: window / causal_shift out of range", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  m.causal_shift = a.causal ? mods->causal_shift : 0;
+  m.win_left = mods->window_left >= 0 ? mods->window_left : kNoBound;
+  m.win_right = mods->window_right >= 0 ? mods->window_right : kNoBound;
+  m.prefix = mods->prefix_lengths;
+  m.seqlen = mods->seq_lengths;
+  m.seg_q = mods->segment_q;
+  m.seg_k = mods->segment_k;
+  m.alibi = mods->alibi_slopes;
+  m.alibi_sym = mods->alibi_symmetric ? 1 : 0;
+  m.softcap = mods->softcap;
+  m.head_scale = mods->head_scales;
+  m.constant = mods->constant;
+  a.ext = (m.causal_shift != 0 || m.win_left != kNoBound || m.win_right != kNoBound || m.prefix ||
+           m.seqlen || m.seg_q || m.alibi || m.softcap > 0.f || m.head_scale || m.constant != 0.f)
+              ? 1
+              : 0;
+  return PJX_OK;
 }
 
 }  // namespace pjx

@@ -114,7 +114,7 @@ __device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x 
 // ---------------------------------------------------------------------------
 // dQ (and delta): one workgroup per (128-query tile, batch, head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
@@ -123,6 +123,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[2 * TILE_B];
 
   BlockGeom g = block_geom(a);
+  if constexpr (EXT) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   g.qw = __builtin_amdgcn_readfirstlane(g.qw);
@@ -173,7 +174,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  ExtRows er;
+  if constexpr (EXT) er = ext_rows(a, g);
 
   uint32_t voff[T::NLD];
 #pragma unroll
@@ -188,11 +191,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
 
-  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int t_begin = g.kv_begin / BK;
+  const int n_tiles = max((g.kv_stop + BK - 1) / BK - t_begin, 0);
   const int q_last_w = g.qw + 31;
 
   auto issue = [&](int t, unsigned char* ks) {
-    const int k0 = t * BK;
+    const int k0 = (t_begin + t) * BK;
     const int nvalid = min(BK, g.kv_stop - k0);
     const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
     const rsrc_t rk = make_rsrc(Kb + (size_t)k0 * rowstride, bytes);
@@ -206,8 +210,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
   };
 
   auto compute = [&](int t, const unsigned char* ks) {
-    const int k0 = t * BK;
-    if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    const int k0 = (t_begin + t) * BK;
+    if constexpr (EXT) {
+      if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
+    } else {
+      if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    }
     const unsigned char* vs = ks + TILE_B;
 
     // S^T[key][query] = K Q^T and dP^T = V dO^T; register r of block kb holds
@@ -228,6 +236,14 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         dp[kb] = mfma32x32x16(vf, dof[st], dp[kb]);
       }
     }
+    if constexpr (EXT) {
+      // modified scores, masks, P and dS = P (dP - delta) * scale * f'(s)
+      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
+                                   [&](int kb, int r, float x, float gg) {
+                                     const float p = fast_exp2(fmaf(x, cx, -lse2));
+                                     s[kb][r] = p * (dp[kb][r] - delta) * a.scale * gg;
+                                   });
+    } else {
     if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -261,6 +277,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
         s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
       }
+    }
     bf16x8 dsf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) dsf[c] = pack_step(s[c >> 1], c & 1);
@@ -302,7 +319,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 // ---------------------------------------------------------------------------
 // dK, dV: one workgroup per (128-key tile, batch, KV head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
@@ -328,9 +345,29 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
   int kv_end = min(a.Lk, a.kv_valid);
   if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
   const int q_hi = min(a.Lq, a.q_valid);
-  // Queries that can see a key of this tile: causal rows start at k0.
-  const int q_begin = a.causal ? (k0 / kBQs) * kBQs : 0;
-  const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + kBQs - 1) / kBQs : 0;
+  // Queries that can see a key of this tile: causal rows start at k0; with
+  // extended masks the rows [qlo(k0), qhi(last key)] (both monotone).
+  int q_begin = a.causal ? (k0 / kBQs) * kBQs : 0;
+  int q_end = q_hi;
+  int qlo = 0, qhi = q_hi - 1, wq_first = 0, wq_last = q_hi - 1, segk = 0;
+  if constexpr (EXT) {
+    q_end = q_begin = 0;
+    if (k0 < kv_end) {
+      int a0, a1, b0, b1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, k0, a0, a1);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(k0 + kBKV, kv_end) - 1, b0, b1);
+      q_begin = max(a0, 0);
+      q_end = b1 + 1;
+    }
+    key_bounds(a.m, a.causal, b, kv_end, q_hi, key, qlo, qhi);
+    if (kw < kv_end) {
+      int c0, c1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, c1);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, c0, wq_last);
+    }
+    if (a.m.seg_k && key < a.Lk) segk = a.m.seg_k[(size_t)b * a.Lk + key];
+  }
+  const int n_qt = (k0 < kv_end && q_end > q_begin) ? (q_end - q_begin + kBQs - 1) / kBQs : 0;
   const int n_tiles = G * n_qt;
 
   // K^T and V^T as B operands: lane holds key `key`, dims 16*s + 8*half + [0,8).
@@ -351,7 +388,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
       vf[s] = as_bf16x8(rv);
     }
   }
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
   const uint32_t rowstride = (uint32_t)a.Hq * D * 2;
 
   uint32_t voff[T::NLD];
@@ -375,7 +412,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
 
   auto issue = [&](int t, unsigned char* st) {
     const int h = tile_head(t), q0 = tile_q0(t);
-    const int nvalid = min(kBQs, a.Lq - q0);
+    const int nvalid = max(min(kBQs, a.Lq - q0), 1);
     const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
     const size_t roff = ((size_t)(b * a.Lq + q0) * a.Hq + h) * ROWB;
     const rsrc_t rq = make_rsrc((const unsigned char*)a.q + roff, bytes);
@@ -406,6 +443,41 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
     for (int qb = 0; qb < kBQs / 32; ++qb) {
       const int qs0 = q0 + 32 * qb;
       if (qs0 >= q_hi || kw >= kv_end) continue;
+      if constexpr (EXT) {
+        if (qs0 > wq_last || qs0 + 31 < wq_first) continue;  // no row of this step sees the wave's keys
+        // S = Q K^T and dP = dO V^T first, then one pass: modified score,
+        // mask, P and dS = P (dP - delta) * scale * f'(s).
+        f32x16 sx = f32x16{}, dpx = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+          const bf16x8 qf = as_bf16x8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[kk]));
+          sx = mfma32x32x16(qf, kf[kk], sx);
+        }
+#pragma unroll
+        for (int kk = 0; kk < D / 16; ++kk) {
+          const bf16x8 df = as_bf16x8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[kk]));
+          dpx = mfma32x32x16(df, vf[kk], dpx);
+        }
+        const HeadMods hm = head_mods(a.m, h);
+        ext_scores_S<BIAS>(a, b, hm, key, qlo, qhi, segk, sx, qs0, half, bbase,
+                           [&](int r, float x, float gg) {
+                             const int ql = 32 * qb + 8 * (r >> 2) + 4 * half + (r & 3);
+                             const float p = fast_exp2(fmaf(x, cx, -lsm[ql]));
+                             sx[r] = p;
+                             dpx[r] = p * (dpx[r] - dlm[ql]) * a.scale * gg;
+                           });
+#pragma unroll
+        for (int c = 0; c < 2; ++c) {
+          const bf16x8 pf = pack_step(sx, c);
+          const bf16x8 dsf = pack_step(dpx, c);
+#pragma unroll
+          for (int db = 0; db < D / 32; ++db) {
+            accv[db] = mfma32x32x16(read_t<D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
+            acck[db] = mfma32x32x16(read_t<D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
+          }
+        }
+        continue;
+      }
       if (a.causal && qs0 + 31 < kw) continue;  // every query before this wave's first key
 
       // S[query][key] = Q K^T: register r holds query qs0 + 8*(r/4) + 4*half + r%4
@@ -513,7 +585,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
 // tile.  Tiles are staged through registers into LDS rows padded to D + 4
 // floats (16-byte reads of 16 consecutive rows hit distinct banks).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   constexpr int BK = (D == 128) ? 32 : 64;
@@ -524,7 +596,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
   __shared__ __attribute__((aligned(16))) float k_lds[2][BK * KS];
   __shared__ __attribute__((aligned(16))) float v_lds[2][BK * KS];
 
-  const BlockGeom g = block_geom(a);
+  BlockGeom g = block_geom(a);
+  if constexpr (EXT) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
   const size_t kv_row = (size_t)a.Hkv * D;
@@ -572,17 +645,20 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  ExtRows er;
+  if constexpr (EXT) er = ext_rows(a, g);
 
   f32x16 acc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
-  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int t_begin = g.kv_begin / BK;
+  const int n_tiles = max((g.kv_stop + BK - 1) / BK - t_begin, 0);
   const int q_last_w = g.qw + 31;
 
   f32x4 kreg[PER_T], vreg[PER_T];
   auto load_tile = [&](int t) {
-    const int k0 = t * BK;
+    const int k0 = (t_begin + t) * BK;
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int u = tid + kThreads * i;
@@ -606,8 +682,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
   };
 
   auto compute = [&](int t, int buf) {
-    const int k0 = t * BK;
-    if (a.causal && k0 > q_last_w) return;
+    const int k0 = (t_begin + t) * BK;
+    if constexpr (EXT) {
+      if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
+    } else {
+      if (a.causal && k0 > q_last_w) return;
+    }
     const float* kl = k_lds[buf];
     const float* vl = v_lds[buf];
     f32x16 s[BK / 32], dp[BK / 32];
@@ -628,6 +708,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
         }
       }
     }
+    if constexpr (EXT) {
+      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
+                                   [&](int kb, int r, float x, float gg) {
+                                     const float p = fast_exp2(fmaf(x, cx, -lse2));
+                                     s[kb][r] = p * (dp[kb][r] - delta) * a.scale * gg;
+                                   });
+    } else {
     if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -659,6 +746,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
         s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
       }
+    }
     // dQ^T[d][query] += K^T dS^T: step (kb, r) contracts keys (r, half 0/1).
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
@@ -697,7 +785,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
   }
 }
 
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   constexpr int BQ = 32;  // queries per stage (one 32-query step)
@@ -722,8 +810,27 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   int kv_end = min(a.Lk, a.kv_valid);
   if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
   const int q_hi = min(a.Lq, a.q_valid);
-  const int q_begin = a.causal ? (k0 / BQ) * BQ : 0;
-  const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + BQ - 1) / BQ : 0;
+  int q_begin = a.causal ? (k0 / BQ) * BQ : 0;
+  int q_end = q_hi;
+  int qlo = 0, qhi = q_hi - 1, wq_first = 0, wq_last = q_hi - 1, segk = 0;
+  if constexpr (EXT) {
+    q_end = q_begin = 0;
+    if (k0 < kv_end) {
+      int a0, a1, b0, b1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, k0, a0, a1);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(k0 + kBKV, kv_end) - 1, b0, b1);
+      q_begin = max(a0, 0);
+      q_end = b1 + 1;
+    }
+    key_bounds(a.m, a.causal, b, kv_end, q_hi, key, qlo, qhi);
+    if (kw < kv_end) {
+      int c0, c1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, c1);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, c0, wq_last);
+    }
+    if (a.m.seg_k && key < a.Lk) segk = a.m.seg_k[(size_t)b * a.Lk + key];
+  }
+  const int n_qt = (k0 < kv_end && q_end > q_begin) ? (q_end - q_begin + BQ - 1) / BQ : 0;
   const int n_tiles = G * n_qt;
 
   float kf[D / 2], vf[D / 2];
@@ -746,7 +853,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
       }
     }
   }
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
   const size_t q_row = (size_t)a.Hq * D;
 
   f32x16 acck[D / 32], accv[D / 32];
@@ -796,7 +903,11 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   auto compute = [&](int t, int buf) {
     const int h = tile_head(t), q0 = tile_q0(t);
     if (q0 >= q_hi || kw >= kv_end) return;
-    if (a.causal && q0 + BQ - 1 < kw) return;  // every query before this wave's first key
+    if constexpr (EXT) {
+      if (q0 > wq_last || q0 + BQ - 1 < wq_first) return;  // no row of this step sees the wave's keys
+    } else {
+      if (a.causal && q0 + BQ - 1 < kw) return;  // every query before this wave's first key
+    }
     const float* ql = q_lds[buf];
     const float* dl = d_lds[buf];
     const float* lsm = ld_lds[buf];
@@ -817,6 +928,19 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
         }
       }
     }
+    f32x16 ds;
+    if constexpr (EXT) {
+      const float* bbase = nullptr;
+      if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
+      const HeadMods hm = head_mods(a.m, h);
+      ext_scores_S<BIAS>(a, b, hm, key, qlo, qhi, segk, s, q0, half, bbase,
+                         [&](int r, float x, float gg) {
+                           const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
+                           const float p = fast_exp2(fmaf(x, cx, -lsm[qi]));
+                           s[r] = p;
+                           ds[r] = p * (dp[r] - lsm[BQ + qi]) * a.scale * gg;
+                         });
+    } else {
     if constexpr (BIAS) {
       const float* bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
 #pragma unroll
@@ -835,13 +959,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
         if (!keep) s[r] = -INFINITY;
       }
     }
-    f32x16 ds;
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
       const float p = fast_exp2(fmaf(s[r], cx, -lsm[qi]));
       s[r] = p;
       ds[r] = p * (dp[r] - lsm[BQ + qi]) * a.scale;
+    }
     }
     // dV^T[d][key] += dO^T P and dK^T[d][key] += Q^T dS: step r contracts
     // queries (r, half 0/1).
@@ -903,21 +1027,27 @@ static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
 
 // dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
 // dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
-template <int D>
-static int run_bwd(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
+template <int D, bool EXT>
+static int run_bwd_t(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
     int rc;
     if (f32)
-      rc = hb ? launch_dq(flash_bwd_dq_f32_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_f32_kernel<D, false>, a, s);
+      rc = hb ? launch_dq(flash_bwd_dq_f32_kernel<D, true, EXT>, a, s) : launch_dq(flash_bwd_dq_f32_kernel<D, false, EXT>, a, s);
     else
-      rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false>, a, s);
+      rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true, EXT>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false, EXT>, a, s);
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
   if (f32)
-    return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true>, a, s)
-              : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false>, a, s);
-  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<D, true>, a, s) : launch_dkdv(flash_bwd_dkdv_kernel<D, false>, a, s);
+    return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true, EXT>, a, s)
+              : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false, EXT>, a, s);
+  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<D, true, EXT>, a, s)
+            : launch_dkdv(flash_bwd_dkdv_kernel<D, false, EXT>, a, s);
+}
+
+template <int D>
+static int run_bwd(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
+  return a.f.ext ? run_bwd_t<D, true>(a, f32, hb, s) : run_bwd_t<D, false>(a, f32, hb, s);
 }
 
 }  // namespace pjx
@@ -935,7 +1065,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
                              const float* bias, int64_t bias_batch, int64_t bias_heads,
                              int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t q_valid, int64_t kv_valid,
-                             int causal, float sm_scale, void* stream) {
+                             int causal, float sm_scale, const pjx_score_mods* mods, void* stream) {
   clear_error();
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
@@ -976,6 +1106,8 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL ||
       (long)((kv_len + kBKV - 1) / kBKV) * batch * kv_heads > 0x7fffffffL)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: grid too large");
+  const int mrc = lower_score_mods(mods, a, "pjx_flash_bwd");
+  if (mrc != PJX_OK) return mrc;
   ba.dout = dout;
   ba.delta = (float*)workspace;
   ba.lse2 = ba.delta + batch * q_heads * q_len;

@@ -3,6 +3,7 @@
 // geometry, the bias loader and the bf16 K/V tile layout.
 #pragma once
 
+#include "attn_mods.h"
 #include "pjx_common.h"
 #include "pjx_internal.h"
 
@@ -22,6 +23,8 @@ struct FlashArgs {
   int q_valid, kv_valid, causal;
   float scale;
   int n_qtiles;
+  int ext;      // extended masks / score modifiers in `m` are active
+  ScoreMods m;
 };
 
 constexpr int kBQ = 128;
@@ -33,6 +36,7 @@ struct BlockGeom {
   int q_hi;     // rows >= q_hi are fully masked (QKVLengthMask / Lq)
   int kv_end;   // keys >= kv_end are masked (KVLenMask, QKVLengthMask, Lk)
   int kv_stop;  // keys the block visits (kv_end, clipped causally)
+  int kv_begin; // first key the block visits (a multiple of the key tile)
 };
 
 __device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) {
@@ -59,7 +63,59 @@ __device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) {
     stop = min(stop, min(g.q0 + kBQ, g.q_hi));
   }
   g.kv_stop = stop;
+  g.kv_begin = 0;
   return g;
+}
+
+// With extended masks: the block's key range [kv_begin, kv_stop) from the
+// interval bounds of its first and last row (both bounds are monotone in the
+// row), kv_begin rounded down to the key tile.
+__device__ __forceinline__ void ext_block_range(const FlashArgs& a, BlockGeom& g, int tile) {
+  g.kv_begin = 0;
+  if (g.q0 >= g.q_hi) {
+    g.kv_stop = 0;
+    return;
+  }
+  int lo0, hi0, lo1, hi1;
+  const int q_last = min(g.q0 + kBQ, g.q_hi) - 1;
+  row_bounds(a.m, a.causal, g.b, g.kv_end, g.q_hi, g.q0, lo0, hi0);
+  row_bounds(a.m, a.causal, g.b, g.kv_end, g.q_hi, q_last, lo1, hi1);
+  g.kv_begin = (max(lo0, 0) / tile) * tile;
+  g.kv_stop = max(min(hi1 + 1, g.kv_end), 0);
+}
+
+// Per-wave view of the extended masks for a wave owning rows qw .. qw+31 and
+// a lane owning row qi (S^T layout: one query per lane).
+struct ExtRows {
+  int lo, hi;          // this lane's key interval
+  int lo_first, hi_first;  // interval of the wave's first row
+  int lo_last, hi_last;    // interval of the wave's last existing row
+  bool any;            // the wave has a row < q_hi
+  int segq;            // this row's segment id
+  HeadMods hm;
+};
+
+__device__ __forceinline__ ExtRows ext_rows(const FlashArgs& a, const BlockGeom& g) {
+  ExtRows e;
+  row_bounds(a.m, a.causal, g.b, g.kv_end, g.q_hi, g.qi, e.lo, e.hi);
+  e.any = g.qw < g.q_hi;
+  const int ql = min(g.qw + 31, g.q_hi - 1);
+  row_bounds(a.m, a.causal, g.b, g.kv_end, g.q_hi, g.qw, e.lo_first, e.hi_first);
+  row_bounds(a.m, a.causal, g.b, g.kv_end, g.q_hi, ql, e.lo_last, e.hi_last);
+  e.segq = (a.m.seg_q && g.qi < a.Lq) ? a.m.seg_q[(size_t)g.b * a.Lq + g.qi] : 0;
+  e.hm = head_mods(a.m, g.h);
+  return e;
+}
+
+// Segment ids of 4 consecutive keys kk .. kk+3 of batch b (0 past Lk).
+__device__ __forceinline__ int4 seg4(const int32_t* seg, int b, int kk, int Lk) {
+  const int32_t* p = seg + (size_t)b * Lk;
+  int4 r;
+  r.x = kk < Lk ? p[kk] : 0;
+  r.y = kk + 1 < Lk ? p[kk + 1] : 0;
+  r.z = kk + 2 < Lk ? p[kk + 2] : 0;
+  r.w = kk + 3 < Lk ? p[kk + 3] : 0;
+  return r;
 }
 
 // Bias for this lane's query row at 4 consecutive keys starting at kk.
@@ -91,8 +147,75 @@ struct Bf16Tile {
   }
 };
 
+// Host: checks the C-ABI modifier block and fills a.m / a.ext; returns a
+// PJX_* status (message set on error).
+int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who);
+
 // Launches the bf16 dense-bias kernel (flash_bias_ring.hip); returns a PJX_*
 // status.
 int launch_flash_bias_ring(int head_dim, const FlashArgs& a, hipStream_t stream);
+
+}  // namespace pjx
+
+namespace pjx {
+
+// Extended masks and modifiers on one key tile in the S^T layout (lane =
+// query g.qi; register r of block kb = key k0 + kb*32 + 8*(r/4) + 4*half +
+// r%4).  For every raw score q.k, emit(kb, r, x, g) receives the modified
+// score x (-inf where masked) and the modifier's derivative g.
+template <int NKB, bool BIAS, typename Emit>
+__device__ __forceinline__ void ext_scores_sT(const FlashArgs& a, const BlockGeom& g,
+                                              const ExtRows& er, const f32x16* s, int k0, int half,
+                                              const float* brow, bool row_in, Emit emit) {
+  const bool bias_vec = (a.Lk & 3) == 0;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+      f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+      if constexpr (BIAS) {
+        if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+      }
+      int4 sg = {0, 0, 0, 0};
+      if (a.m.seg_q) sg = seg4(a.m.seg_k, g.b, kk, a.Lk);
+      const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int r = 4 * gq + j, kj = kk + j;
+        float gg;
+        const float x = modify_score(a.m, er.hm, s[kb][r] * a.scale, bv[j], g.qi, kj, gg);
+        const bool keep = kj >= er.lo && kj <= er.hi && (!a.m.seg_q || sgv[j] == er.segq);
+        emit(kb, r, keep ? x : -INFINITY, gg);
+      }
+    }
+}
+
+// The same in the S layout of the dK/dV kernels (lane = key `key`, register
+// r = query qs0 + 8*(r/4) + 4*half + r%4); [qlo, qhi] are the rows that see
+// `key`, segk its segment id, bbase the bias slice of (b, h).
+// emit(r, x, g) as above.
+template <bool BIAS, typename Emit>
+__device__ __forceinline__ void ext_scores_S(const FlashArgs& a, int b, const HeadMods& hm, int key,
+                                             int qlo, int qhi, int segk, const f32x16& s, int qs0,
+                                             int half, const float* bbase, Emit emit) {
+#pragma unroll
+  for (int gq = 0; gq < 4; ++gq) {
+    const int q4 = qs0 + 8 * gq + 4 * half;
+    int4 sg = {0, 0, 0, 0};
+    if (a.m.seg_q) sg = seg4(a.m.seg_q, b, q4, a.Lq);
+    const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = 4 * gq + j, qr = q4 + j;
+      float bv = 0.f;
+      if constexpr (BIAS) bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
+      float gg;
+      const float x = modify_score(a.m, hm, s[r] * a.scale, bv, qr, key, gg);
+      const bool keep = qr >= qlo && qr <= qhi && (!a.m.seg_q || sgv[j] == segk);
+      emit(r, keep ? x : -INFINITY, gg);
+    }
+  }
+}
 
 }  // namespace pjx

@@ -61,7 +61,7 @@ namespace pjx {
 // ---------------------------------------------------------------------------
 
 
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
   using T = Bf16Tile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
@@ -72,6 +72,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
 
   BlockGeom g = block_geom(a);
+  if constexpr (EXT) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave index and the wave's first row as wave-uniform (scalar) values, so
   // that branches on them are scalar branches.
@@ -102,7 +103,11 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;  // score units -> log2 units
+  // score units -> log2 units (the scale is applied to the score itself when
+  // a bias or modifier is added to it)
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  ExtRows er;
+  if constexpr (EXT) er = ext_rows(a, g);
 
   // Per-lane byte offsets, fixed for the whole key loop.
   uint32_t voffK[T::NLD], voffV[T::NLD];
@@ -131,11 +136,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
   float m_run = kMaxInit, l_run = 0.f;
 
-  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int t_begin = g.kv_begin / BK;
+  const int n_tiles = max((g.kv_stop + BK - 1) / BK - t_begin, 0);
   const int q_last_w = g.qw + 31;
 
   auto issue = [&](int t, unsigned char* ks) {
-    const int k0 = t * BK;
+    const int k0 = (t_begin + t) * BK;
     const int nvalid = min(BK, g.kv_stop - k0);
     const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
     const rsrc_t rk = make_rsrc(Kb + (size_t)k0 * rowstride, bytes);
@@ -149,8 +155,13 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   };
 
   auto compute = [&](int t, const unsigned char* ks) {
-    const int k0 = t * BK;
-    if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    const int k0 = (t_begin + t) * BK;
+    if constexpr (EXT) {
+      // tile outside every row of this wave
+      if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
+    } else {
+      if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
+    }
     const unsigned char* vs = ks + TILE_B;
 
     // S^T[key][query] = K Q^T
@@ -166,7 +177,10 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     }
 
     // Register r of block kb holds key k0 + kb*32 + 8*(r/4) + 4*half + r%4.
-    if constexpr (BIAS) {
+    if constexpr (EXT) {
+      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
+                                       [&](int kb, int r, float x, float) { s[kb][r] = x; });
+    } else if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb) {
 #pragma unroll
@@ -179,8 +193,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
         }
       }
     }
-    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                           (g.qw + 31 >= g.q_hi);
+    const bool need_mask = !EXT && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                    (g.qw + 31 >= g.q_hi));
     if (need_mask) {
       // Key k0 + 4*half + o (o = kb*32 + 8*(r/4) + r%4) is kept iff o <= lim.
       const int base = k0 + 4 * half;
@@ -289,7 +303,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 // P.V the step pairs key (r, half 0) with key (r, half 1) of the S^T layout,
 // so V is read in its natural [key][dim] layout: no transpose needed.
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS>
+template <int D, bool BIAS, bool EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a) {
   constexpr int BK = (D == 128) ? 32 : 64;
   constexpr int KS = D + 4;  // floats; b128 reads of 16 rows hit distinct banks
@@ -301,7 +315,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
   __shared__ __attribute__((aligned(16))) float k_lds[2][BK * KS];
   __shared__ __attribute__((aligned(16))) float v_lds[2][BK * VS];
 
-  const BlockGeom g = block_geom(a);
+  BlockGeom g = block_geom(a);
+  if constexpr (EXT) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
   const size_t kv_row = (size_t)a.Hkv * D;
@@ -328,18 +343,21 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = BIAS ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  ExtRows er;
+  if constexpr (EXT) er = ext_rows(a, g);
 
   f32x16 acc[D / 32];
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
   float m_run = kMaxInit, l_run = 0.f;
-  const int n_tiles = (g.kv_stop + BK - 1) / BK;
+  const int t_begin = g.kv_begin / BK;
+  const int n_tiles = max((g.kv_stop + BK - 1) / BK - t_begin, 0);
   const int q_last_w = g.qw + 31;
 
   f32x4 kreg[PER_T], vreg[PER_T];
   auto load_tile = [&](int t) {
-    const int k0 = t * BK;
+    const int k0 = (t_begin + t) * BK;
 #pragma unroll
     for (int i = 0; i < PER_T; ++i) {
       const int u = tid + kThreads * i;
@@ -363,8 +381,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
   };
 
   auto compute = [&](int t, int buf) {
-    const int k0 = t * BK;
-    if (a.causal && k0 > q_last_w) return;
+    const int k0 = (t_begin + t) * BK;
+    if constexpr (EXT) {
+      if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
+    } else {
+      if (a.causal && k0 > q_last_w) return;
+    }
     const float* kl = k_lds[buf];
     const float* vl = v_lds[buf];
     f32x16 s[BK / 32];
@@ -379,7 +401,10 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
         for (int j = 0; j < 4; ++j) s[kb] = mfma32x32x2f32(kf[j], qf[4 * st4 + j], s[kb]);
       }
     }
-    if constexpr (BIAS) {
+    if constexpr (EXT) {
+      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
+                                       [&](int kb, int r, float x, float) { s[kb][r] = x; });
+    } else if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
@@ -391,8 +416,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
           for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
         }
     }
-    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                           (g.qw + 31 >= g.q_hi);
+    const bool need_mask = !EXT && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                    (g.qw + 31 >= g.q_hi));
     if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -685,7 +710,7 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
                              int64_t bias_batch, int64_t bias_heads, int64_t batch,
                              int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                              int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
-                             float sm_scale, void* stream) {
+                             float sm_scale, const pjx_score_mods* mods, void* stream) {
   clear_error();
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
     return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
@@ -719,18 +744,31 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
   if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL)
     return fail(PJX_ERR_INVALID, "pjx_flash_fwd: grid too large");
+  const int mrc = lower_score_mods(mods, a, "pjx_flash_fwd");
+  if (mrc != PJX_OK) return mrc;
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
+  if (a.ext) {
+    // Extended masks / score modifiers: the one-pass kernels' EXT variants.
+    if (dtype == PJX_DTYPE_BF16) {
+      if (head_dim == 128)
+        return hb ? launch(flash_fwd_bf16_kernel<128, true, true>, a, s) : launch(flash_fwd_bf16_kernel<128, false, true>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<64, true, true>, a, s) : launch(flash_fwd_bf16_kernel<64, false, true>, a, s);
+    }
+    if (head_dim == 128)
+      return hb ? launch(flash_fwd_f32_kernel<128, true, true>, a, s) : launch(flash_fwd_f32_kernel<128, false, true>, a, s);
+    return hb ? launch(flash_fwd_f32_kernel<64, true, true>, a, s) : launch(flash_fwd_f32_kernel<64, false, true>, a, s);
+  }
   if (dtype == PJX_DTYPE_BF16) {
     // Dense bias with 16-byte aligned rows and 32-bit slice offsets: the LDS
     // ring that streams the bias; otherwise bias loads into registers.
     const bool ring = hb && kv_len % 4 == 0 && q_len * kv_len * 4 < ((int64_t)1 << 31);
     if (head_dim == 128) {
       if (ring) return launch_flash_bias_ring(128, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<128, true>, a, s) : launch(flash_fwd_bf16_kernel<128, false>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<128, true, false>, a, s) : launch(flash_fwd_bf16_kernel<128, false, false>, a, s);
     }
     if (ring) return launch_flash_bias_ring(64, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<64, true>, a, s) : launch(flash_fwd_bf16_kernel<64, false>, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<64, true, false>, a, s) : launch(flash_fwd_bf16_kernel<64, false, false>, a, s);
   }
   // fp32 with fewer 128-row workgroups than CUs: split each query block's
   // keys over several waves (latency-bound sizes, like the reference's CPU
@@ -742,6 +780,6 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
     return hb ? launch_split<64>(flash_fwd_f32_split_kernel<64, true>, a, s)
               : launch_split<64>(flash_fwd_f32_split_kernel<64, false>, a, s);
   }
-  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true>, a, s) : launch(flash_fwd_f32_kernel<128, false>, a, s);
-  return hb ? launch(flash_fwd_f32_kernel<64, true>, a, s) : launch(flash_fwd_f32_kernel<64, false>, a, s);
+  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true, false>, a, s) : launch(flash_fwd_f32_kernel<128, false, false>, a, s);
+  return hb ? launch(flash_fwd_f32_kernel<64, true, false>, a, s) : launch(flash_fwd_f32_kernel<64, false, false>, a, s);
 }

@@ -9,6 +9,7 @@ device; nothing is copied between host and device.
 from __future__ import annotations
 
 import ctypes
+from dataclasses import dataclass
 
 import torch
 
@@ -55,15 +56,67 @@ def _lengths(kv_lengths, batch, dev):
     return L
 
 
+@dataclass
+class ScoreModsArgs:
+    """Extended masks and score modifiers of the flash kernels
+    (``pjx_score_mods``): device tensors, or None / defaults for absent."""
+
+    causal_shift: int = 0  # with causal: k <= q + causal_shift
+    window_left: int = -1  # >= 0: k >= q - window_left
+    window_right: int = -1  # >= 0: k <= q + window_right
+    prefix_lengths: torch.Tensor | None = None  # [B] int32
+    seq_lengths: torch.Tensor | None = None  # [B] int32
+    segment_q: torch.Tensor | None = None  # [B, Lq] int32
+    segment_k: torch.Tensor | None = None  # [B, Lk] int32
+    alibi_slopes: torch.Tensor | None = None  # [Hq] float32
+    alibi_symmetric: bool = False
+    softcap: float = 0.0
+    head_scales: torch.Tensor | None = None  # [Hq] float32
+    constant: float = 0.0
+
+
+def _mods_struct(m: ScoreModsArgs | None, B, Lq, Lk, Hq, dev):
+    """``pjx_score_mods`` for the call (shapes and dtypes checked), or None."""
+    if m is None:
+        return None
+
+    def dev_tensor(t, shape, dtype, what):
+        if t is None:
+            return None
+        if not isinstance(t, torch.Tensor) or t.device != dev or t.dtype != dtype:
+            raise ValueError(f"{what} must be a {dtype} tensor on {dev}")
+        if tuple(t.shape) != shape:
+            raise ValueError(f"{what} must have shape {shape}, got {tuple(t.shape)}")
+        return t.contiguous()
+
+    ts = {
+        "prefix_lengths": dev_tensor(m.prefix_lengths, (B,), torch.int32, "prefix_lengths"),
+        "seq_lengths": dev_tensor(m.seq_lengths, (B,), torch.int32, "seq_lengths"),
+        "segment_q": dev_tensor(m.segment_q, (B, Lq), torch.int32, "segment_q"),
+        "segment_k": dev_tensor(m.segment_k, (B, Lk), torch.int32, "segment_k"),
+        "alibi_slopes": dev_tensor(m.alibi_slopes, (Hq,), torch.float32, "alibi_slopes"),
+        "head_scales": dev_tensor(m.head_scales, (Hq,), torch.float32, "head_scales"),
+    }
+    st = native.ScoreMods(
+        causal_shift=int(m.causal_shift), window_left=int(m.window_left),
+        window_right=int(m.window_right), alibi_symmetric=int(bool(m.alibi_symmetric)),
+        softcap=float(m.softcap), constant=float(m.constant),
+        **{k: (None if v is None else v.data_ptr()) for k, v in ts.items()},
+    )
+    return st, ts  # the tensors stay alive for the call
+
+
 def flash_attention_fwd(
     q, k, v, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
     q_valid: int | None = None, kv_valid: int | None = None, return_lse: bool = False,
+    mods: ScoreModsArgs | None = None,
 ):
     """``pjx_flash_fwd``: ``q [B, Lq, Hq, D]``, ``k/v [B, Lk, Hkv, D]`` -> ``o``.
 
     ``bias`` is fp32 ``[1|B, 1|Hq, Lq, Lk]``; ``kv_lengths`` int ``[B]``;
     ``q_valid``/``kv_valid`` are static query/key lengths (QKVLengthMask).
     Returns ``o`` (and the natural-log LSE ``[B, Hq, Lq]`` with ``return_lse``).
+    ``mods``: extended masks / score modifiers.
     """
     dev = _on_device(q, k, v, bias)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -91,13 +144,15 @@ def flash_attention_fwd(
             raise ValueError(f"bias {tuple(bias.shape)} does not broadcast to B={B}, H={Hq}")
         bias = bias.to(torch.float32).contiguous()
     L = _lengths(kv_lengths, B, dev)
+    ms = _mods_struct(mods, B, Lq, Lk, Hq, dev)
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=dev) if return_lse else None
     lib = native.load()
     rc = lib.pjx_flash_fwd(
         code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(lse), _ptr(L), _ptr(bias), bb, bh,
         B, Lq, Lk, Hq, Hkv, D, Lq if q_valid is None else int(q_valid),
-        Lk if kv_valid is None else int(kv_valid), int(bool(causal)), float(sm_scale), _stream(dev),
+        Lk if kv_valid is None else int(kv_valid), int(bool(causal)), float(sm_scale),
+        None if ms is None else ctypes.byref(ms[0]), _stream(dev),
     )
     native.check(rc)
     return (o, lse) if return_lse else o
@@ -106,6 +161,7 @@ def flash_attention_fwd(
 def flash_attention_bwd(
     q, k, v, o, do, lse, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
     q_valid: int | None = None, kv_valid: int | None = None, workspace=None,
+    mods: ScoreModsArgs | None = None,
 ):
     """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``.
 
@@ -141,6 +197,7 @@ def flash_attention_bwd(
             raise ValueError(f"bias {tuple(bias.shape)} does not broadcast to B={B}, H={Hq}")
         bias = bias.to(torch.float32).contiguous()
     L = _lengths(kv_lengths, B, dev)
+    ms = _mods_struct(mods, B, Lq, Lk, Hq, dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     lib = native.load()
     ws = _workspace(int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq)), dev, workspace)
@@ -148,7 +205,7 @@ def flash_attention_bwd(
         code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
         _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
         Lq if q_valid is None else int(q_valid), Lk if kv_valid is None else int(kv_valid),
-        int(bool(causal)), float(sm_scale), _stream(dev),
+        int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
     )
     native.check(rc)
     return dq, dk, dv

@@ -10,17 +10,32 @@ attention_mask_bias.py):
 * ``QKVLengthMask``   -- :1077-1127, static ``(q < q_length) & (k < kv_length)``;
 * ``KVLenMask``       -- :1399-1532, key ``k`` of batch ``b`` kept iff
   ``k < kv_lengths[b]``;
+* ``CausalFromBottomRightMask`` -- :753-782, ``q + (kv_length - q_length) >= k``;
+* ``LocalWindowMask`` / ``CausalLocalWindowMask`` -- :651-750, a band
+  ``q - left <= k <= q + right`` (right 0 for the causal one);
+* ``PrefixLMMask``    -- :785-868, ``k < P[b]`` or ``q >= k``;
+* ``SeqLenMask``      -- :1239-1398, full attention inside ``L[b]``, the
+  diagonal outside;
+* ``SameSegmentMask`` / ``BlockDiagonalMask`` / ``BlockDiagonalCausalMask`` --
+  :1537-1668, :871-1076, equal segment ids (and ``q >= k``);
 * ``ComposeMask``     -- :324-525; only ``"and"`` compositions lower to the
   kernels (what the kernels evaluate is an AND of the above);
 * ``DenseBias``       -- :1807-1922, ``scores + bias[b|0, h|0, q, k]`` with an
-  fp32 ``[B|1, H|1, Q, K]`` tensor.
+  fp32 ``[B|1, H|1, Q, K]`` tensor;
+* score modifiers     -- ``IdentityBias``, ``ConstantBias``, ``CausalAlibiBias``,
+  ``SymmetricAlibiBias``, ``DistanceDecayBias`` (additive, composable with
+  ``+`` / ``SumBias`` :553-582) and ``SoftCappingBias`` / ``PerHeadScaleBias``
+  (alone: the reference's SumBias gives every child the derivative 1,
+  :286-298).
 
 The kernels evaluate these in-kernel: ``lower_mask`` / ``lower_bias`` turn an
-object into the kernel's arguments (``causal``, per-batch ``kv_lengths``,
-static ``q_valid``/``kv_valid``, the bias tensor) and return ``None`` for
-anything the kernels cannot compute exactly, so that a route can fall
-through.  Objects from probjax itself are recognised by class name and
-fields, so the route can also be handed probjax's own mask objects.
+object into the kernel's arguments (``causal`` and its shift, per-batch
+``kv_lengths``, static ``q_valid``/``kv_valid``, window bounds, per-batch
+prefix / sequence lengths, segment ids, the bias tensor, the modifiers) and
+return ``None`` / ``False`` for anything the kernels cannot compute exactly,
+so that a route can fall through.  Objects from probjax itself are
+recognised by class name and fields, so the route can also be handed
+probjax's own mask objects.
 """
 
 from __future__ import annotations
@@ -44,7 +59,10 @@ class AttentionMask:
 
 
 class AttentionBias:
-    """Base class of additive score biases."""
+    """Base class of score biases; ``a + b`` composes (SumBias)."""
+
+    def __add__(self, other):
+        return SumBias(self, other)
 
 
 class NoMask(AttentionMask):
@@ -76,6 +94,48 @@ class ComposeMask(AttentionMask):
         self.op, self.lhs, self.rhs = op, lhs, rhs
 
 
+class CausalFromBottomRightMask(AttentionMask):
+    def __init__(self, q_length: int, kv_length: int):
+        self.q_length, self.kv_length = int(q_length), int(kv_length)
+
+
+class LocalWindowMask(AttentionMask):
+    def __init__(self, left_window: int, right_window: int | None = None):
+        self.left_window = int(left_window)
+        self.right_window = right_window
+
+
+class CausalLocalWindowMask(AttentionMask):
+    def __init__(self, left_window: int):
+        self.left_window = int(left_window)
+
+
+class PrefixLMMask(AttentionMask):
+    def __init__(self, prefix_lengths):
+        self.prefix_lengths = prefix_lengths
+
+
+class SeqLenMask(AttentionMask):
+    def __init__(self, seq_lengths):
+        self.seq_lengths = seq_lengths
+
+
+class SameSegmentMask(AttentionMask):
+    def __init__(self, query_segment_ids, key_segment_ids=None):
+        self.query_segment_ids = query_segment_ids
+        self.key_segment_ids = key_segment_ids
+
+
+class BlockDiagonalMask(AttentionMask):
+    def __init__(self, query_block_ids, key_block_ids=None):
+        self.query_block_ids = query_block_ids
+        self.key_block_ids = key_block_ids
+
+
+class BlockDiagonalCausalMask(BlockDiagonalMask):
+    pass
+
+
 class DenseBias(AttentionBias):
     def __init__(self, bias):
         if bias.ndim != 4:
@@ -83,36 +143,117 @@ class DenseBias(AttentionBias):
         self.bias = bias
 
 
+class SumBias(AttentionBias):
+    def __init__(self, lhs: AttentionBias, rhs: AttentionBias):
+        self.lhs, self.rhs = lhs, rhs
+
+
+class IdentityBias(AttentionBias):
+    pass
+
+
+class ConstantBias(AttentionBias):
+    def __init__(self, value: float):
+        self.value = float(value)
+
+
+class CausalAlibiBias(AttentionBias):
+    pass
+
+
+class SymmetricAlibiBias(AttentionBias):
+    pass
+
+
+class DistanceDecayBias(AttentionBias):
+    def __init__(self, alpha: float = 1.0):
+        self.alpha = float(alpha)
+
+
+class SoftCappingBias(AttentionBias):
+    def __init__(self, softcap: float = 20.0):
+        if softcap <= 0:
+            raise ValueError("softcap must be > 0")
+        self.softcap = float(softcap)
+
+
+class PerHeadScaleBias(AttentionBias):
+    def __init__(self, scales):
+        self.scales = scales
+
+
 def _name(obj) -> str:
     return type(obj).__name__
 
 
+_STATEFUL = ("KVLenMask", "PrefixLMMask", "SeqLenMask", "SameSegmentMask", "BlockDiagonalMask",
+             "BlockDiagonalCausalMask", "KeyPaddingMask")
+
+
 def _is_stateful(m) -> bool:
-    return _name(m) == "KVLenMask" or (
+    return _name(m) in _STATEFUL or (
         _name(m) == "ComposeMask" and (_is_stateful(m.lhs) or _is_stateful(m.rhs))
     )
 
 
+def _min_opt(a, b):
+    vals = [v for v in (a, b) if v is not None]
+    return min(vals) if vals else None
+
+
 @dataclass
 class LoweredMask:
-    """Kernel arguments of a mask: AND of causal, per-batch KV length and
-    static query / key lengths."""
+    """Kernel arguments of a mask: an AND of positional intervals (causal with
+    a shift, a window), per-batch KV / prefix / sequence lengths, segment ids
+    and static query / key lengths."""
 
-    causal: bool = False
+    causal_shift: int | None = None  # None: no causal bound; 0: CausalMask
     kv_lengths: object = None  # [B] int lengths (tensor, array or sequence) or None
     q_valid: int | None = None
     kv_valid: int | None = None
+    window_left: int | None = None
+    window_right: int | None = None
+    prefix_lengths: object = None  # scalar or [B]
+    seq_lengths: object = None  # [B]
+    segment_q: object = None  # [B, Lq] or [Lq]
+    segment_k: object = None  # [B, Lk] or [Lk] (None: the query ids)
+
+    @property
+    def causal(self) -> bool:
+        return self.causal_shift is not None
+
+    @property
+    def extended(self) -> bool:
+        """Needs the kernels' extended-mask path (anything beyond causal,
+        KV lengths and static lengths)."""
+        return (
+            (self.causal_shift not in (None, 0))
+            or self.window_left is not None
+            or self.window_right is not None
+            or self.prefix_lengths is not None
+            or self.seq_lengths is not None
+            or self.segment_q is not None
+        )
 
     def merge(self, other: "LoweredMask") -> "LoweredMask | None":
-        if self.kv_lengths is not None and other.kv_lengths is not None:
+        state = [
+            n for n in ("kv_lengths", "prefix_lengths", "seq_lengths", "segment_q")
+            for m in (self, other) if getattr(m, n) is not None
+        ]
+        if len(state) > 1:
             return None  # two stateful masks: not representable (and refused by ComposeMask)
-        qv = [v for v in (self.q_valid, other.q_valid) if v is not None]
-        kv = [v for v in (self.kv_valid, other.kv_valid) if v is not None]
+        pick = lambda n: getattr(self, n) if getattr(self, n) is not None else getattr(other, n)  # noqa: E731
         return LoweredMask(
-            causal=self.causal or other.causal,
-            kv_lengths=self.kv_lengths if self.kv_lengths is not None else other.kv_lengths,
-            q_valid=min(qv) if qv else None,
-            kv_valid=min(kv) if kv else None,
+            causal_shift=_min_opt(self.causal_shift, other.causal_shift),
+            kv_lengths=pick("kv_lengths"),
+            q_valid=_min_opt(self.q_valid, other.q_valid),
+            kv_valid=_min_opt(self.kv_valid, other.kv_valid),
+            window_left=_min_opt(self.window_left, other.window_left),
+            window_right=_min_opt(self.window_right, other.window_right),
+            prefix_lengths=pick("prefix_lengths"),
+            seq_lengths=pick("seq_lengths"),
+            segment_q=pick("segment_q"),
+            segment_k=pick("segment_k"),
         )
 
 
@@ -125,9 +266,29 @@ def lower_mask(mask) -> LoweredMask | None:
     if name == "NoMask":
         return LoweredMask()
     if name == "CausalMask":
-        return LoweredMask(causal=True)
+        return LoweredMask(causal_shift=0)
+    if name == "CausalFromBottomRightMask":
+        return LoweredMask(causal_shift=int(mask.kv_length) - int(mask.q_length))
+    if name == "LocalWindowMask":
+        rw = 0 if mask.right_window is None else int(mask.right_window)
+        if mask.left_window < 0 or rw < 0:
+            return None
+        return LoweredMask(window_left=int(mask.left_window), window_right=rw)
+    if name == "CausalLocalWindowMask":
+        if mask.left_window < 0:
+            return None
+        return LoweredMask(window_left=int(mask.left_window), window_right=0)
     if name == "KVLenMask":
         return LoweredMask(kv_lengths=mask.kv_lengths)
+    if name == "PrefixLMMask":
+        return LoweredMask(prefix_lengths=mask.prefix_lengths)
+    if name == "SeqLenMask":
+        return LoweredMask(seq_lengths=mask.seq_lengths)
+    if name == "SameSegmentMask":
+        return LoweredMask(segment_q=mask.query_segment_ids, segment_k=mask.key_segment_ids)
+    if name in ("BlockDiagonalMask", "BlockDiagonalCausalMask"):
+        return LoweredMask(segment_q=mask.query_block_ids, segment_k=mask.key_block_ids,
+                           causal_shift=0 if name == "BlockDiagonalCausalMask" else None)
     if name == "QKVLengthMask":
         return LoweredMask(q_valid=int(mask.q_length), kv_valid=int(mask.kv_length))
     if name == "ComposeMask" and getattr(mask, "op", None) == "and":
@@ -138,12 +299,66 @@ def lower_mask(mask) -> LoweredMask | None:
     return None
 
 
+@dataclass
+class LoweredBias:
+    """Kernel arguments of a bias: s' = f(s) + dense + alibi + constant with
+    f the soft cap, the per-head scale or the identity."""
+
+    dense: object = None  # [B|1, H|1, Q, K] tensor
+    alibi: str | None = None  # "causal" (2^-(h+1), relu), "symmetric" (2^-(h+1), |.|), "decay"
+    alibi_alpha: float = 1.0  # DistanceDecayBias
+    softcap: float = 0.0
+    head_scales: object = None  # [H|1]
+    constant: float = 0.0
+
+    @property
+    def extended(self) -> bool:
+        return (self.alibi is not None or self.softcap > 0 or self.head_scales is not None
+                or self.constant != 0.0)
+
+
+_ADDITIVE = ("DenseBias", "IdentityBias", "ConstantBias", "CausalAlibiBias", "SymmetricAlibiBias",
+             "DistanceDecayBias")
+
+
+def _flatten_sum(bias, out) -> bool:
+    name = _name(bias)
+    if name == "SumBias":
+        return _flatten_sum(bias.lhs, out) and _flatten_sum(bias.rhs, out)
+    if name not in _ADDITIVE:
+        return False
+    out.append(bias)
+    return True
+
+
 def lower_bias(bias):
-    """The dense fp32 bias tensor of ``bias`` (``None`` for no bias), or the
-    sentinel ``False`` when the kernels cannot add it exactly."""
+    """Kernel arguments of ``bias`` (``None`` for no bias), or the sentinel
+    ``False`` when the kernels cannot apply it exactly."""
     if bias is None:
         return None
-    if _name(bias) == "DenseBias":
-        b = bias.bias
-        return b if isinstance(b, torch.Tensor) else torch.as_tensor(b)
-    return False
+    name = _name(bias)
+    if name == "SoftCappingBias":
+        return LoweredBias(softcap=float(bias.softcap))
+    if name == "PerHeadScaleBias":
+        sc = bias.scales
+        return LoweredBias(head_scales=sc if isinstance(sc, torch.Tensor) else torch.as_tensor(sc))
+    parts = []
+    if not _flatten_sum(bias, parts):
+        return False
+    lb = LoweredBias()
+    for p in parts:
+        pn = _name(p)
+        if pn == "DenseBias":
+            if lb.dense is not None:
+                return False
+            b = p.bias
+            lb.dense = b if isinstance(b, torch.Tensor) else torch.as_tensor(b)
+        elif pn == "ConstantBias":
+            lb.constant += float(p.value)
+        elif pn in ("CausalAlibiBias", "SymmetricAlibiBias", "DistanceDecayBias"):
+            if lb.alibi is not None:
+                return False
+            lb.alibi = {"CausalAlibiBias": "causal", "SymmetricAlibiBias": "symmetric",
+                        "DistanceDecayBias": "decay"}[pn]
+            lb.alibi_alpha = float(getattr(p, "alpha", 1.0))
+    return lb

@@ -17,22 +17,45 @@ PJX_DTYPE_F32 = 0
 PJX_DTYPE_BF16 = 1
 PJX_OK = 0
 
+
+
+class ScoreMods(ctypes.Structure):
+    """``pjx_score_mods`` of include/probjax_hip.h (extended masks and score
+    modifiers; device pointers as integers, None for absent)."""
+
+    _fields_ = [
+        ("causal_shift", ctypes.c_int32),
+        ("window_left", ctypes.c_int32),
+        ("window_right", ctypes.c_int32),
+        ("prefix_lengths", ctypes.c_void_p),
+        ("seq_lengths", ctypes.c_void_p),
+        ("segment_q", ctypes.c_void_p),
+        ("segment_k", ctypes.c_void_p),
+        ("alibi_slopes", ctypes.c_void_p),
+        ("alibi_symmetric", ctypes.c_int32),
+        ("softcap", ctypes.c_float),
+        ("head_scales", ctypes.c_void_p),
+        ("constant", ctypes.c_float),
+    ]
+
+
 # (name, restype, argtypes) of every exported entry point.
 _P = ctypes.c_void_p
 _I64 = ctypes.c_int64
+_MODS = ctypes.POINTER(ScoreMods)
 _SIGNATURES = {
     "pjx_version": (ctypes.c_int, []),
     "pjx_last_error": (ctypes.c_char_p, []),
     "pjx_flash_fwd": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
-         _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _P],
+         _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _MODS, _P],
     ),
     "pjx_flash_bwd_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64]),
     "pjx_flash_bwd": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P, _P, _I64,
-         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _P],
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _MODS, _P],
     ),
     "pjx_decode_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64, _I64]),
     "pjx_splitkv_decode": (

@@ -42,16 +42,16 @@ def test_lower_mask_accepts_foreign_objects_by_name():
     assert M.lower_mask(CausalMask()).causal
     assert M.lower_mask(KVLenMask([2])).kv_lengths == [2]
 
-    class LocalWindowMask:
+    class MarginalizationMask:
         pass
 
-    assert M.lower_mask(LocalWindowMask()) is None
+    assert M.lower_mask(MarginalizationMask()) is None
 
 
 def test_lower_bias():
     b = torch.zeros(1, 2, 3, 4)
     assert M.lower_bias(None) is None
-    assert M.lower_bias(M.DenseBias(b)) is b
+    assert M.lower_bias(M.DenseBias(b)).dense is b
     assert M.lower_bias(object()) is False
     with pytest.raises(ValueError):
         M.DenseBias(torch.zeros(3, 4))
@@ -174,3 +174,50 @@ def test_splitkv_forward_num_splits_to_chunk(monkeypatch):
     with pytest.raises(ValueError):
         A.splitkv_forward(q, k, v, sm_scale=0.1, num_splits=0)
     assert np.isclose(A._SPLITKV_MIN_KV_LEN, 1024)
+
+
+def test_lower_extended_masks():
+    """Positional masks lower to intersected intervals; stateful ones carry data."""
+    lm = M.lower_mask(M.CausalMask() & M.LocalWindowMask(5, 2))
+    assert (lm.causal_shift, lm.window_left, lm.window_right) == (0, 5, 2) and lm.extended
+    lm = M.lower_mask(M.LocalWindowMask(4) & M.CausalLocalWindowMask(3))
+    assert (lm.window_left, lm.window_right) == (3, 0)
+    lm = M.lower_mask(M.CausalFromBottomRightMask(3, 10) & M.CausalMask())
+    assert lm.causal_shift == 0  # k <= q + 7 and k <= q  ->  k <= q
+    assert M.lower_mask(M.CausalFromBottomRightMask(3, 10)).causal_shift == 7
+    assert not M.lower_mask(M.CausalMask()).extended
+    lm = M.lower_mask(M.PrefixLMMask([2, 3]) & M.QKVLengthMask(5, 6))
+    assert lm.prefix_lengths == [2, 3] and lm.q_valid == 5 and not lm.causal
+    lm = M.lower_mask(M.BlockDiagonalCausalMask([0, 0, 1]))
+    assert lm.segment_q == [0, 0, 1] and lm.segment_k is None and lm.causal_shift == 0
+    assert M.lower_mask(M.SeqLenMask([3])).seq_lengths == [3]
+    with pytest.raises(ValueError):
+        M.SameSegmentMask([0]) & M.KVLenMask([1])
+    assert M.lower_mask(M.LocalWindowMask(-1)) is None
+
+
+def test_lower_score_modifiers():
+    lb = M.lower_bias(M.SymmetricAlibiBias() + M.ConstantBias(0.5) + M.ConstantBias(0.25) + M.IdentityBias())
+    assert lb.alibi == "symmetric" and lb.constant == 0.75 and lb.dense is None and lb.extended
+    lb = M.lower_bias(M.DistanceDecayBias(0.3) + M.DenseBias(torch.zeros(1, 1, 2, 2)))
+    assert lb.alibi == "decay" and lb.alibi_alpha == 0.3 and lb.dense is not None
+    assert M.lower_bias(M.SoftCappingBias(30.0)).softcap == 30.0
+    assert M.lower_bias(M.PerHeadScaleBias([1.0, 2.0])).head_scales.tolist() == [1.0, 2.0]
+    # a non-additive modifier inside a sum, two dense biases, two ALiBi terms: not taken
+    assert M.lower_bias(M.SoftCappingBias(5.0) + M.ConstantBias(1.0)) is False
+    d = M.DenseBias(torch.zeros(1, 1, 2, 2))
+    assert M.lower_bias(d + d) is False
+    assert M.lower_bias(M.CausalAlibiBias() + M.SymmetricAlibiBias()) is False
+
+
+def test_score_mods_arguments():
+    lm = M.lower_mask(M.CausalFromBottomRightMask(4, 6) & M.SameSegmentMask([0, 0, 1, 1]))
+    # segment ids per position: the key ids default to the query ids, so Lq == Lk is needed
+    assert A._score_mods(lm, None, 2, 4, 6, 3, "cpu") is False
+    lm = M.lower_mask(M.CausalFromBottomRightMask(4, 4) & M.SameSegmentMask([0, 0, 1, 1]))
+    m = A._score_mods(lm, M.lower_bias(M.CausalAlibiBias()), 2, 4, 4, 3, "cpu")
+    assert m.causal_shift == 0 and m.segment_q.shape == (2, 4) and m.segment_k.dtype == torch.int32
+    assert torch.allclose(m.alibi_slopes, torch.tensor([0.5, 0.25, 0.125])) and not m.alibi_symmetric
+    m = A._score_mods(M.lower_mask(M.PrefixLMMask(3)), M.lower_bias(M.PerHeadScaleBias([2.0])), 2, 4, 4, 3, "cpu")
+    assert m.prefix_lengths.tolist() == [3, 3] and m.head_scales.tolist() == [2.0, 2.0, 2.0]
+    assert A._score_mods(M.lower_mask(M.CausalMask()), None, 1, 4, 4, 1, "cpu") is None

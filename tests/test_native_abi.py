@@ -46,7 +46,7 @@ def test_version_and_error_string(lib):
 def _flash_args(**over):
     a = dict(dtype=native.PJX_DTYPE_BF16, q=1, k=1, v=1, o=1, lse=None, kvl=None, bias=None,
              bb=1, bh=1, B=1, Lq=16, Lk=16, Hq=2, Hkv=1, D=128, qv=16, kv=16, causal=1,
-             scale=0.1, stream=None)
+             scale=0.1, mods=None, stream=None)
     a.update(over)
     return list(a.values())
 
@@ -67,6 +67,52 @@ def test_flash_rejects_invalid_arguments(lib, over, msg):
     rc = lib.pjx_flash_fwd(*_flash_args(**over))
     assert rc == 1
     assert msg in lib.pjx_last_error().decode()
+
+
+@pytest.mark.parametrize(
+    "fields,msg",
+    [
+        (dict(softcap=-1.0), "softcap"),
+        (dict(softcap=5.0, head_scales=1), "exclude"),
+        (dict(segment_q=1), "segment_q and segment_k"),
+        (dict(window_left=0x3FFFFFFF), "out of range"),
+    ],
+)
+def test_flash_rejects_invalid_score_mods(lib, fields, msg):
+    m = native.ScoreMods(**{"window_left": -1, "window_right": -1, **fields})
+    for fn, args in (("pjx_flash_fwd", _flash_args(mods=ctypes.pointer(m))),
+                     ("pjx_flash_bwd", _bwd_args(mods=ctypes.pointer(m)))):
+        assert getattr(lib, fn)(*args) == 1, fn
+        assert msg in lib.pjx_last_error().decode(), fn
+
+
+def _bwd_args(**over):
+    a = dict(dtype=native.PJX_DTYPE_BF16, q=1, k=1, v=1, o=1, do=1, lse=1, dq=1, dk=1, dv=1,
+             ws=1, ws_bytes=1 << 20, kvl=None, bias=None, bb=1, bh=1, B=1, Lq=16, Lk=16, Hq=2,
+             Hkv=1, D=128, qv=16, kv=16, causal=1, scale=0.1, mods=None, stream=None)
+    a.update(over)
+    return list(a.values())
+
+
+@pytest.mark.parametrize(
+    "over,msg,code",
+    [
+        (dict(dtype=7), "dtype", 1),
+        (dict(do=None), "non-null", 1),
+        (dict(D=96), "head_dim", 1),
+        (dict(Hq=3, Hkv=2), "multiple of kv_heads", 1),
+        (dict(ws=None), "workspace", 3),
+        (dict(ws_bytes=16), "workspace", 3),
+    ],
+)
+def test_flash_bwd_rejects_invalid_arguments(lib, over, msg, code):
+    assert lib.pjx_flash_bwd(*_bwd_args(**over)) == code
+    assert msg in lib.pjx_last_error().decode()
+
+
+def test_flash_bwd_workspace_size(lib):
+    assert lib.pjx_flash_bwd_workspace_size(2, 3, 5) == 8 * 2 * 3 * 5
+    assert lib.pjx_flash_bwd_workspace_size(0, 3, 5) == 0
 
 
 def test_flash_empty_batch_is_a_no_op(lib):
