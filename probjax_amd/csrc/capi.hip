@@ -66,10 +66,10 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) 
   m.softcap = mods->softcap;
   m.head_scale = mods->head_scales;
   m.constant = mods->constant;
-  a.ext = (m.causal_shift != 0 || m.win_left != kNoBound || m.win_right != kNoBound || m.prefix ||
-           m.seqlen || m.seg_q || m.alibi || m.softcap > 0.f || m.head_scale || m.constant != 0.f)
-              ? 1
-              : 0;
+  const bool full = m.seg_q || m.alibi || m.softcap > 0.f || m.head_scale || m.constant != 0.f;
+  const bool intervals = m.causal_shift != 0 || m.win_left != kNoBound || m.win_right != kNoBound ||
+                         m.prefix || m.seqlen;
+  a.ext = full ? 2 : intervals ? 1 : 0;
   return PJX_OK;
 }
 

@@ -114,7 +114,7 @@ __device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x 
 // ---------------------------------------------------------------------------
 // dQ (and delta): one workgroup per (128-query tile, batch, head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
@@ -123,7 +123,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[2 * TILE_B];
 
   BlockGeom g = block_geom(a);
-  if constexpr (EXT) ext_block_range(a, g, BK);
+  if constexpr (EXT > 0) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   g.qw = __builtin_amdgcn_readfirstlane(g.qw);
@@ -174,9 +174,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
-  if constexpr (EXT) er = ext_rows(a, g);
+  if constexpr (EXT > 0) er = ext_rows(a, g);
 
   uint32_t voff[T::NLD];
 #pragma unroll
@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 
   auto compute = [&](int t, const unsigned char* ks) {
     const int k0 = (t_begin + t) * BK;
-    if constexpr (EXT) {
+    if constexpr (EXT > 0) {
       if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
     } else {
       if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         dp[kb] = mfma32x32x16(vf, dof[st], dp[kb]);
       }
     }
-    if constexpr (EXT) {
+    if constexpr (EXT == 2) {
       // modified scores, masks, P and dS = P (dP - delta) * scale * f'(s)
       ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
                                    [&](int kb, int r, float x, float gg) {
@@ -256,8 +256,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
           for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
         }
     }
-    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                           (g.qw + 31 >= g.q_hi);
+    if constexpr (EXT == 1) ext_mask_sT<BK / 32>(g, er, s, k0, half);
+    const bool need_mask = EXT == 0 && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                        (g.qw + 31 >= g.q_hi));
     if (need_mask) {
       const int base = k0 + 4 * half;
       int lim = g.kv_end - 1 - base;
@@ -319,7 +320,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 // ---------------------------------------------------------------------------
 // dK, dV: one workgroup per (128-key tile, batch, KV head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
@@ -350,7 +351,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
   int q_begin = a.causal ? (k0 / kBQs) * kBQs : 0;
   int q_end = q_hi;
   int qlo = 0, qhi = q_hi - 1, wq_first = 0, wq_last = q_hi - 1, segk = 0;
-  if constexpr (EXT) {
+  int qhi_first = q_hi - 1, qlo_last = 0;  // rows seen by every key of the wave: [qlo_last, qhi_first]
+  if constexpr (EXT > 0) {
     q_end = q_begin = 0;
     if (k0 < kv_end) {
       int a0, a1, b0, b1;
@@ -361,9 +363,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
     }
     key_bounds(a.m, a.causal, b, kv_end, q_hi, key, qlo, qhi);
     if (kw < kv_end) {
-      int c0, c1;
-      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, c1);
-      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, c0, wq_last);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, qhi_first);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, qlo_last, wq_last);
     }
     if (a.m.seg_k && key < a.Lk) segk = a.m.seg_k[(size_t)b * a.Lk + key];
   }
@@ -388,7 +389,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
       vf[s] = as_bf16x8(rv);
     }
   }
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   const uint32_t rowstride = (uint32_t)a.Hq * D * 2;
 
   uint32_t voff[T::NLD];
@@ -443,8 +444,10 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
     for (int qb = 0; qb < kBQs / 32; ++qb) {
       const int qs0 = q0 + 32 * qb;
       if (qs0 >= q_hi || kw >= kv_end) continue;
-      if constexpr (EXT) {
+      if constexpr (EXT > 0) {
         if (qs0 > wq_last || qs0 + 31 < wq_first) continue;  // no row of this step sees the wave's keys
+      }
+      if constexpr (EXT == 2) {
         // S = Q K^T and dP = dO V^T first, then one pass: modified score,
         // mask, P and dS = P (dP - delta) * scale * f'(s).
         f32x16 sx = f32x16{}, dpx = f32x16{};
@@ -478,7 +481,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
         }
         continue;
       }
-      if (a.causal && qs0 + 31 < kw) continue;  // every query before this wave's first key
+      if (EXT == 0 && a.causal && qs0 + 31 < kw) continue;  // every query before this wave's first key
 
       // S[query][key] = Q K^T: register r holds query qs0 + 8*(r/4) + 4*half + r%4
       // of key `key`.
@@ -496,7 +499,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
           s[r] = fmaf(s[r], a.scale, bv);
         }
       }
-      const bool need_mask = (a.causal && qs0 < kw + 31) || (kw + 32 > kv_end) || (qs0 + 32 > q_hi);
+      if constexpr (EXT == 1)
+        ext_mask_S(s, qs0, half, qlo, qhi, !(kw + 31 < kv_end && qs0 >= qlo_last && qs0 + 31 <= qhi_first));
+      const bool need_mask = EXT == 0 && ((a.causal && qs0 < kw + 31) || (kw + 32 > kv_end) || (qs0 + 32 > q_hi));
       if (need_mask) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
@@ -585,7 +590,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
 // tile.  Tiles are staged through registers into LDS rows padded to D + 4
 // floats (16-byte reads of 16 consecutive rows hit distinct banks).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   constexpr int BK = (D == 128) ? 32 : 64;
@@ -597,7 +602,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
   __shared__ __attribute__((aligned(16))) float v_lds[2][BK * KS];
 
   BlockGeom g = block_geom(a);
-  if constexpr (EXT) ext_block_range(a, g, BK);
+  if constexpr (EXT > 0) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
   const size_t kv_row = (size_t)a.Hkv * D;
@@ -645,9 +650,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
-  if constexpr (EXT) er = ext_rows(a, g);
+  if constexpr (EXT > 0) er = ext_rows(a, g);
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -683,7 +688,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
 
   auto compute = [&](int t, int buf) {
     const int k0 = (t_begin + t) * BK;
-    if constexpr (EXT) {
+    if constexpr (EXT > 0) {
       if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
     } else {
       if (a.causal && k0 > q_last_w) return;
@@ -708,7 +713,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
         }
       }
     }
-    if constexpr (EXT) {
+    if constexpr (EXT == 2) {
       ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
                                    [&](int kb, int r, float x, float gg) {
                                      const float p = fast_exp2(fmaf(x, cx, -lse2));
@@ -727,8 +732,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
           for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
         }
     }
-    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                           (g.qw + 31 >= g.q_hi);
+    if constexpr (EXT == 1) ext_mask_sT<BK / 32>(g, er, s, k0, half);
+    const bool need_mask = EXT == 0 && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                        (g.qw + 31 >= g.q_hi));
     if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -785,7 +791,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
   }
 }
 
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   constexpr int BQ = 32;  // queries per stage (one 32-query step)
@@ -813,7 +819,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   int q_begin = a.causal ? (k0 / BQ) * BQ : 0;
   int q_end = q_hi;
   int qlo = 0, qhi = q_hi - 1, wq_first = 0, wq_last = q_hi - 1, segk = 0;
-  if constexpr (EXT) {
+  int qhi_first = q_hi - 1, qlo_last = 0;  // rows seen by every key of the wave: [qlo_last, qhi_first]
+  if constexpr (EXT > 0) {
     q_end = q_begin = 0;
     if (k0 < kv_end) {
       int a0, a1, b0, b1;
@@ -824,9 +831,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
     }
     key_bounds(a.m, a.causal, b, kv_end, q_hi, key, qlo, qhi);
     if (kw < kv_end) {
-      int c0, c1;
-      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, c1);
-      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, c0, wq_last);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, qhi_first);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 32, kv_end) - 1, qlo_last, wq_last);
     }
     if (a.m.seg_k && key < a.Lk) segk = a.m.seg_k[(size_t)b * a.Lk + key];
   }
@@ -853,7 +859,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
       }
     }
   }
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   const size_t q_row = (size_t)a.Hq * D;
 
   f32x16 acck[D / 32], accv[D / 32];
@@ -903,7 +909,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   auto compute = [&](int t, int buf) {
     const int h = tile_head(t), q0 = tile_q0(t);
     if (q0 >= q_hi || kw >= kv_end) return;
-    if constexpr (EXT) {
+    if constexpr (EXT > 0) {
       if (q0 > wq_last || q0 + BQ - 1 < wq_first) return;  // no row of this step sees the wave's keys
     } else {
       if (a.causal && q0 + BQ - 1 < kw) return;  // every query before this wave's first key
@@ -929,7 +935,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
       }
     }
     f32x16 ds;
-    if constexpr (EXT) {
+    if constexpr (EXT == 2) {
       const float* bbase = nullptr;
       if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
       const HeadMods hm = head_mods(a.m, h);
@@ -950,7 +956,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
         s[r] = fmaf(s[r], a.scale, bv);
       }
     }
-    const bool need_mask = (a.causal && q0 < kw + 31) || (kw + 32 > kv_end) || (q0 + BQ > q_hi);
+    if constexpr (EXT == 1)
+      ext_mask_S(s, q0, half, qlo, qhi, !(kw + 31 < kv_end && q0 >= qlo_last && q0 + BQ - 1 <= qhi_first));
+    const bool need_mask = EXT == 0 && ((a.causal && q0 < kw + 31) || (kw + 32 > kv_end) || (q0 + BQ > q_hi));
     if (need_mask) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -1027,7 +1035,7 @@ static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
 
 // dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
 // dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
-template <int D, bool EXT>
+template <int D, int EXT>
 static int run_bwd_t(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
     int rc;
@@ -1047,7 +1055,8 @@ static int run_bwd_t(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
 
 template <int D>
 static int run_bwd(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
-  return a.f.ext ? run_bwd_t<D, true>(a, f32, hb, s) : run_bwd_t<D, false>(a, f32, hb, s);
+  if (a.f.ext == 2) return run_bwd_t<D, 2>(a, f32, hb, s);
+  return a.f.ext == 1 ? run_bwd_t<D, 1>(a, f32, hb, s) : run_bwd_t<D, 0>(a, f32, hb, s);
 }
 
 }  // namespace pjx

@@ -23,7 +23,7 @@ struct FlashArgs {
   int q_valid, kv_valid, causal;
   float scale;
   int n_qtiles;
-  int ext;      // extended masks / score modifiers in `m` are active
+  int ext;      // 0: none; 1: interval masks in `m`; 2: also segment ids / score modifiers
   ScoreMods m;
 };
 
@@ -188,7 +188,42 @@ __device__ __forceinline__ void ext_scores_sT(const FlashArgs& a, const BlockGeo
         const bool keep = kj >= er.lo && kj <= er.hi && (!a.m.seg_q || sgv[j] == er.segq);
         emit(kb, r, keep ? x : -INFINITY, gg);
       }
+      // one group of 4 keys at a time: keeps the loads and temporaries of
+      // the groups from piling up in registers
+      __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// Interval masks only (the positional masks; no segment ids or modifiers)
+// in the S^T layout: scores outside this row's key interval become -inf.
+// Tiles inside the interval of every row of the wave are left alone.
+template <int NKB>
+__device__ __forceinline__ void ext_mask_sT(const BlockGeom& g, const ExtRows& er, f32x16* s, int k0,
+                                            int half) {
+  constexpr int BK = NKB * 32;
+  if (k0 >= er.lo_last && k0 + BK - 1 <= er.hi_first && g.qw + 31 < g.q_hi) return;
+  const int base = k0 + 4 * half;
+  const int lo = er.lo - base, hi = er.hi - base;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int o = kb * 32 + 8 * (r >> 2) + (r & 3);
+      if (o < lo || o > hi) s[kb][r] = -INFINITY;
+    }
+}
+
+// The same in the S layout (lane = key with query rows [qlo, qhi]; register
+// r = query qs0 + 8*(r/4) + 4*half + r%4); `need` false skips the step.
+__device__ __forceinline__ void ext_mask_S(f32x16& s, int qs0, int half, int qlo, int qhi, bool need) {
+  if (!need) return;
+  const int base = qs0 + 4 * half;
+  const int lo = qlo - base, hi = qhi - base;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int o = 8 * (r >> 2) + (r & 3);
+    if (o < lo || o > hi) s[r] = -INFINITY;
+  }
 }
 
 // The same in the S layout of the dK/dV kernels (lane = key `key`, register
@@ -215,6 +250,7 @@ __device__ __forceinline__ void ext_scores_S(const FlashArgs& a, int b, const He
       const bool keep = qr >= qlo && qr <= qhi && (!a.m.seg_q || sgv[j] == segk);
       emit(r, keep ? x : -INFINITY, gg);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 

@@ -61,7 +61,7 @@ namespace pjx {
 // ---------------------------------------------------------------------------
 
 
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
   using T = Bf16Tile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
@@ -72,7 +72,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
 
   BlockGeom g = block_geom(a);
-  if constexpr (EXT) ext_block_range(a, g, BK);
+  if constexpr (EXT > 0) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   // Wave index and the wave's first row as wave-uniform (scalar) values, so
   // that branches on them are scalar branches.
@@ -105,9 +105,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   const bool bias_vec = (a.Lk & 3) == 0;
   // score units -> log2 units (the scale is applied to the score itself when
   // a bias or modifier is added to it)
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
-  if constexpr (EXT) er = ext_rows(a, g);
+  if constexpr (EXT > 0) er = ext_rows(a, g);
 
   // Per-lane byte offsets, fixed for the whole key loop.
   uint32_t voffK[T::NLD], voffV[T::NLD];
@@ -156,7 +156,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 
   auto compute = [&](int t, const unsigned char* ks) {
     const int k0 = (t_begin + t) * BK;
-    if constexpr (EXT) {
+    if constexpr (EXT > 0) {
       // tile outside every row of this wave
       if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
     } else {
@@ -177,9 +177,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     }
 
     // Register r of block kb holds key k0 + kb*32 + 8*(r/4) + 4*half + r%4.
-    if constexpr (EXT) {
+    if constexpr (EXT == 2) {
       ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
-                                       [&](int kb, int r, float x, float) { s[kb][r] = x; });
+                                   [&](int kb, int r, float x, float) { s[kb][r] = x; });
     } else if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb) {
@@ -193,8 +193,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
         }
       }
     }
-    const bool need_mask = !EXT && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                                    (g.qw + 31 >= g.q_hi));
+    if constexpr (EXT == 1) ext_mask_sT<BK / 32>(g, er, s, k0, half);
+    const bool need_mask = EXT == 0 && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                        (g.qw + 31 >= g.q_hi));
     if (need_mask) {
       // Key k0 + 4*half + o (o = kb*32 + 8*(r/4) + r%4) is kept iff o <= lim.
       const int base = k0 + 4 * half;
@@ -303,7 +304,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 // P.V the step pairs key (r, half 0) with key (r, half 1) of the S^T layout,
 // so V is read in its natural [key][dim] layout: no transpose needed.
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, bool EXT>
+template <int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a) {
   constexpr int BK = (D == 128) ? 32 : 64;
   constexpr int KS = D + 4;  // floats; b128 reads of 16 rows hit distinct banks
@@ -316,7 +317,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
   __shared__ __attribute__((aligned(16))) float v_lds[2][BK * VS];
 
   BlockGeom g = block_geom(a);
-  if constexpr (EXT) ext_block_range(a, g, BK);
+  if constexpr (EXT > 0) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
   const int col = lane & 31, half = lane >> 5;
   const size_t kv_row = (size_t)a.Hkv * D;
@@ -343,9 +344,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = (BIAS || EXT) ? kLog2e : a.scale * kLog2e;
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
-  if constexpr (EXT) er = ext_rows(a, g);
+  if constexpr (EXT > 0) er = ext_rows(a, g);
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -382,7 +383,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
 
   auto compute = [&](int t, int buf) {
     const int k0 = (t_begin + t) * BK;
-    if constexpr (EXT) {
+    if constexpr (EXT > 0) {
       if (!er.any || k0 > er.hi_last || k0 + BK - 1 < er.lo_first) return;
     } else {
       if (a.causal && k0 > q_last_w) return;
@@ -401,9 +402,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
         for (int j = 0; j < 4; ++j) s[kb] = mfma32x32x2f32(kf[j], qf[4 * st4 + j], s[kb]);
       }
     }
-    if constexpr (EXT) {
+    if constexpr (EXT == 2) {
       ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
-                                       [&](int kb, int r, float x, float) { s[kb][r] = x; });
+                                   [&](int kb, int r, float x, float) { s[kb][r] = x; });
     } else if constexpr (BIAS) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -416,8 +417,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_f32_kernel(FlashArgs a)
           for (int j = 0; j < 4; ++j) s[kb][4 * gq + j] = fmaf(s[kb][4 * gq + j], a.scale, bv[j]);
         }
     }
-    const bool need_mask = !EXT && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
-                                    (g.qw + 31 >= g.q_hi));
+    if constexpr (EXT == 1) ext_mask_sT<BK / 32>(g, er, s, k0, half);
+    const bool need_mask = EXT == 0 && ((k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) ||
+                                        (g.qw + 31 >= g.q_hi));
     if (need_mask) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
@@ -749,15 +751,23 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
   if (a.ext) {
-    // Extended masks / score modifiers: the one-pass kernels' EXT variants.
+    // Extended masks / score modifiers: the one-pass kernels' EXT variants
+    // (1: interval masks, 2: segment ids / score modifiers as well).
+    const bool full = a.ext == 2;
     if (dtype == PJX_DTYPE_BF16) {
-      if (head_dim == 128)
-        return hb ? launch(flash_fwd_bf16_kernel<128, true, true>, a, s) : launch(flash_fwd_bf16_kernel<128, false, true>, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<64, true, true>, a, s) : launch(flash_fwd_bf16_kernel<64, false, true>, a, s);
+      if (head_dim == 128) {
+        if (full) return hb ? launch(flash_fwd_bf16_kernel<128, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 2>, a, s);
+        return hb ? launch(flash_fwd_bf16_kernel<128, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 1>, a, s);
+      }
+      if (full) return hb ? launch(flash_fwd_bf16_kernel<64, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 2>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<64, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 1>, a, s);
     }
-    if (head_dim == 128)
-      return hb ? launch(flash_fwd_f32_kernel<128, true, true>, a, s) : launch(flash_fwd_f32_kernel<128, false, true>, a, s);
-    return hb ? launch(flash_fwd_f32_kernel<64, true, true>, a, s) : launch(flash_fwd_f32_kernel<64, false, true>, a, s);
+    if (head_dim == 128) {
+      if (full) return hb ? launch(flash_fwd_f32_kernel<128, true, 2>, a, s) : launch(flash_fwd_f32_kernel<128, false, 2>, a, s);
+      return hb ? launch(flash_fwd_f32_kernel<128, true, 1>, a, s) : launch(flash_fwd_f32_kernel<128, false, 1>, a, s);
+    }
+    if (full) return hb ? launch(flash_fwd_f32_kernel<64, true, 2>, a, s) : launch(flash_fwd_f32_kernel<64, false, 2>, a, s);
+    return hb ? launch(flash_fwd_f32_kernel<64, true, 1>, a, s) : launch(flash_fwd_f32_kernel<64, false, 1>, a, s);
   }
   if (dtype == PJX_DTYPE_BF16) {
     // Dense bias with 16-byte aligned rows and 32-bit slice offsets: the LDS
@@ -765,10 +775,10 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
     const bool ring = hb && kv_len % 4 == 0 && q_len * kv_len * 4 < ((int64_t)1 << 31);
     if (head_dim == 128) {
       if (ring) return launch_flash_bias_ring(128, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<128, true, false>, a, s) : launch(flash_fwd_bf16_kernel<128, false, false>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<128, true, 0>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 0>, a, s);
     }
     if (ring) return launch_flash_bias_ring(64, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<64, true, false>, a, s) : launch(flash_fwd_bf16_kernel<64, false, false>, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<64, true, 0>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 0>, a, s);
   }
   // fp32 with fewer 128-row workgroups than CUs: split each query block's
   // keys over several waves (latency-bound sizes, like the reference's CPU
@@ -780,6 +790,6 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
     return hb ? launch_split<64>(flash_fwd_f32_split_kernel<64, true>, a, s)
               : launch_split<64>(flash_fwd_f32_split_kernel<64, false>, a, s);
   }
-  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true, false>, a, s) : launch(flash_fwd_f32_kernel<128, false, false>, a, s);
-  return hb ? launch(flash_fwd_f32_kernel<64, true, false>, a, s) : launch(flash_fwd_f32_kernel<64, false, false>, a, s);
+  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true, 0>, a, s) : launch(flash_fwd_f32_kernel<128, false, 0>, a, s);
+  return hb ? launch(flash_fwd_f32_kernel<64, true, 0>, a, s) : launch(flash_fwd_f32_kernel<64, false, 0>, a, s);
 }
