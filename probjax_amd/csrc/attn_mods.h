@@ -117,10 +117,13 @@ __device__ __forceinline__ HeadMods head_mods(const ScoreMods& m, int h) {
 }
 
 // Modified score of s = sm_scale * q.k plus `add` (the dense bias), for
-// query q and key k; g receives d(modified)/d(s).
+// query q and key k; g receives d(modified)/d(s).  Branch-free per score:
+// an absent ALiBi term has slope 0, an absent head scale is 1; the soft cap
+// is chosen per tile (SOFTCAP).
+template <bool SOFTCAP>
 __device__ __forceinline__ float modify_score(const ScoreMods& m, const HeadMods& hm, float s,
                                               float add, int q, int k, float& g) {
-  if (m.softcap > 0.f) {
+  if constexpr (SOFTCAP) {
     // tanh(x) = sign(x) * (1 - 2 / (1 + e^{2|x|})); e^{2|x|} -> inf gives 1.
     const float x = s * (1.f / m.softcap);
     const float e = __builtin_amdgcn_exp2f(2.f * 1.4426950408889634f * fabsf(x));
@@ -131,11 +134,9 @@ __device__ __forceinline__ float modify_score(const ScoreMods& m, const HeadMods
     s *= hm.hscale;
     g = hm.hscale;
   }
-  if (m.alibi) {
-    const int d = q - k;
-    s -= hm.slope * (float)(m.alibi_sym ? abs(d) : max(d, 0));
-  }
-  return s + add + m.constant;
+  const int d = q - k;
+  const int f = m.alibi_sym ? abs(d) : max(d, 0);
+  return fmaf(-hm.slope, (float)f, s) + add + m.constant;
 }
 
 }  // namespace pjx

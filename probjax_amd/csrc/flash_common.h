@@ -107,14 +107,16 @@ __device__ __forceinline__ ExtRows ext_rows(const FlashArgs& a, const BlockGeom&
   return e;
 }
 
-// Segment ids of 4 consecutive keys kk .. kk+3 of batch b (0 past Lk).
-__device__ __forceinline__ int4 seg4(const int32_t* seg, int b, int kk, int Lk) {
-  const int32_t* p = seg + (size_t)b * Lk;
+// Segment ids of 4 consecutive positions kk .. kk+3 (kk a multiple of 4) of
+// batch b in ids [B, L] (0 past L).
+__device__ __forceinline__ int4 seg4(const int32_t* seg, int b, int kk, int L) {
+  const int32_t* p = seg + (size_t)b * L;
+  if ((L & 3) == 0 && kk + 3 < L) return *(const int4*)(p + kk);
   int4 r;
-  r.x = kk < Lk ? p[kk] : 0;
-  r.y = kk + 1 < Lk ? p[kk + 1] : 0;
-  r.z = kk + 2 < Lk ? p[kk + 2] : 0;
-  r.w = kk + 3 < Lk ? p[kk + 3] : 0;
+  r.x = kk < L ? p[kk] : 0;
+  r.y = kk + 1 < L ? p[kk + 1] : 0;
+  r.z = kk + 2 < L ? p[kk + 2] : 0;
+  r.w = kk + 3 < L ? p[kk + 3] : 0;
   return r;
 }
 
@@ -163,8 +165,8 @@ namespace pjx {
 // query g.qi; register r of block kb = key k0 + kb*32 + 8*(r/4) + 4*half +
 // r%4).  For every raw score q.k, emit(kb, r, x, g) receives the modified
 // score x (-inf where masked) and the modifier's derivative g.
-template <int NKB, bool BIAS, typename Emit>
-__device__ __forceinline__ void ext_scores_sT(const FlashArgs& a, const BlockGeom& g,
+template <int NKB, bool BIAS, bool SOFTCAP, typename Emit>
+__device__ __forceinline__ void ext_scores_sT_t(const FlashArgs& a, const BlockGeom& g,
                                               const ExtRows& er, const f32x16* s, int k0, int half,
                                               const float* brow, bool row_in, Emit emit) {
   const bool bias_vec = (a.Lk & 3) == 0;
@@ -184,7 +186,7 @@ __device__ __forceinline__ void ext_scores_sT(const FlashArgs& a, const BlockGeo
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * gq + j, kj = kk + j;
         float gg;
-        const float x = modify_score(a.m, er.hm, s[kb][r] * a.scale, bv[j], g.qi, kj, gg);
+        const float x = modify_score<SOFTCAP>(a.m, er.hm, s[kb][r] * a.scale, bv[j], g.qi, kj, gg);
         const bool keep = kj >= er.lo && kj <= er.hi && (!a.m.seg_q || sgv[j] == er.segq);
         emit(kb, r, keep ? x : -INFINITY, gg);
       }
@@ -230,8 +232,8 @@ __device__ __forceinline__ void ext_mask_S(f32x16& s, int qs0, int half, int qlo
 // r = query qs0 + 8*(r/4) + 4*half + r%4); [qlo, qhi] are the rows that see
 // `key`, segk its segment id, bbase the bias slice of (b, h).
 // emit(r, x, g) as above.
-template <bool BIAS, typename Emit>
-__device__ __forceinline__ void ext_scores_S(const FlashArgs& a, int b, const HeadMods& hm, int key,
+template <bool BIAS, bool SOFTCAP, typename Emit>
+__device__ __forceinline__ void ext_scores_S_t(const FlashArgs& a, int b, const HeadMods& hm, int key,
                                              int qlo, int qhi, int segk, const f32x16& s, int qs0,
                                              int half, const float* bbase, Emit emit) {
 #pragma unroll
@@ -246,12 +248,33 @@ __device__ __forceinline__ void ext_scores_S(const FlashArgs& a, int b, const He
       float bv = 0.f;
       if constexpr (BIAS) bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
       float gg;
-      const float x = modify_score(a.m, hm, s[r] * a.scale, bv, qr, key, gg);
+      const float x = modify_score<SOFTCAP>(a.m, hm, s[r] * a.scale, bv, qr, key, gg);
       const bool keep = qr >= qlo && qr <= qhi && (!a.m.seg_q || sgv[j] == segk);
       emit(r, keep ? x : -INFINITY, gg);
     }
     __builtin_amdgcn_sched_barrier(0);
   }
+}
+
+// The soft cap (two transcendentals per score) is chosen once per tile.
+template <int NKB, bool BIAS, typename Emit>
+__device__ __forceinline__ void ext_scores_sT(const FlashArgs& a, const BlockGeom& g,
+                                              const ExtRows& er, const f32x16* s, int k0, int half,
+                                              const float* brow, bool row_in, Emit emit) {
+  if (a.m.softcap > 0.f)
+    ext_scores_sT_t<NKB, BIAS, true>(a, g, er, s, k0, half, brow, row_in, emit);
+  else
+    ext_scores_sT_t<NKB, BIAS, false>(a, g, er, s, k0, half, brow, row_in, emit);
+}
+
+template <bool BIAS, typename Emit>
+__device__ __forceinline__ void ext_scores_S(const FlashArgs& a, int b, const HeadMods& hm, int key,
+                                             int qlo, int qhi, int segk, const f32x16& s, int qs0,
+                                             int half, const float* bbase, Emit emit) {
+  if (a.m.softcap > 0.f)
+    ext_scores_S_t<BIAS, true>(a, b, hm, key, qlo, qhi, segk, s, qs0, half, bbase, emit);
+  else
+    ext_scores_S_t<BIAS, false>(a, b, hm, key, qlo, qhi, segk, s, qs0, half, bbase, emit);
 }
 
 }  // namespace pjx
