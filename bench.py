@@ -117,7 +117,7 @@ def make_c1(dev, gen):
     nbytes = 4 * B * L * H * D * 4
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, causal=True)  # noqa: E731
     return dict(name="C1 causal fwd f32 B=1 H=4 L=512 D=64", fn=fn, flop=flop, bytes=nbytes,
-                bound="latency", dtype="f32", kernel="flash_fwd_f32_kernel<64,false>")
+                bound="latency", dtype="f32", kernel="flash_fwd_f32_split_kernel<64,false>")
 
 
 def make_c2(dev, gen):
@@ -130,7 +130,7 @@ def make_c2(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="C2 causal fwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_kernel<128,false>")
+                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_kernel<128,false,0>")
 
 
 def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
@@ -178,7 +178,7 @@ def make_c4(dev, gen):
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, kv_lengths=L_, bias=bias)  # noqa: E731
     return dict(name="C4 bias+kvlen fwd bf16 B=2 H=8 L=2048 D=64, bias f32 [8,2048,2048]",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="flash_fwd_bf16_kernel<64,true>")
+                kernel="flash_fwd_bf16_bias_ring_kernel<64>")
 
 
 def make_c5(dev, gen):
@@ -194,7 +194,7 @@ def make_c5(dev, gen):
     fn = lambda: mla_decode(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, workspace=ws)  # noqa: E731
     return dict(name="C5 MLA absorbed decode bf16 B=16 H=16 S=4096 R=576 Dv=512",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="decode_chunk_kernel<576,8,true>")
+                kernel="mla_decode_kernel<576,512> + decode_merge_kernel")
 
 
 def _c2_train_inputs(dev, gen):
@@ -225,7 +225,7 @@ def make_c2b(dev, gen):
                                      workspace=ws)
     return dict(name="C2 causal bwd bf16 B=4 H=16 L=4096 D=128 (dq, dk, dv)", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_bwd_dq_kernel<128,false> + flash_bwd_dkdv_kernel<128,false>")
+                kernel="flash_bwd_dq_kernel<128,false,0> + flash_bwd_dkdv_kernel<128,false,0>")
 
 
 def make_c2fb(dev, gen):
@@ -246,7 +246,7 @@ def make_c2fb(dev, gen):
     nbytes = 2 * B * L * H * D * 2 * 5 + B * H * L * 4
     return dict(name="C2 causal fwd+bwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_fwd_bf16_kernel<128,false> + flash_bwd_*<128,false>")
+                kernel="flash_fwd_bf16_kernel<128,false,0> + flash_bwd_*<128,false,0>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
@@ -415,7 +415,7 @@ def main():
                        "head_dim": 128, "mask": "causal", "flop_per_step": w["flop"]},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(frac, 4),
-                         "traffic": measured_traffic("pjx::flash_fwd_bf16_kernel<128, false>"),
+                         "traffic": measured_traffic("pjx::flash_fwd_bf16_kernel<128, false, 0>"),
                          "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
                          "kernel": w["kernel"]},
         })
