@@ -52,6 +52,10 @@ extern "C" {
  *   segment_q, segment_k -- [B, Lq], [B, Lk]: ids equal (SameSegmentMask
  *                     :1537-1668, BlockDiagonalMask :871-981; with causal
  *                     BlockDiagonalCausalMask :984-1076)
+ *   row_kv_lengths -- [B, Lq]: k < row_kv_lengths[b, q] (KeyPaddingMask
+ *                     :1132-1236, whose payload the reference reads per query
+ *                     row: get_data :1192-1204 with the query block spec
+ *                     :1175-1190); excludes segment_q / segment_k
  * Score modifiers, on s = sm_scale * q.k in the order of SumBias (:553-582):
  *   s' = f(s) + bias + alibi + constant, with
  *   f(s) = softcap * tanh(s / softcap) if softcap > 0 (SoftCappingBias
@@ -77,6 +81,7 @@ typedef struct pjx_score_mods {
   float softcap;
   const float* head_scales;
   float constant;
+  const int32_t* row_kv_lengths;
 } pjx_score_mods;
 
 /* Library version (major*10000 + minor*100 + patch). */
@@ -208,6 +213,27 @@ int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* k
                    int64_t batch, int64_t q_len, int64_t heads, int64_t kv_len,
                    int64_t rank, int64_t v_dim, float sm_scale, int64_t chunk,
                    void* stream);
+
+/*
+ * Latent up-projection of materialised latent attention (mla with wk / wv).
+ * Replaces the key/value formation of the reference: `_materialize_kv`
+ * (probjax/nn/pallas_kernels/kernels/latent_attention.py:396-410) with the
+ * zero head-dim padding of `_materialized_mla` (:413-468), the in-loop
+ * `K = C W_K^T`, `V = C W_V^T` of `_mla_forward_kernel` (:132-177):
+ *
+ *   k[b, s, h, d] = sum_r cache[b, s, r] * wk[h, d, r]  (d < qk_dim; 0 up to width)
+ *   v[b, s, h, d] = sum_r cache[b, s, r] * wv[h, d, r]  (d < v_dim;  0 up to width)
+ *
+ * fp32 accumulation, rounded to dtype (PJX_DTYPE_BF16 or PJX_DTYPE_F32; all
+ * operands the same dtype).  cache [B, S, R]; wk [H, qk_dim, R];
+ * wv [H, v_dim, R]; k, v [B, S, H, width] fully written.  The flash kernels
+ * then attend q (zero-padded to width) over k / v: the padded channels carry
+ * zeros, so scores and the first v_dim output channels are unchanged.
+ * 1 <= qk_dim, v_dim <= width; H * width <= 2^20.
+ */
+int pjx_mla_project(int dtype, const void* cache, const void* wk, const void* wv, void* k,
+                    void* v, int64_t batch, int64_t kv_len, int64_t heads, int64_t rank,
+                    int64_t qk_dim, int64_t v_dim, int64_t width, void* stream);
 
 #ifdef __cplusplus
 }

@@ -35,6 +35,7 @@ from .masks import (  # noqa: F401
     PrefixLMMask,
     QKVLengthMask,
     SameSegmentMask,
+    KeyPaddingMask,
     SeqLenMask,
     SoftCappingBias,
     SumBias,
@@ -42,5 +43,5 @@ from .masks import (  # noqa: F401
 )
 from .attention_xla import auto_strategy, xla_attention  # noqa: F401
 from .splitkv import default_num_splits, splitkv_forward  # noqa: F401
-from .latent import materialize_kv, xla_mla  # noqa: F401
+from .latent import materialize_kv, materialized_mla, materialized_mla_backward, xla_mla  # noqa: F401
 from .rope import apply_rotary, inv_freq  # noqa: F401

@@ -303,6 +303,51 @@ class BlockDiagonalCausalMask(SameSegmentMask):
         return same & (np.asarray(span_q)[:, None] >= np.asarray(span_k)[None, :])
 
 
+class KeyPaddingMask(AttentionMask):
+    """:1132-1236: keys ``k < count`` with a count per query row.
+
+    ``__call__`` (:1143-1164): a scalar payload holds for every row; a vector
+    ``kl`` gives row ``i`` the keys ``k < kl[i]``.  ``tile_keep`` follows the
+    XLA path: ``get_data`` (:1192-1204) shapes a ``[T]`` payload as
+    ``[1, T, 1, 1]`` (shared by every batch) and ``[B, T]`` as
+    ``[B, T, 1, 1]``; the query block spec (:1175-1190) and
+    ``_mask_data_window`` (attention_xla.py:146-168, 250-268) window it over
+    query positions, zero-filled past ``T`` (attention_xla.py:130-133).  So
+    row ``q`` of batch ``b`` keeps ``k < kl[q]`` (or ``kl[b, q]``) and rows
+    ``q >= T`` keep nothing.  A boolean payload compares as 0/1.
+    """
+
+    stateful = True
+
+    def __init__(self, key_lengths):
+        self.key_lengths = np.asarray(key_lengths)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        kl = np.asarray(seg_q if seg_q is not None else self.key_lengths)
+        k_idx = np.asarray(k_idx)
+        if kl.ndim == 0:
+            return np.broadcast_to(k_idx[None, :] < kl, (len(q_idx), len(k_idx)))
+        if kl.ndim != 1:
+            raise ValueError("KeyPaddingMask.__call__ takes a scalar or per-row vector payload")
+        valid = k_idx[None, :] < kl.astype(np.int64)[:, None]
+        return valid[: len(q_idx), :]
+
+    def rows(self, b, span_q):
+        """The count of each query row in ``span_q`` of batch ``b``."""
+        kl = self.key_lengths.astype(np.int64)
+        span_q = np.asarray(span_q)
+        if kl.ndim == 0:
+            return np.full(len(span_q), kl)
+        vec = kl if kl.ndim == 1 else kl[b]
+        padded = np.zeros(int(span_q.max()) + 1 if len(span_q) else 0, np.int64)
+        n = min(len(vec), len(padded))
+        padded[:n] = vec[:n]
+        return padded[span_q]
+
+    def tile_keep(self, b, span_q, span_k):
+        return self(span_q, span_k, seg_q=self.rows(b, span_q))
+
+
 class ComposeMask(AttentionMask):
     def __init__(self, op: str, lhs: AttentionMask, rhs: AttentionMask):
         if op not in ("and", "or", "xor"):

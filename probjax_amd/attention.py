@@ -89,6 +89,33 @@ def _lengths_tensor(kv_lengths, batch, device):
     return L.to(torch.int32)
 
 
+def _row_kv_lengths(kl, B, l_q, device):
+    """``[B, Lq]`` int32 key count of every query row of a ``KeyPaddingMask``
+    payload, or None.
+
+    The reference reads the payload per query position (its ``get_data`` and
+    query block spec, attention_mask_bias.py:1175-1204, windowed by
+    attention_xla.py:130-133, 146-168): a vector ``[T]`` gives row ``i`` the
+    count ``kl[i]`` in every batch, ``[B, T]`` gives ``kl[b, i]``, rows past
+    ``T`` read the zero fill, a scalar holds for every row; the mask then
+    keeps ``k < count`` (:1143-1164, a boolean payload comparing as 0/1).
+    """
+    t = torch.as_tensor(kl, device=device)
+    if t.dtype.is_floating_point or t.dtype.is_complex:
+        return None
+    t = t.to(torch.int32)
+    if t.ndim == 0:
+        return t.reshape(1, 1).expand(B, l_q).contiguous()
+    if t.ndim == 1:
+        t = t[None].expand(B, -1)
+    elif t.ndim != 2 or t.shape[0] != B:
+        return None
+    out = torch.zeros((B, l_q), dtype=torch.int32, device=device)
+    n = min(int(t.shape[1]), l_q)
+    out[:, :n] = t[:, :n]
+    return out
+
+
 def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
     """Arguments of the split-KV decode for this call, or None."""
     if lb is not None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
@@ -130,6 +157,8 @@ def _score_mods(lm: LoweredMask, lb: LoweredBias | None, B, l_q, l_k, h_q, devic
             if t is None:
                 return False
             setattr(m, name, t)
+    if lm.row_kv_lengths is not None:
+        m.row_kv_lengths = lm.row_kv_lengths  # [B, Lq] int32 (prepared by _eligible)
     if lm.segment_q is not None:
         kid = lm.segment_k if lm.segment_k is not None else lm.segment_q
         sq, sk = torch.as_tensor(lm.segment_q), torch.as_tensor(kid)
@@ -194,6 +223,17 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
     lm = lower_mask(mask)
     if lm is None:
         return None
+    if lm.row_kv_lengths is not None:
+        rows = _row_kv_lengths(lm.row_kv_lengths, B, l_q, query.device)
+        if rows is None:
+            return None
+        if l_q == 1:
+            # One query row: its count is a per-batch key length, which is what
+            # MultiHeadAttention's cached decode builds each step
+            # (layers/attention.py:612-675); the KV-length kernels take it.
+            lm.row_kv_lengths, lm.kv_lengths = None, rows[:, 0]
+        else:
+            lm.row_kv_lengths = rows
     if lm.kv_lengths is not None:
         L = _lengths_tensor(lm.kv_lengths, B, query.device)
         if L is None:
@@ -235,7 +275,10 @@ def use_splitkv(q, k, *, mask=None, bias=None, dropout_rate: float = 0.0,
     past each length are skipped), so a length mask does not disable it here;
     it needs bf16, head_dim 64/128 and ``(Hq/Hkv)*Lq <= 16``.
     """
-    return _splitkv_ok(q, k, lower_mask(mask), bias is not None, dropout_rate, split_kv)
+    lm = lower_mask(mask)
+    if lm is not None and lm.row_kv_lengths is not None and getattr(q, "ndim", 0) == 4 and q.shape[1] == 1:
+        lm.kv_lengths, lm.row_kv_lengths = lm.row_kv_lengths, None  # one row: per-batch lengths
+    return _splitkv_ok(q, k, lm, bias is not None, dropout_rate, split_kv)
 
 
 class _AttentionFunction(torch.autograd.Function):
@@ -391,16 +434,101 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
                               chunk=chunk, return_lse=return_lse)
 
 
+class _MaterializedMLAFunction(torch.autograd.Function):
+    """Differentiable materialised latent attention: the custom VJP of
+    probjax's ``mla`` with projections (latent_attention.py:527-589).
+
+    Forward: ``pjx_mla_project`` forms ``K = C W_K^T`` and ``V = C W_V^T``
+    (zero-padded to the common head width) once, then the flash forward
+    attends the zero-padded ``q`` over them.  Backward: the VJP of that
+    materialised computation, as in the reference (:571-589): the flash
+    backward gives ``dq, dK, dV``; the projection's chain rule gives
+    ``dC = dK W_K + dV W_V``, ``dW_K = dK^T C``, ``dW_V = dV^T C`` (plain
+    GEMMs, the reference's einsum VJPs).  K and V are kept from the forward
+    rather than formed a second time."""
+
+    @staticmethod
+    def forward(ctx, q, cache, wk, wv, st):
+        o, lse = hip.flash_attention_fwd(st["qp"], st["k"], st["v"], sm_scale=st["sm_scale"],
+                                         return_lse=True, **st["plan"])
+        ctx.save_for_backward(cache, wk, wv, st["qp"], st["k"], st["v"], o, lse)
+        ctx.st = {n: st[n] for n in ("sm_scale", "plan", "dk", "dv", "width")}
+        return o if st["dv"] == st["width"] else o[..., : st["dv"]].contiguous()
+
+    @staticmethod
+    def backward(ctx, dout):
+        cache, wk, wv, qp, k, v, o, lse = ctx.saved_tensors
+        st = ctx.st
+        dk_dim, dv_dim, width = st["dk"], st["dv"], st["width"]
+        dop = _pad_head(dout.to(o.dtype), width)
+        dqp, dkp, dvp = hip.flash_attention_bwd(qp, k, v, o, dop, lse, sm_scale=st["sm_scale"], **st["plan"])
+        B, S, R = cache.shape
+        H = wk.shape[0]
+        dK = dkp[..., :dk_dim].reshape(B * S, H * dk_dim)
+        dV = dvp[..., :dv_dim].reshape(B * S, H * dv_dim)
+        c2 = cache.reshape(B * S, R)
+        dcache = dK @ wk.reshape(H * dk_dim, R) + dV @ wv.reshape(H * dv_dim, R)
+        dwk = (dK.t().contiguous() @ c2).reshape(H, dk_dim, R)
+        dwv = (dV.t().contiguous() @ c2).reshape(H, dv_dim, R)
+        dq = dqp if dk_dim == width else dqp[..., :dk_dim].contiguous()
+        return dq, dcache.reshape(B, S, R), dwk, dwv, None
+
+
+def _pad_head(x, width):
+    """``x`` zero-padded on its last (head) axis to ``width`` (contiguous)."""
+    if x.shape[-1] == width:
+        return x.contiguous()
+    out = torch.zeros(x.shape[:-1] + (width,), dtype=x.dtype, device=x.device)
+    out[..., : x.shape[-1]] = x
+    return out
+
+
+def _mla_materialized(q, cache, wk, wv, *, mask, bias, sm_scale):
+    """Materialised ``mla`` (latent_attention.py:413-468, 527-589) on the HIP
+    kernels; ValueError when they cannot compute the call exactly."""
+    B, l_q, H, dk_dim = q.shape
+    dv_dim = wv.shape[1]
+    width = max(dk_dim, dv_dim)
+    width = next((w for w in FLASH_HEAD_DIMS if w >= width), None)
+    if width is None:
+        raise ValueError(f"materialised mla supports head dims up to {FLASH_HEAD_DIMS[-1]}, "
+                         f"got qk {dk_dim}, v {dv_dim}")
+    if not (q.dtype == cache.dtype == wk.dtype == wv.dtype) or q.dtype not in BACKWARD_DTYPES:
+        raise ValueError("materialised mla takes q, cache, wk and wv of one dtype (bfloat16 or float32)")
+    if not all(hip_device(t) and t.device == q.device for t in (cache, wk, wv)):
+        raise ValueError(f"the HIP latent-attention kernels need tensors on a {HIP_ARCH} ROCm device")
+    with torch.no_grad():
+        k, v = hip.mla_project(cache.detach(), wk.detach(), wv.detach(), width=width)
+        qp = _pad_head(q.detach(), width)
+    e = _eligible(qp, k, v, mask=mask, bias=bias, dropout_rate=0.0)
+    plan = None if e is None else _flash_plan(qp, k, v, e[0], e[1])
+    if plan is None:
+        raise ValueError("the HIP kernels cannot compute this materialised mla call exactly: "
+                         + _unsupported_message(qp, k, mask, bias, 0.0))
+    st = dict(qp=qp, k=k, v=v, plan=plan, sm_scale=float(sm_scale), dk=dk_dim, dv=dv_dim, width=width)
+    if not _needs_grad(q, cache, wk, wv):
+        o = hip.flash_attention_fwd(qp, k, v, sm_scale=float(sm_scale), **plan)
+        return o if dv_dim == width else o[..., :dv_dim]
+    return _MaterializedMLAFunction.apply(q, cache, wk, wv, st)
+
+
 def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
         sm_scale: float | None = None, dropout_rate: float = 0.0, v_dim: int | None = None,
         **unused_tuning):
     """Attention of ``q`` over a shared latent ``cache`` (probjax ``mla``,
-    kernels/latent_attention.py:636-766), absorbed form ``K = V = cache``.
+    kernels/latent_attention.py:636-766).
 
-    ``q [B, Q, H, R]``, ``cache [B, S, R]`` -> ``[B, Q, H, R]`` (or the first
-    ``v_dim`` columns, which is all a caller that multiplies by ``W_UV`` of
-    width ``v_dim`` needs).  ``mask``: ``None`` / ``NoMask`` / ``KVLenMask``.
-    Materialised mode (``wk``/``wv`` given) and biases raise ``ValueError``.
+    Absorbed form (``wk = wv = None``, ``K = V = cache``): ``q [B, Q, H, R]``,
+    ``cache [B, S, R]`` -> ``[B, Q, H, R]`` (or the first ``v_dim`` columns,
+    which is all a caller that multiplies by ``W_UV`` of width ``v_dim``
+    needs); ``mask``: ``None`` / ``NoMask`` / ``KVLenMask``, no bias.
+
+    Materialised form (``wk [H, qk_head_dim, R]``, ``wv [H, v_head_dim, R]``):
+    ``q [B, Q, H, qk_head_dim]`` -> ``[B, Q, H, v_head_dim]``, every mask and
+    bias of the flash route (the reference's contract: equal to ``mha`` over
+    the materialised K/V, tests/test_latent_attention.py:341-379), bf16 or
+    fp32, differentiable in ``q``, ``cache``, ``wk`` and ``wv``; head dims up
+    to 128.  Dropout raises ``ValueError``.
     """
     del rng, unused_tuning
     if q.ndim != 4:
@@ -419,10 +547,16 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
             "absorbed mode (wk=None) requires qk_head_dim == kv_lora_rank "
             f"({q.shape[-1]} != {cache.shape[-1]})"
         )
-    if wk is not None:
-        raise ValueError("the HIP latent-attention kernel takes the absorbed form (wk = wv = None)")
+    if wk is not None and tuple(wk.shape) != (q.shape[-2], q.shape[-1], cache.shape[-1]):
+        raise ValueError(f"wk must be {(q.shape[-2], q.shape[-1], cache.shape[-1])}, got {tuple(wk.shape)}")
+    if wv is not None and (wv.ndim != 3 or wv.shape[0] != q.shape[-2] or wv.shape[2] != cache.shape[-1]):
+        raise ValueError(f"wv must be [heads, v_head_dim, {cache.shape[-1]}], got {tuple(wv.shape)}")
     if sm_scale is None:
         sm_scale = 1.0 / math.sqrt(q.shape[-1])
+    if wk is not None:
+        if dropout_rate > 0:
+            raise ValueError("the HIP latent-attention kernels take no dropout")
+        return _mla_materialized(q, cache, wk, wv, mask=mask, bias=bias, sm_scale=sm_scale)
     if bias is not None or dropout_rate > 0:
         raise ValueError("the HIP latent-attention kernel takes no bias or dropout")
     lm = lower_mask(mask)

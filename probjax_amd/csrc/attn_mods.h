@@ -17,7 +17,9 @@
 // view), so masking is two compares per score.
 //
 // SameSegmentMask / BlockDiagonal(Causal)Mask (:1537-1668, :871-1076) compare
-// per-position segment ids on top of the interval.
+// per-position segment ids on top of the interval; KeyPaddingMask
+// (:1132-1236) gives each query row its own key count (k < seg_q[q], seg_lt),
+// which is not monotone in q and so is checked per score like the ids.
 //
 // Score modifiers, applied to s = sm_scale * q.k in the order of the
 // reference's SumBias composition (:553-582): one multiplicative modifier
@@ -41,8 +43,9 @@ struct ScoreMods {
   int win_right;         // kNoBound: none
   const int32_t* prefix; // [B] PrefixLM lengths or null
   const int32_t* seqlen; // [B] SeqLenMask lengths or null
-  const int32_t* seg_q;  // [B, Lq] segment ids or null
-  const int32_t* seg_k;  // [B, Lk]
+  const int32_t* seg_q;  // [B, Lq] segment ids (or row key lengths) or null
+  const int32_t* seg_k;  // [B, Lk]; null with seg_lt
+  int seg_lt;            // 0: keep seg_q[q] == seg_k[k]; 1: keep k < seg_q[q]
   const float* alibi;    // [Hq] slopes or null
   int alibi_sym;         // f = |q-k| (1) or max(q-k, 0) (0)
   float softcap;         // > 0: s = softcap * tanh(s / softcap)

@@ -29,6 +29,7 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) 
   m.causal_shift = 0;
   m.win_left = m.win_right = kNoBound;
   m.prefix = m.seqlen = m.seg_q = m.seg_k = nullptr;
+  m.seg_lt = 0;
   m.alibi = nullptr;
   m.alibi_sym = 0;
   m.softcap = 0.f;
@@ -49,6 +50,10 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) 
     snprintf(buf, sizeof(buf), "%s: segment_q and segment_k go together", who);
     return fail(PJX_ERR_INVALID, buf);
   }
+  if (mods->row_kv_lengths && mods->segment_q) {
+    snprintf(buf, sizeof(buf), "%s: row_kv_lengths excludes segment ids (one stateful mask)", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
   if (mods->window_left >= kNoBound || mods->window_right >= kNoBound ||
       mods->causal_shift >= kNoBound || mods->causal_shift <= -kNoBound) {
     snprintf(buf, sizeof(buf), "%s: window / causal_shift out of range", who);
@@ -61,6 +66,11 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) 
   m.seqlen = mods->seq_lengths;
   m.seg_q = mods->segment_q;
   m.seg_k = mods->segment_k;
+  if (mods->row_kv_lengths) {
+    m.seg_q = mods->row_kv_lengths;
+    m.seg_k = nullptr;
+    m.seg_lt = 1;
+  }
   m.alibi = mods->alibi_slopes;
   m.alibi_sym = mods->alibi_symmetric ? 1 : 0;
   m.softcap = mods->softcap;

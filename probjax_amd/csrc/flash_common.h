@@ -180,14 +180,15 @@ __device__ __forceinline__ void ext_scores_sT_t(const FlashArgs& a, const BlockG
         if (row_in) bv = bias_vec ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
       }
       int4 sg = {0, 0, 0, 0};
-      if (a.m.seg_q) sg = seg4(a.m.seg_k, g.b, kk, a.Lk);
+      if (a.m.seg_k) sg = seg4(a.m.seg_k, g.b, kk, a.Lk);
       const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const int r = 4 * gq + j, kj = kk + j;
         float gg;
         const float x = modify_score<SOFTCAP>(a.m, er.hm, s[kb][r] * a.scale, bv[j], g.qi, kj, gg);
-        const bool keep = kj >= er.lo && kj <= er.hi && (!a.m.seg_q || sgv[j] == er.segq);
+        const bool keep = kj >= er.lo && kj <= er.hi &&
+                          (!a.m.seg_q || (a.m.seg_lt ? kj < er.segq : sgv[j] == er.segq));
         emit(kb, r, keep ? x : -INFINITY, gg);
       }
       // one group of 4 keys at a time: keeps the loads and temporaries of
@@ -249,7 +250,8 @@ __device__ __forceinline__ void ext_scores_S_t(const FlashArgs& a, int b, const 
       if constexpr (BIAS) bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
       float gg;
       const float x = modify_score<SOFTCAP>(a.m, hm, s[r] * a.scale, bv, qr, key, gg);
-      const bool keep = qr >= qlo && qr <= qhi && (!a.m.seg_q || sgv[j] == segk);
+      const bool keep = qr >= qlo && qr <= qhi &&
+                        (!a.m.seg_q || (a.m.seg_lt ? key < sgv[j] : sgv[j] == segk));
       emit(r, keep ? x : -INFINITY, gg);
     }
     __builtin_amdgcn_sched_barrier(0);

@@ -1,0 +1,263 @@
+// Up-projection of the shared latent for materialised latent attention:
+//
+//   k[b, s, h, d] = sum_r cache[b, s, r] * wk[h, d, r]   (d < qk_dim, else 0)
+//   v[b, s, h, d] = sum_r cache[b, s, r] * wv[h, d, r]   (d < v_dim,  else 0)
+//
+// for d < width, fp32 accumulation rounded to the storage dtype.  This is
+// `_materialize_kv` (probjax/nn/pallas_kernels/kernels/latent_attention.py:
+// 396-410) with the zero head-dim padding of `_materialized_mla` (:413-468,
+// `_pad_head_dim`) written by the same pass, so that the flash kernels take K
+// and V directly.  The reference's Triton kernel forms these tiles inside its
+// KV loop (:132-177) once per query block; here they are formed once per call:
+// for L query rows that saves (L / 128 - 1) recomputations of the whole
+// projection, and K/V of a full prefill fit HBM many times over.
+//
+// As a GEMM: out[m, n] = sum_r C[m, r] W[n, r] with m = b*S + s over the
+// latent rows and n = h*width + d over the output channels; both operands
+// have the rank contiguous (the "NT" form of Q K^T).  One launch covers K
+// (grid.y < ny) and V (grid.y >= ny).
+//
+// bf16: 128 x 128 output tiles, 4 waves of 64 x 64 (2 x 2 MFMA 32x32x16
+// blocks), rank chunks of 64 staged through LDS via registers (the next
+// chunk's global loads are in flight while the current one is multiplied).
+// fp32: 64 x 64 tiles of plain FMA, 4 x 4 per thread (no roundings).
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "pjx_common.h"
+#include "pjx_internal.h"
+
+namespace pjx {
+namespace {
+
+struct ProjArgs {
+  const void* cache;  // [M, R]
+  const void* w[2];   // [H, dim, R]
+  void* out[2];       // [M, H * width]
+  int64_t M;          // latent rows B * S
+  int H, R, width;
+  int dim[2];         // qk_dim, v_dim
+  int ny;             // column tiles per output
+};
+
+// ---------------------------------------------------------------------------
+// bf16
+// ---------------------------------------------------------------------------
+constexpr int kBM = 128, kBN = 128, kBK = 64;
+constexpr int kPitch = kBK * 2 + 16;  // LDS bytes per staged row (16 B pad: fewer bank conflicts)
+constexpr int kChunks = kBK / 8;      // 16-byte chunks per staged row
+constexpr int kPerThread = kBM * kChunks / 256;
+
+__device__ __forceinline__ u32x4 load_chunk_bf16(const uint16_t* row, int r0, int R, bool vec) {
+  // 8 consecutive rank entries r0 .. r0+7 of one row (0 past R / for a null row)
+  if (!row) return u32x4{0u, 0u, 0u, 0u};
+  if (vec) {
+    if (r0 + 8 <= R) return *(const u32x4*)(row + r0);
+    return u32x4{0u, 0u, 0u, 0u};
+  }
+  uint32_t h[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = (r0 + j < R) ? row[r0 + j] : 0u;
+  return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
+}
+
+__global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBM * kPitch];
+  unsigned char* As = lds;
+  unsigned char* Bs = lds + kBM * kPitch;
+
+  const int which = blockIdx.y >= (unsigned)a.ny ? 1 : 0;
+  const int n0 = (blockIdx.y - which * a.ny) * kBN;
+  const int64_t m0 = (int64_t)blockIdx.x * kBM;
+  const int ncols = a.H * a.width;
+  const int dim = a.dim[which];
+  const uint16_t* C = (const uint16_t*)a.cache;
+  const uint16_t* W = (const uint16_t*)a.w[which];
+  const bool vec = (a.R & 7) == 0;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+
+  // Source rows of this thread's staged chunks (null: zero row).
+  const uint16_t* arow[kPerThread];
+  const uint16_t* brow[kPerThread];
+  int part[kPerThread];
+#pragma unroll
+  for (int i = 0; i < kPerThread; ++i) {
+    const int c = tid + i * 256;
+    const int row = c / kChunks;
+    part[i] = c % kChunks;
+    const int64_t m = m0 + row;
+    arow[i] = m < a.M ? C + m * a.R : nullptr;
+    const int n = n0 + row;
+    const int h = n / a.width, d = n - h * a.width;
+    brow[i] = (n < ncols && d < dim) ? W + ((int64_t)h * dim + d) * a.R : nullptr;
+  }
+
+  u32x4 ra[kPerThread], rb[kPerThread];
+  auto load = [&](int r0) {
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      ra[i] = load_chunk_bf16(arow[i], r0 + 8 * part[i], a.R, vec);
+      rb[i] = load_chunk_bf16(brow[i], r0 + 8 * part[i], a.R, vec);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  const int frag = (lane & 31) * kPitch + (lane >> 5) * 16;
+  const int nk = (a.R + kBK - 1) / kBK;
+  load(0);
+  for (int t = 0; t < nk; ++t) {
+    __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+    for (int i = 0; i < kPerThread; ++i) {
+      const int c = tid + i * 256;
+      const int off = (c / kChunks) * kPitch + (c % kChunks) * 16;
+      *(u32x4*)(As + off) = ra[i];
+      *(u32x4*)(Bs + off) = rb[i];
+    }
+    __syncthreads();
+    if (t + 1 < nk) load((t + 1) * kBK);
+#pragma unroll
+    for (int ks = 0; ks < kBK / 16; ++ks) {
+      bf16x8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = as_bf16x8(*(const u32x4*)(As + (wr + 32 * i) * kPitch + frag + ks * 32));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = as_bf16x8(*(const u32x4*)(Bs + (wc + 32 * j) * kPitch + frag + ks * 32));
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
+    }
+  }
+
+  // Register r of block (i, j): row wr + 32i + 8(r/4) + 4(lane/32) + r%4,
+  // column wc + 32j + lane%32.
+  uint16_t* O = (uint16_t*)a.out[which];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int n = n0 + wc + 32 * j + (lane & 31);
+      if (n >= ncols) continue;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t m = m0 + wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        if (m < a.M) O[m * ncols + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// fp32
+// ---------------------------------------------------------------------------
+constexpr int kFM = 64, kFN = 64, kFK = 16;
+
+__global__ __launch_bounds__(256) void mla_project_f32_kernel(ProjArgs a) {
+  __shared__ float As[kFK][kFM + 4];
+  __shared__ float Bs[kFK][kFN + 4];
+  const int which = blockIdx.y >= (unsigned)a.ny ? 1 : 0;
+  const int n0 = (blockIdx.y - which * a.ny) * kFN;
+  const int64_t m0 = (int64_t)blockIdx.x * kFM;
+  const int ncols = a.H * a.width;
+  const int dim = a.dim[which];
+  const float* C = (const float*)a.cache;
+  const float* W = (const float*)a.w[which];
+  const int tid = threadIdx.x, tx = tid & 15, ty = tid >> 4;
+
+  // staging: row tid/4, rank entries 4*(tid%4) .. +3 of the chunk
+  const int srow = tid >> 2, sk = 4 * (tid & 3);
+  const int64_t m = m0 + srow;
+  const float* arow = m < a.M ? C + m * a.R : nullptr;
+  const int n = n0 + srow;
+  const int h = n / a.width, d = n - h * a.width;
+  const float* brow = (n < ncols && d < dim) ? W + ((int64_t)h * dim + d) * a.R : nullptr;
+
+  float acc[4][4] = {};
+  for (int r0 = 0; r0 < a.R; r0 += kFK) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int r = r0 + sk + j;
+      As[sk + j][srow] = (arow && r < a.R) ? arow[r] : 0.f;
+      Bs[sk + j][srow] = (brow && r < a.R) ? brow[r] : 0.f;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < kFK; ++k) {
+      float av[4], bv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) av[i] = As[k][ty * 4 + i];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) bv[j] = Bs[k][tx * 4 + j];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(av[i], bv[j], acc[i][j]);
+    }
+    __syncthreads();
+  }
+  float* O = (float*)a.out[which];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t mo = m0 + ty * 4 + i;
+    if (mo >= a.M) continue;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int no = n0 + tx * 4 + j;
+      if (no < ncols) O[mo * ncols + no] = acc[i][j];
+    }
+  }
+}
+
+}  // namespace
+}  // namespace pjx
+
+using namespace pjx;
+
+extern "C" int pjx_mla_project(int dtype, const void* cache, const void* wk, const void* wv, void* k,
+                               void* v, int64_t batch, int64_t kv_len, int64_t heads, int64_t rank,
+                               int64_t qk_dim, int64_t v_dim, int64_t width, void* stream) {
+  clear_error();
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_mla_project: dtype must be bf16 or f32");
+  if (batch < 0 || kv_len < 0 || heads <= 0 || rank <= 0)
+    return fail(PJX_ERR_INVALID, "pjx_mla_project: bad sizes");
+  if (width <= 0 || qk_dim <= 0 || v_dim <= 0 || qk_dim > width || v_dim > width)
+    return fail(PJX_ERR_INVALID, "pjx_mla_project: need 1 <= qk_dim, v_dim <= width");
+  if (rank > (1 << 20) || heads * width > (1 << 20) || batch * kv_len > ((int64_t)1 << 34))
+    return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
+  const int64_t M = batch * kv_len;
+  if (M == 0) return PJX_OK;
+  if (!cache || !wk || !wv || !k || !v) return fail(PJX_ERR_INVALID, "pjx_mla_project: null pointer");
+  ProjArgs a = {};
+  a.cache = cache;
+  a.w[0] = wk;
+  a.w[1] = wv;
+  a.out[0] = k;
+  a.out[1] = v;
+  a.M = M;
+  a.H = (int)heads;
+  a.R = (int)rank;
+  a.width = (int)width;
+  a.dim[0] = (int)qk_dim;
+  a.dim[1] = (int)v_dim;
+  const int ncols = a.H * a.width;
+  hipStream_t s = (hipStream_t)stream;
+  if (dtype == PJX_DTYPE_BF16) {
+    a.ny = (ncols + kBN - 1) / kBN;
+    const int64_t gx = (M + kBM - 1) / kBM;
+    if (gx > 0x7fffffff) return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
+    hipLaunchKernelGGL(mla_project_bf16_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+  } else {
+    a.ny = (ncols + kFN - 1) / kFN;
+    const int64_t gx = (M + kFM - 1) / kFM;
+    if (gx > 0x7fffffff) return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
+    hipLaunchKernelGGL(mla_project_f32_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+  }
+  return check_launch("pjx_mla_project");
+}

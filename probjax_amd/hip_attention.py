@@ -73,6 +73,7 @@ class ScoreModsArgs:
     softcap: float = 0.0
     head_scales: torch.Tensor | None = None  # [Hq] float32
     constant: float = 0.0
+    row_kv_lengths: torch.Tensor | None = None  # [B, Lq] int32: k < row_kv_lengths[b, q]
 
 
 def _mods_struct(m: ScoreModsArgs | None, B, Lq, Lk, Hq, dev):
@@ -96,6 +97,7 @@ def _mods_struct(m: ScoreModsArgs | None, B, Lq, Lk, Hq, dev):
         "segment_k": dev_tensor(m.segment_k, (B, Lk), torch.int32, "segment_k"),
         "alibi_slopes": dev_tensor(m.alibi_slopes, (Hq,), torch.float32, "alibi_slopes"),
         "head_scales": dev_tensor(m.head_scales, (Hq,), torch.float32, "head_scales"),
+        "row_kv_lengths": dev_tensor(m.row_kv_lengths, (B, Lq), torch.int32, "row_kv_lengths"),
     }
     st = native.ScoreMods(
         causal_shift=int(m.causal_shift), window_left=int(m.window_left),
@@ -283,3 +285,28 @@ def mla_decode(
     )
     native.check(rc)
     return (o, lse) if return_lse else o
+
+
+def mla_project(cache, wk, wv, *, width: int):
+    """``pjx_mla_project``: ``K = C W_K^T``, ``V = C W_V^T`` per head, zero-padded
+    to ``width`` channels -> ``(k, v)`` each ``[B, S, H, width]``
+    (latent_attention.py:396-410, 413-468)."""
+    dev = _on_device(cache, wk, wv)
+    if cache.ndim != 3 or wk.ndim != 3 or wv.ndim != 3:
+        raise ValueError("cache must be [B, S, R], wk [H, qk_dim, R] and wv [H, v_dim, R]")
+    B, S, R = cache.shape
+    H, dk, Rk = wk.shape
+    if Rk != R or wv.shape[0] != H or wv.shape[2] != R:
+        raise ValueError(f"incompatible shapes cache {tuple(cache.shape)}, wk {tuple(wk.shape)}, wv {tuple(wv.shape)}")
+    dv = wv.shape[1]
+    if not (cache.dtype == wk.dtype == wv.dtype) or cache.dtype not in _DTYPES:
+        raise ValueError("cache, wk and wv must share one dtype (bfloat16 or float32)")
+    cache, wk, wv = cache.contiguous(), wk.contiguous(), wv.contiguous()
+    k = torch.empty((B, S, H, width), dtype=cache.dtype, device=dev)
+    v = torch.empty((B, S, H, width), dtype=cache.dtype, device=dev)
+    rc = native.load().pjx_mla_project(
+        _DTYPES[cache.dtype], _ptr(cache), _ptr(wk), _ptr(wv), _ptr(k), _ptr(v),
+        B, S, H, R, dk, dv, int(width), _stream(dev),
+    )
+    native.check(rc)
+    return k, v

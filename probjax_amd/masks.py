@@ -18,6 +18,10 @@ attention_mask_bias.py):
   diagonal outside;
 * ``SameSegmentMask`` / ``BlockDiagonalMask`` / ``BlockDiagonalCausalMask`` --
   :1537-1668, :871-1076, equal segment ids (and ``q >= k``);
+* ``KeyPaddingMask``  -- :1132-1236, key ``k`` kept for query row ``q`` iff
+  ``k < key_lengths`` read per query row (the reference's payload layout:
+  ``[T]`` gives row ``i`` the count ``kl[i]`` in every batch, ``[B, T]``
+  gives ``kl[b, i]``, rows past ``T`` count 0, a scalar holds everywhere);
 * ``ComposeMask``     -- :324-525; only ``"and"`` compositions lower to the
   kernels (what the kernels evaluate is an AND of the above);
 * ``DenseBias``       -- :1807-1922, ``scores + bias[b|0, h|0, q, k]`` with an
@@ -136,6 +140,11 @@ class BlockDiagonalCausalMask(BlockDiagonalMask):
     pass
 
 
+class KeyPaddingMask(AttentionMask):
+    def __init__(self, key_lengths):
+        self.key_lengths = key_lengths
+
+
 class DenseBias(AttentionBias):
     def __init__(self, bias):
         if bias.ndim != 4:
@@ -217,6 +226,7 @@ class LoweredMask:
     seq_lengths: object = None  # [B]
     segment_q: object = None  # [B, Lq] or [Lq]
     segment_k: object = None  # [B, Lk] or [Lk] (None: the query ids)
+    row_kv_lengths: object = None  # KeyPaddingMask payload: scalar, [T] or [B, T]
 
     @property
     def causal(self) -> bool:
@@ -233,11 +243,12 @@ class LoweredMask:
             or self.prefix_lengths is not None
             or self.seq_lengths is not None
             or self.segment_q is not None
+            or self.row_kv_lengths is not None
         )
 
     def merge(self, other: "LoweredMask") -> "LoweredMask | None":
         state = [
-            n for n in ("kv_lengths", "prefix_lengths", "seq_lengths", "segment_q")
+            n for n in ("kv_lengths", "prefix_lengths", "seq_lengths", "segment_q", "row_kv_lengths")
             for m in (self, other) if getattr(m, n) is not None
         ]
         if len(state) > 1:
@@ -254,6 +265,7 @@ class LoweredMask:
             seq_lengths=pick("seq_lengths"),
             segment_q=pick("segment_q"),
             segment_k=pick("segment_k"),
+            row_kv_lengths=pick("row_kv_lengths"),
         )
 
 
@@ -289,6 +301,8 @@ def lower_mask(mask) -> LoweredMask | None:
     if name in ("BlockDiagonalMask", "BlockDiagonalCausalMask"):
         return LoweredMask(segment_q=mask.query_block_ids, segment_k=mask.key_block_ids,
                            causal_shift=0 if name == "BlockDiagonalCausalMask" else None)
+    if name == "KeyPaddingMask":
+        return LoweredMask(row_kv_lengths=mask.key_lengths)
     if name == "QKVLengthMask":
         return LoweredMask(q_valid=int(mask.q_length), kv_valid=int(mask.kv_length))
     if name == "ComposeMask" and getattr(mask, "op", None) == "and":

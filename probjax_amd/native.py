@@ -36,6 +36,7 @@ class ScoreMods(ctypes.Structure):
         ("softcap", ctypes.c_float),
         ("head_scales", ctypes.c_void_p),
         ("constant", ctypes.c_float),
+        ("row_kv_lengths", ctypes.c_void_p),
     ]
 
 
@@ -67,6 +68,10 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64, _I64, _I64,
          _I64, _I64, ctypes.c_float, _I64, _P],
+    ),
+    "pjx_mla_project": (
+        ctypes.c_int,
+        [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],
     ),
 }
 EXPORTED = tuple(_SIGNATURES)

@@ -68,6 +68,27 @@ def test_config3_gqa_decode_kvlen_dispatches_splitkv(device, monkeypatch):
     assert max_abs(to_np(got), want) <= 2e-2
 
 
+def test_cached_decode_key_padding_mask_dispatches_splitkv(device, monkeypatch):
+    """MultiHeadAttention's cached decode step (layers/attention.py:612-675)
+    builds KeyPaddingMask(full(B, index + 1)) for one query row; the route
+    takes it as per-batch KV lengths and runs the split-KV kernel."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd import hip_attention as H
+    from probjax_amd.masks import KeyPaddingMask
+
+    lengths = np.full(2, 1500, np.int32)
+    q, k, v = (oracle.round_bf16(x) for x in rng_normal(7, (2, 1, 16, 128), (2, 2048, 16, 128), (2, 2048, 16, 128)))
+    want = oracle.xla_attention(q, k, v, mask=oracle.KeyPaddingMask(lengths), sm_scale=1 / math.sqrt(128))
+    calls = []
+    real = H.splitkv_decode
+    monkeypatch.setattr(H, "splitkv_decode", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    got = A.flex_attention(*(_bf(x, device) for x in (q, k, v)),
+                           mask=KeyPaddingMask(torch.from_numpy(lengths).to(device)))
+    assert calls, "a one-row KeyPaddingMask call should run the split-KV kernel"
+    assert max_abs(to_np(got), want) <= 2e-2
+
+
 def test_config4_bias_and_padding_mask(device):
     import torch
     from probjax_amd import attention as A

@@ -53,6 +53,15 @@ def _case(name, B, Lq, Lk):
         "headscale": (None, M.PerHeadScaleBias(torch.tensor([0.5, 2.0, 1.5, 3.0])), None,
                       oracle.PerHeadScaleBias(np.array([0.5, 2.0, 1.5, 3.0], np.float32))),
     }
+    if name == "key_padding":
+        # per-row counts, shorter than Lq: rows past the payload keep no key
+        kl = np.random.default_rng(52).integers(0, Lk + 1, size=Lq - 20).astype(np.int32)
+        return (M.KeyPaddingMask(torch.from_numpy(kl).to(dev)) & M.CausalMask(), None,
+                oracle.KeyPaddingMask(kl) & oracle.CausalMask(), None)
+    if name == "key_padding_2d":
+        kl = np.random.default_rng(53).integers(0, Lk + 1, size=(B, Lq)).astype(np.int32)
+        return (M.KeyPaddingMask(torch.from_numpy(kl).to(dev)), M.ConstantBias(0.5),
+                oracle.KeyPaddingMask(kl), oracle.ConstantBias(0.5))
     if name == "decay_dense":
         (bias,) = rng_normal(50, (1, 4, Lq, Lk), scale=0.5)
         return (M.KVLenMask(torch.tensor([Lk, Lk // 2][:B], device=dev)),
@@ -76,6 +85,8 @@ CASES = [
     ("decay_dense", 2, 256, 256, 4, 2, 128),
     ("softcap", 2, 256, 256, 4, 4, 128),
     ("headscale", 2, 192, 192, 4, 1, 64),
+    ("key_padding", 2, 256, 320, 4, 2, 128),
+    ("key_padding_2d", 2, 160, 200, 4, 4, 64),
 ]
 
 
@@ -135,6 +146,7 @@ def test_ext_bf16_forward_and_grads(device, name, B, Lq, Lk, Hq, Hkv, D):
 
 
 @pytest.mark.parametrize("name,B,Lq,Lk,Hq,Hkv,D", [c for c in CASES if c[0] in (
-    "bottom_right", "causal_window_kvlen", "segments", "alibi_sym_const", "softcap", "headscale", "seqlen")])
+    "bottom_right", "causal_window_kvlen", "segments", "alibi_sym_const", "softcap", "headscale", "seqlen",
+    "key_padding")])
 def test_ext_f32_forward_and_grads(device, name, B, Lq, Lk, Hq, Hkv, D):
     _run(device, "f32", name, B, Lq, Lk, Hq, Hkv, D)

@@ -150,6 +150,19 @@ def test_mha_and_mla_refuse_off_device():
         A.mla(qm, c, wk=torch.zeros(16, 576, 576))
     with pytest.raises(ValueError, match="qk_head_dim == kv_lora_rank"):
         A.mla(qm[..., :512], c)
+    # materialised mode: the reference's shape checks (latent_attention.py:690-701)
+    qd = torch.zeros(2, 4, 16, 96, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="wk must be"):
+        A.mla(qd, c, torch.zeros(16, 64, 576), torch.zeros(16, 64, 576))
+    with pytest.raises(ValueError, match="wv must be"):
+        A.mla(qd, c, torch.zeros(16, 96, 576), torch.zeros(16, 64, 512))
+    wk, wv = torch.zeros(16, 96, 576, dtype=torch.bfloat16), torch.zeros(16, 64, 576, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="ROCm device"):
+        A.mla(qd, c, wk, wv)
+    with pytest.raises(ValueError, match="head dims up to 128"):
+        A.mla(torch.zeros(2, 4, 16, 192), c.float(), torch.zeros(16, 192, 576), torch.zeros(16, 128, 576))
+    with pytest.raises(ValueError, match="no dropout"):
+        A.mla(qd, c, wk, wv, dropout_rate=0.1)
 
 
 def test_dot_product_attention_refuses_array_masks():
@@ -221,3 +234,26 @@ def test_score_mods_arguments():
     m = A._score_mods(M.lower_mask(M.PrefixLMMask(3)), M.lower_bias(M.PerHeadScaleBias([2.0])), 2, 4, 4, 3, "cpu")
     assert m.prefix_lengths.tolist() == [3, 3] and m.head_scales.tolist() == [2.0, 2.0, 2.0]
     assert A._score_mods(M.lower_mask(M.CausalMask()), None, 1, 4, 4, 1, "cpu") is None
+
+
+def test_key_padding_lowering():
+    """KeyPaddingMask carries a per-row key count: [T] shared by every batch,
+    [B, T] per batch, rows past T count 0; one query row folds to per-batch
+    lengths (the split-KV route)."""
+    lm = M.lower_mask(M.KeyPaddingMask([4, 2]) & M.CausalMask())
+    assert lm.extended and lm.row_kv_lengths == [4, 2] and lm.causal_shift == 0
+    with pytest.raises(ValueError):
+        M.KeyPaddingMask([1]) & M.KVLenMask([1])
+    rows = A._row_kv_lengths(torch.tensor([4, 2]), 3, 3, "cpu")
+    assert rows.tolist() == [[4, 2, 0]] * 3 and rows.dtype == torch.int32
+    assert A._row_kv_lengths(torch.tensor([[5, 6, 7], [1, 2, 3]]), 2, 2, "cpu").tolist() == [[5, 6], [1, 2]]
+    assert A._row_kv_lengths(7, 2, 3, "cpu").tolist() == [[7, 7, 7]] * 2
+    assert A._row_kv_lengths(torch.tensor([True, False]), 1, 2, "cpu").tolist() == [[1, 0]]
+    assert A._row_kv_lengths(torch.tensor([1.5]), 1, 1, "cpu") is None
+    assert A._row_kv_lengths(torch.ones(3, 2, dtype=torch.int32), 2, 2, "cpu") is None  # batch mismatch
+    m = A._score_mods(M.LoweredMask(row_kv_lengths=rows), None, 3, 3, 5, 2, "cpu")
+    assert m.row_kv_lengths is rows and m.segment_q is None
+    q = torch.zeros(2, 1, 8, 128, dtype=torch.bfloat16)
+    k = torch.zeros(2, 4096, 8, 128, dtype=torch.bfloat16)
+    assert A.use_splitkv(q, k, mask=M.KeyPaddingMask(torch.tensor([9, 9])))
+    assert not A.use_splitkv(torch.zeros(2, 2, 8, 128, dtype=torch.bfloat16), k, mask=M.KeyPaddingMask([9, 9]))

@@ -75,6 +75,7 @@ def test_flash_rejects_invalid_arguments(lib, over, msg):
         (dict(softcap=-1.0), "softcap"),
         (dict(softcap=5.0, head_scales=1), "exclude"),
         (dict(segment_q=1), "segment_q and segment_k"),
+        (dict(segment_q=1, segment_k=1, row_kv_lengths=1), "row_kv_lengths excludes"),
         (dict(window_left=0x3FFFFFFF), "out of range"),
     ],
 )

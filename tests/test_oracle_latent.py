@@ -100,3 +100,84 @@ def test_rope_pair_rotation_closed_form():
     # interleaved pairs (x0, x1) -> (x0 cos - x1 sin, x1 cos + x0 sin)
     np.testing.assert_allclose(r[0], [math.cos(a0), math.sin(a0), -math.sin(a1), math.cos(a1)],
                                atol=1e-6)
+
+
+def _torch_materialized_grads(q, cache, wk, wv, do, keep, scale):
+    """float64 torch autograd through C W^T, a masked softmax and P V."""
+    import torch
+
+    ts = [torch.tensor(np.array(x), dtype=torch.float64, requires_grad=True) for x in (q, cache, wk, wv)]
+    tq, tc, twk, twv = ts
+    key = torch.einsum("bsr,hdr->bshd", tc, twk)
+    value = torch.einsum("bsr,hdr->bshd", tc, twv)
+    s = torch.einsum("bqhd,bkhd->bhqk", tq, key) * scale
+    s = s.masked_fill(~torch.as_tensor(keep)[:, None], float("-inf"))
+    o = torch.einsum("bhqk,bkhd->bqhd", torch.softmax(s, dim=-1), value)
+    (o * torch.tensor(do, dtype=torch.float64)).sum().backward()
+    return o.detach().numpy(), [t.grad.numpy() for t in ts]
+
+
+@pytest.mark.parametrize("mask_name", ["none", "causal", "kvlen"])
+def test_materialized_backward_matches_torch_autograd(mask_name):
+    """The reference's gradient test shape (tests/test_latent_attention.py:
+    280-297: b=2, s=32, heads=4, head_dim=16, rank=8, v_dim=12)."""
+    b, s, h, dk, r, dv = 2, 32, 4, 16, 8, 12
+    q, cache, do = rng_normal(3, (b, s, h, dk), (b, s, r), (b, s, h, dv))
+    wk, wv = rng_normal(4, (h, dk, r), (h, dv, r), scale=1 / math.sqrt(r))
+    masks = {"none": (None, np.ones((b, s, s), bool)),
+             "causal": (oracle.CausalMask(), np.broadcast_to(np.tril(np.ones((s, s), bool)), (b, s, s))),
+             "kvlen": (oracle.KVLenMask(np.array([32, 9], np.int32)),
+                       np.arange(s)[None, None, :] < np.array([32, 9])[:, None, None] + np.zeros((1, s, 1), int))}
+    mask, keep = masks[mask_name]
+    scale = 1 / math.sqrt(dk)
+    want_o, want = _torch_materialized_grads(q, cache, wk, wv, do, keep, scale)
+    # The oracle keeps K / V / O in the fp32 storage dtype of the reference's
+    # f32 mode (its einsum and attention outputs are fp32 arrays), so it sits
+    # within a few fp32 ulps of the float64 chain; a dropped term, a sign or a
+    # transposed operand is off by orders of magnitude more.
+    got_o = oracle.materialized_mla(q, cache, wk, wv, mask=mask, compute_dtype=np.float64)
+    np.testing.assert_allclose(got_o, want_o, atol=1e-6)
+    got = oracle.materialized_mla_backward(q, cache, wk, wv, do, mask=mask, compute_dtype=np.float64)
+    for name, g, w in zip(("dq", "dcache", "dwk", "dwv"), got, want):
+        assert g.shape == w.shape, name
+        np.testing.assert_allclose(g, w, atol=2e-6 * max(1.0, float(np.max(np.abs(w)))), err_msg=name)
+
+
+def test_materialized_backward_finite_differences():
+    b, s, h, dk, r, dv = 1, 6, 2, 5, 3, 4
+    q, cache, do = rng_normal(5, (b, s, h, dk), (b, s, r), (b, s, h, dv))
+    wk, wv = rng_normal(6, (h, dk, r), (h, dv, r))
+    mask = oracle.CausalMask()
+    args = [np.asarray(x, np.float64) for x in (q, cache, wk, wv)]
+
+    def loss(xs):
+        o = oracle.materialized_mla(*xs, mask=mask, compute_dtype=np.float64)
+        return float(np.sum(o * do))
+
+    grads = oracle.materialized_mla_backward(*args, do, mask=mask, compute_dtype=np.float64)
+    eps = 1e-3
+    rng = np.random.default_rng(7)
+    for i, g in enumerate(grads):
+        for _ in range(4):
+            idx = tuple(int(rng.integers(n)) for n in args[i].shape)
+            up = [a.copy() for a in args]
+            dn = [a.copy() for a in args]
+            up[i][idx] += eps
+            dn[i][idx] -= eps
+            fd = (loss(up) - loss(dn)) / (2 * eps)
+            # the forward stores fp32 (see above), so the step is large and the
+            # bound covers its O(eps^2) truncation; planted mistakes are O(1e-1)
+            assert abs(fd - g[idx]) <= 3e-3 * max(1.0, abs(fd)), (i, idx, fd, g[idx])
+
+
+def test_materialized_bf16_close_to_f32():
+    b, s, h, dk, r, dv = 2, 64, 2, 32, 48, 24
+    q, cache, do = rng_normal(8, (b, s, h, dk), (b, s, r), (b, s, h, dv))
+    wk, wv = rng_normal(9, (h, dk, r), (h, dv, r), scale=1 / math.sqrt(r))
+    o32 = oracle.materialized_mla(q, cache, wk, wv, mask=oracle.CausalMask())
+    o16 = oracle.materialized_mla(q, cache, wk, wv, mask=oracle.CausalMask(), dtype="bf16")
+    assert np.max(np.abs(o32 - o16)) <= 3e-2
+    g32 = oracle.materialized_mla_backward(q, cache, wk, wv, do, mask=oracle.CausalMask())
+    g16 = oracle.materialized_mla_backward(q, cache, wk, wv, do, mask=oracle.CausalMask(), dtype="bf16")
+    for a, c in zip(g32, g16):
+        assert np.max(np.abs(a - c)) <= 3e-2 * max(1.0, np.max(np.abs(a)))

@@ -241,3 +241,36 @@ def test_per_head_scale():
     np.testing.assert_allclose(b(scores, 0, _idx(2), _idx(3)), 2 * scores)
     np.testing.assert_allclose(b(scores, 1, _idx(2), _idx(3)), 0.5 * scores)
     np.testing.assert_allclose(b.grad_tile(scores, 0, 1, 0, 2, 0, 3), 0.5 * scores)
+
+
+def test_key_padding_known_answer():
+    """probjax tests/test_attention_mask_bias.py:182-188: a per-row vector
+    payload keeps k < seg_q[q]."""
+    seg_q = np.array([1, 3, 5, 6], np.int32)
+    got = oracle.KeyPaddingMask(np.array([6], np.int32))(_idx(4), _idx(6), seg_q=seg_q)
+    np.testing.assert_array_equal(got, _idx(6)[None, :] < seg_q[:, None])
+
+
+def test_key_padding_payload_rows():
+    """The XLA path reads the payload per query position: a [T] payload is
+    shared by every batch ([1, T, 1, 1], attention_mask_bias.py:1186-1187),
+    [B, T] is paged by batch, rows past T read the zero fill; a scalar payload
+    is KVLenMask with one length."""
+    m = oracle.KeyPaddingMask(np.array([16, 12], np.int32))
+    for b in range(2):
+        keep = m.tile_keep(b, _idx(4), _idx(20))
+        np.testing.assert_array_equal(keep[0], _idx(20) < 16)
+        np.testing.assert_array_equal(keep[1], _idx(20) < 12)
+        assert not keep[2:].any()
+    m2 = oracle.KeyPaddingMask(np.array([[3, 1, 2], [0, 5, 5]], np.int32))
+    np.testing.assert_array_equal(m2.tile_keep(1, _idx(3), _idx(6)).sum(axis=1), [0, 5, 5])
+    np.testing.assert_array_equal(m2.tile_keep(0, _idx(4), _idx(6)).sum(axis=1), [3, 1, 2, 0])
+    # a window of rows reads the same counts as the whole
+    np.testing.assert_array_equal(m2.tile_keep(0, _idx(4)[1:3], _idx(6)), m2.tile_keep(0, _idx(4), _idx(6))[1:3])
+    s = oracle.KeyPaddingMask(np.int32(7))
+    kv = oracle.KVLenMask(np.array([7, 7], np.int32))
+    for b in range(2):
+        np.testing.assert_array_equal(s.tile_keep(b, _idx(5), _idx(9)), kv.tile_keep(b, _idx(5), _idx(9)))
+    # boolean payloads compare as 0 / 1
+    mb = oracle.KeyPaddingMask(np.array([True, False]))
+    np.testing.assert_array_equal(mb.tile_keep(0, _idx(2), _idx(3)).sum(axis=1), [1, 0])
