@@ -18,6 +18,8 @@ algorithm must move: valid K/V + q + o; bias configs include the bias once).
 ``C2B`` is the backward of the headline workload (one ``pjx_flash_bwd`` call)
 and ``C2FB`` forward + backward, both as TFLOP/s with the reference
 benchmark's FlashAttention convention (fwd+bwd = 3.5x the forward's FLOPs).
+``C5P`` is the materialised-MLA up-projection alone (``pjx_mla_project``) and
+``C5M`` a materialised-MLA causal prefill (projection + flash forward).
 
 ``cpu_baseline`` times the numpy restatement of probjax's XLA CPU path
 (``oracle.xla_attention``, 256x256 tiles with causal tile skipping) on one
@@ -249,8 +251,51 @@ def make_c2fb(dev, gen):
                 kernel="flash_fwd_bf16_kernel<128,false,0> + flash_bwd_*<128,false,0>")
 
 
+def _mla_prefill_inputs(dev, gen):
+    import torch
+
+    B, L, H, R, D = 1, 4096, 16, 512, 128
+    q = _randn((B, L, H, D), gen, dev, torch.bfloat16)
+    cache = _randn((B, L, R), gen, dev, torch.bfloat16)
+    wk, wv = (_randn((H, D, R), gen, dev, torch.bfloat16, scale=1 / math.sqrt(R)) for _ in range(2))
+    return B, L, H, R, D, q, cache, wk, wv
+
+
+def make_c5p(dev, gen):
+    """The latent up-projection alone (pjx_mla_project: K and V of a 4096-token
+    latent, 16 heads x 128), a GEMM of 2 * M * R * N FLOPs."""
+    from probjax_amd.hip_attention import mla_project
+
+    B, L, H, R, D, _, cache, wk, wv = _mla_prefill_inputs(dev, gen)
+    flop = 2 * B * L * R * H * 2 * D
+    nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
+    fn = lambda: mla_project(cache, wk, wv, width=D)  # noqa: E731
+    return dict(name="MLA up-projection bf16 B=1 S=4096 R=512 H=16 dk=dv=128 (K and V)", fn=fn,
+                flop=flop, bytes=nbytes, bound="mfma", dtype="bf16", kernel="mla_project_bf16_kernel")
+
+
+def make_c5m(dev, gen):
+    """Materialised latent attention prefill (mla with wk / wv, causal): the
+    up-projection then the flash forward over the materialised K / V.  FLOPs:
+    the projection's plus the causal attention's (reference convention)."""
+    from probjax_amd.hip_attention import flash_attention_fwd, mla_project
+
+    B, L, H, R, D, q, cache, wk, wv = _mla_prefill_inputs(dev, gen)
+    sc = 1 / math.sqrt(D)
+
+    def fn():
+        k, v = mla_project(cache, wk, wv, width=D)
+        return flash_attention_fwd(q, k, v, sm_scale=sc, causal=True)
+
+    flop = 2 * B * L * R * H * 2 * D + 4 * B * H * L * L * D / 2
+    nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
+    return dict(name="MLA materialised causal prefill bf16 B=1 L=4096 R=512 H=16 dk=dv=128", fn=fn,
+                flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
+                kernel="mla_project_bf16_kernel + flash_fwd_bf16_kernel<128,false,0>")
+
+
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
-          "C2B": make_c2b, "C2FB": make_c2fb}
+          "C2B": make_c2b, "C2FB": make_c2fb, "C5P": make_c5p, "C5M": make_c5m}
 
 
 def _settle(fn, seconds):

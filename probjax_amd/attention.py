@@ -512,6 +512,60 @@ def _mla_materialized(q, cache, wk, wv, *, mask, bias, sm_scale):
     return _MaterializedMLAFunction.apply(q, cache, wk, wv, st)
 
 
+def _absorbed_cheaper(l_q: int, kv_len: int, rank: int, dk: int, dv: int) -> bool:
+    """probjax's choice between the two exact factorisations of projected
+    latent attention, by FLOP count (latent_attention.py:616-620)."""
+    materialized = kv_len * rank * (dk + dv) + l_q * kv_len * (dk + dv)
+    absorbed = l_q * rank * (dk + dv) + 2 * l_q * kv_len * rank
+    return absorbed < materialized
+
+
+def _mla_absorbed_lengths(q, cache, wk, wv, mask, bias):
+    """Per-batch KV lengths (or "all") when a projected ``mla`` call is cheaper
+    absorbed and the latent decode kernel computes it exactly; else None."""
+    B, l_q, H, dk = q.shape
+    R, dv = cache.shape[-1], wv.shape[1]
+    if bias is not None or _needs_grad(q, cache, wk, wv):
+        return None
+    if not (q.dtype == cache.dtype == wk.dtype == wv.dtype == torch.bfloat16):
+        return None
+    if (R, R) not in MLA_SHAPES or l_q * H > DECODE_MAX_ROWS:
+        return None
+    if not _absorbed_cheaper(l_q, cache.shape[1], R, dk, dv):
+        return None
+    if not all(hip_device(t) and t.device == q.device for t in (q, cache, wk, wv)):
+        return None
+    lm = lower_mask(mask)
+    if lm is None:
+        return None
+    if lm.row_kv_lengths is not None and l_q == 1:
+        rows = _row_kv_lengths(lm.row_kv_lengths, B, 1, q.device)
+        if rows is None:
+            return None
+        lm.row_kv_lengths, lm.kv_lengths = None, rows[:, 0]
+    if lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
+        return None
+    if lm.kv_lengths is None:
+        return "all"
+    return _lengths_tensor(lm.kv_lengths, B, q.device)
+
+
+def _mla_absorbed(q, cache, wk, wv, kv_lengths, sm_scale):
+    """Projected ``mla`` in the absorbed factorisation (latent_attention.py:
+    621-623): ``q W_K`` attends over the latent (``K = V = C``) on the latent
+    decode kernel, then ``W_V`` maps the latent-space output.  The two
+    per-head products are plain batched GEMMs."""
+    B, l_q, H, dk = q.shape
+    R, dv = cache.shape[-1], wv.shape[1]
+    qh = q.permute(2, 0, 1, 3).reshape(H, B * l_q, dk).contiguous()
+    q_lat = torch.bmm(qh, wk.contiguous()).reshape(H, B, l_q, R).permute(1, 2, 0, 3).contiguous()
+    o_lat = hip.mla_decode(q_lat, cache, sm_scale=float(sm_scale),
+                           kv_lengths=None if isinstance(kv_lengths, str) else kv_lengths)
+    oh = o_lat.permute(2, 0, 1, 3).reshape(H, B * l_q, R).contiguous()
+    out = torch.bmm(oh, wv.transpose(1, 2).contiguous())
+    return out.reshape(H, B, l_q, dv).permute(1, 2, 0, 3).contiguous()
+
+
 def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
         sm_scale: float | None = None, dropout_rate: float = 0.0, v_dim: int | None = None,
         **unused_tuning):
@@ -528,7 +582,11 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     bias of the flash route (the reference's contract: equal to ``mha`` over
     the materialised K/V, tests/test_latent_attention.py:341-379), bf16 or
     fp32, differentiable in ``q``, ``cache``, ``wk`` and ``wv``; head dims up
-    to 128.  Dropout raises ``ValueError``.
+    to 128.  Decode-shaped calls that probjax's FLOP rule (:616-620) finds
+    cheaper absorbed run absorbed on the latent decode kernel (no gradient
+    needed, bf16, no bias, ``None`` / ``KVLenMask`` / one-row
+    ``KeyPaddingMask``, rank 128 / 512 / 576, ``Lq * H <= 16``); the rest
+    materialise.  Dropout raises ``ValueError``.
     """
     del rng, unused_tuning
     if q.ndim != 4:
@@ -556,6 +614,9 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     if wk is not None:
         if dropout_rate > 0:
             raise ValueError("the HIP latent-attention kernels take no dropout")
+        lengths = _mla_absorbed_lengths(q, cache, wk, wv, mask, bias)
+        if lengths is not None:
+            return _mla_absorbed(q, cache, wk, wv, lengths, sm_scale)
         return _mla_materialized(q, cache, wk, wv, mask=mask, bias=bias, sm_scale=sm_scale)
     if bias is not None or dropout_rate > 0:
         raise ValueError("the HIP latent-attention kernel takes no bias or dropout")

@@ -18,11 +18,16 @@
 // (grid.y < ny) and V (grid.y >= ny).
 //
 // bf16: 128 x 128 output tiles, 4 waves of 64 x 64 (2 x 2 MFMA 32x32x16
-// blocks), rank chunks of 64 staged through LDS via registers (the next
-// chunk's global loads are in flight while the current one is multiplied).
+// blocks).  Ranks that are a multiple of 8 stream chunks of 32 rank entries
+// straight from HBM into a 2-stage LDS ring (buffer -> LDS loads, the next
+// chunk in flight while the current one is multiplied, one barrier per
+// chunk); other ranks stage chunks of 64 through registers with element
+// loads.
 // fp32: 64 x 64 tiles of plain FMA, 4 x 4 per thread (no roundings).
 #include <hip/hip_runtime.h>
 #include <stdint.h>
+
+#include <algorithm>
 
 #include "pjx_common.h"
 #include "pjx_internal.h"
@@ -61,7 +66,8 @@ __device__ __forceinline__ u32x4 load_chunk_bf16(const uint16_t* row, int r0, in
   return u32x4{h[0] | (h[1] << 16), h[2] | (h[3] << 16), h[4] | (h[5] << 16), h[6] | (h[7] << 16)};
 }
 
-__global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
+// Ranks that are not a multiple of 8: register-staged chunks, element loads.
+__global__ __launch_bounds__(256, 2) void mla_project_bf16_ragged_kernel(ProjArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBM * kPitch];
   unsigned char* As = lds;
   unsigned char* Bs = lds + kBM * kPitch;
@@ -151,6 +157,129 @@ __global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
         if (m < a.M) O[m * ncols + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
       }
     }
+}
+
+// Ranks that are a multiple of 8: buffer -> LDS ring.  A staged row holds
+// 32 rank entries (64 bytes, 4 chunks of 16); chunk c of row r sits in slot
+// c ^ ((r / 4) % 4), so the 16 rows one pass of an MFMA operand read touches
+// cover the 64 banks once.  One buffer -> LDS load moves 16 rows (64 lanes x
+// 16 bytes).  34 KiB of LDS per workgroup: 4 workgroups per CU.
+constexpr int kRK = 32;                // rank entries per ring chunk
+constexpr int kRowB = kRK * 2;
+constexpr int kTileB = kBM * kRowB;    // one operand's chunk: 8 KiB
+constexpr int kStageB = 2 * kTileB;    // A and B
+constexpr uint32_t kOff = 0x80000000u;  // a buffer offset past every range: loads 0
+constexpr int kOutPitch = kBN * 2 + 16;  // LDS bytes per output row in the epilogue
+constexpr int kLdsB = 2 * kStageB > kBM * kOutPitch ? 2 * kStageB : kBM * kOutPitch;
+
+__global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
+  __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsB];
+  const int which = blockIdx.y >= (unsigned)a.ny ? 1 : 0;
+  const int n0 = (blockIdx.y - which * a.ny) * kBN;
+  const int64_t m0 = (int64_t)blockIdx.x * kBM;
+  const int ncols = a.H * a.width;
+  const int dim = a.dim[which];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // (readfirstlane: the descriptor fields must be wave-uniform scalars)
+  const uint32_t abytes = __builtin_amdgcn_readfirstlane((uint32_t)(min<int64_t>(kBM, a.M - m0) * a.R * 2));
+  const uint32_t bbytes = __builtin_amdgcn_readfirstlane((uint32_t)((int64_t)a.H * dim * a.R * 2));
+  const rsrc_t ra = make_rsrc((const uint16_t*)a.cache + m0 * a.R, abytes);
+  const rsrc_t rb = make_rsrc(a.w[which], bbytes);
+
+  // This lane's rows in its wave's 2 loads per operand: wave*32 + 16*i +
+  // lane/4; it fetches logical chunk (lane%4) ^ ((row/4)%4) of each.
+  const int lrow = lane >> 2;
+  const int lchunk = (lane & 3) ^ ((lrow >> 2) & 3);  // (row/4)%4 == (lrow/4)%4
+  uint32_t aoff[2], boff[2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int row = wave * 32 + 16 * i + lrow;
+    aoff[i] = (uint32_t)(row * a.R + 8 * lchunk) * 2u;
+    const int n = n0 + row;
+    const int h = n / a.width, d = n - h * a.width;
+    boff[i] = (n < ncols && d < dim) ? (uint32_t)(((int64_t)h * dim + d) * a.R + 8 * lchunk) * 2u : kOff;
+  }
+  auto issue = [&](int t, int stage) {
+    const int k0 = t * kRK;
+    const bool in = k0 + 8 * lchunk < a.R;  // chunks past the rank load 0
+    unsigned char* base = lds + stage * kStageB + wave * 32 * kRowB;
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      buffer_load_lds16(ra, base + 16 * i * kRowB, in ? aoff[i] + 2u * k0 : kOff);
+      buffer_load_lds16(rb, base + kTileB + 16 * i * kRowB, (in && boff[i] != kOff) ? boff[i] + 2u * k0 : kOff);
+    }
+  };
+
+  f32x16 acc[2][2];
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j) acc[i][j] = f32x16{};
+
+  const int wr = (wave >> 1) * 64, wc = (wave & 1) * 64;
+  // operand reads: row (lane % 32) of a 32-row block, logical chunk 2*ks + lane/32
+  const int rrow = lane & 31, rsw = (rrow >> 2) & 3;
+  const int nk = (a.R + kRK - 1) / kRK;
+  issue(0, 0);
+  for (int t = 0; t < nk; ++t) {
+    wait_vmcnt<0>();
+    stage_barrier();  // chunk t landed for every wave; every wave is done with chunk t-1
+    if (t + 1 < nk) issue(t + 1, (t + 1) & 1);
+    const unsigned char* As = lds + (t & 1) * kStageB;
+    const unsigned char* Bs = As + kTileB;
+#pragma unroll
+    for (int ks = 0; ks < kRK / 16; ++ks) {
+      const int slot = 16 * ((2 * ks + (lane >> 5)) ^ rsw);
+      bf16x8 af[2], bf[2];
+#pragma unroll
+      for (int i = 0; i < 2; ++i) af[i] = as_bf16x8(*(const u32x4*)(As + (wr + 32 * i + rrow) * kRowB + slot));
+#pragma unroll
+      for (int j = 0; j < 2; ++j) bf[j] = as_bf16x8(*(const u32x4*)(Bs + (wc + 32 * j + rrow) * kRowB + slot));
+      // W as the MFMA's first operand: the result is out^T, so each lane ends
+      // with 4 consecutive output columns of one row per register group
+#pragma unroll
+      for (int i = 0; i < 2; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(bf[j], af[i], acc[i][j]);
+    }
+  }
+
+  // The 128 x 128 bf16 tile goes through LDS so that the HBM stores are
+  // whole 256-byte rows.  Register r of block (i, j): row wr + 32i + lane%32,
+  // columns wc + 32j + 8(r/4) + 4(lane/32) + r%4 (4 consecutive per group).
+  stage_barrier();  // every wave is done with the ring
+#pragma unroll
+  for (int i = 0; i < 2; ++i)
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const f32x16& c = acc[i][j];
+        const int row = wr + 32 * i + (lane & 31), col = wc + 32 * j + 8 * g + 4 * (lane >> 5);
+        *(u32x2*)(lds + row * kOutPitch + col * 2) =
+            u32x2{pack_bf16x2(c[4 * g], c[4 * g + 1]), pack_bf16x2(c[4 * g + 2], c[4 * g + 3])};
+      }
+  stage_barrier();
+  uint16_t* O = (uint16_t*)a.out[which];
+  const bool vec = (ncols & 7) == 0;
+#pragma unroll
+  for (int q = 0; q < kBM * kBN / 8 / 256; ++q) {
+    const int idx = tid + 256 * q;
+    const int row = idx / (kBN / 8), c8 = 8 * (idx % (kBN / 8));
+    const int64_t m = m0 + row;
+    const int n = n0 + c8;
+    if (m >= a.M || n >= ncols) continue;
+    const u32x4 v = *(const u32x4*)(lds + row * kOutPitch + c8 * 2);
+    uint16_t* dst = O + m * ncols + n;
+    if (vec) {
+      *(u32x4*)dst = v;
+    } else {
+      const uint32_t w[4] = {v[0], v[1], v[2], v[3]};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (n + e < ncols) dst[e] = (uint16_t)(w[e >> 1] >> (16 * (e & 1)));
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -252,7 +381,13 @@ extern "C" int pjx_mla_project(int dtype, const void* cache, const void* wk, con
     a.ny = (ncols + kBN - 1) / kBN;
     const int64_t gx = (M + kBM - 1) / kBM;
     if (gx > 0x7fffffff) return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
-    hipLaunchKernelGGL(mla_project_bf16_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+    // the ring's buffer offsets are 32-bit: 128 latent rows and each weight tensor
+    const bool ring = (rank & 7) == 0 && 128 * rank * 2 < ((int64_t)1 << 31) &&
+                      heads * std::max(qk_dim, v_dim) * rank * 2 < ((int64_t)1 << 31);
+    if (ring)
+      hipLaunchKernelGGL(mla_project_bf16_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+    else
+      hipLaunchKernelGGL(mla_project_bf16_ragged_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
   } else {
     a.ny = (ncols + kFN - 1) / kFN;
     const int64_t gx = (M + kFM - 1) / kFM;

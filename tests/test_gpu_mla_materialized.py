@@ -134,19 +134,32 @@ def test_materialized_mla_forward_and_grads(device, dtype, mask_name, B, Lq, S, 
     assert torch.equal(out.detach(), out2)
 
 
-def test_materialized_mla_decode_shape(device):
-    """One query row per sequence over a long latent cache with per-sequence
-    lengths (the shape of a cached decode step)."""
+def test_projected_decode_routes(device, monkeypatch):
+    """One query row per sequence over a long latent cache (a cached decode
+    step): without gradients probjax's FLOP rule picks the absorbed form,
+    which runs on the latent decode kernel; with gradients the call
+    materialises.  Both against the oracle (xla_mla follows the same rule)."""
     import torch
     from probjax_amd import attention as A
+    from probjax_amd import hip_attention as H_
     from probjax_amd.masks import KVLenMask
 
     B, S, H, R, d = 2, 2048, 16, 512, 128
-    print(f"mla-mat decode B={B} S={S} H={H} R={R} d={d}", flush=True)
+    print(f"mla projected decode B={B} S={S} H={H} R={R} d={d}", flush=True)
     lens = np.array([2048, 777], np.int32)
     q, cache = (oracle.round_bf16(x) for x in rng_normal(66, (B, 1, H, d), (B, S, R)))
     wk, wv = (oracle.round_bf16(x) for x in rng_normal(67, (H, d, R), (H, d, R), scale=1 / math.sqrt(R)))
-    got = A.mla(*(to_dev(x, device, torch.bfloat16) for x in (q, cache, wk, wv)),
-                mask=KVLenMask(torch.from_numpy(lens).to(device)))
-    want = oracle.materialized_mla(q, cache, wk, wv, mask=oracle.KVLenMask(lens), dtype="bf16")
+    assert A._absorbed_cheaper(1, S, R, d, d)
+    calls = []
+    real = H_.mla_decode
+    monkeypatch.setattr(H_, "mla_decode", lambda *a, **kw: calls.append(1) or real(*a, **kw))
+    ts = [to_dev(x, device, torch.bfloat16) for x in (q, cache, wk, wv)]
+    mask = KVLenMask(torch.from_numpy(lens).to(device))
+    got = A.mla(*ts, mask=mask)
+    assert calls == [1], "the absorbed route runs the latent decode kernel"
+    want = oracle.xla_mla(q, cache, wk, wv, mask=oracle.KVLenMask(lens), dtype="bf16")
     assert max_abs(to_np(got), want) <= 2e-2
+    got_m = A.mla(ts[0].requires_grad_(True), *ts[1:], mask=mask)
+    assert calls == [1], "with gradients the call materialises"
+    want_m = oracle.materialized_mla(q, cache, wk, wv, mask=oracle.KVLenMask(lens), dtype="bf16")
+    assert max_abs(to_np(got_m), want_m) <= 2e-2

@@ -257,3 +257,11 @@ def test_key_padding_lowering():
     k = torch.zeros(2, 4096, 8, 128, dtype=torch.bfloat16)
     assert A.use_splitkv(q, k, mask=M.KeyPaddingMask(torch.tensor([9, 9])))
     assert not A.use_splitkv(torch.zeros(2, 2, 8, 128, dtype=torch.bfloat16), k, mask=M.KeyPaddingMask([9, 9]))
+
+
+def test_mla_absorb_rule():
+    """probjax's FLOP rule (latent_attention.py:616-620): decoding absorbs,
+    full-length prefill with a wide latent materialises."""
+    assert A._absorbed_cheaper(1, 4096, 512, 128, 128)
+    assert not A._absorbed_cheaper(4096, 4096, 512, 128, 128)
+    assert A._absorbed_cheaper(4096, 4096, 64, 128, 128)  # narrow latent
