@@ -36,6 +36,9 @@ from .masks import (  # noqa: F401
     QKVLengthMask,
     SameSegmentMask,
     KeyPaddingMask,
+    LowRankBias,
+    BatchedLowRankBias,
+    LearnedAlibiBias,
     SeqLenMask,
     SoftCappingBias,
     SumBias,
@@ -45,3 +48,4 @@ from .attention_xla import auto_strategy, xla_attention  # noqa: F401
 from .splitkv import default_num_splits, splitkv_forward  # noqa: F401
 from .latent import materialize_kv, materialized_mla, materialized_mla_backward, xla_mla  # noqa: F401
 from .rope import apply_rotary, inv_freq  # noqa: F401
+from .lowrank import fold_low_rank, flex_low_rank, flex_low_rank_backward, split_low_rank_bias  # noqa: F401

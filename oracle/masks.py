@@ -545,6 +545,113 @@ class PerHeadScaleBias(AttentionBias):
         return np.full_like(scores, self._scale(h))
 
 
+class LowRankBias(AttentionBias):
+    """:1926-2024: ``scores + scale * U[h, q] . V[h, k]``, factors
+    ``[H|1, max_length, rank]``."""
+
+    def __init__(self, query_factors, key_factors, *, scale: float = 1.0):
+        qf = np.asarray(query_factors, np.float32)
+        kf = np.asarray(key_factors, np.float32)
+        if qf.ndim == 2:
+            qf = qf[None]
+        if kf.ndim == 2:
+            kf = kf[None]
+        if qf.ndim != 3 or kf.ndim != 3 or qf.shape[-1] != kf.shape[-1] or qf.shape[0] != kf.shape[0]:
+            raise ValueError("factors must have shape [H|1, length, rank] with one rank and head count")
+        if scale < 0:
+            raise ValueError("scale must be non-negative")
+        self.query_factors, self.key_factors, self.scale = qf, kf, float(scale)
+
+    @property
+    def rank(self):
+        return self.query_factors.shape[-1]
+
+    def factors(self, q_len, kv_len, num_heads):
+        """:1962-1995 -> ``[1, length, heads, rank]``."""
+        if self.query_factors.shape[0] not in (1, num_heads):
+            raise ValueError("factor head count cannot broadcast")
+        qf = np.broadcast_to(self.query_factors[:, :q_len], (num_heads, q_len, self.rank))
+        kf = np.broadcast_to(self.key_factors[:, :kv_len], (num_heads, kv_len, self.rank))
+        return np.swapaxes(qf, 0, 1)[None], np.swapaxes(kf, 0, 1)[None]
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        # :1997-2013
+        head = 0 if self.query_factors.shape[0] == 1 else int(h_idx)
+        u = self.query_factors[head][np.asarray(q_idx)]
+        v = self.key_factors[head][np.asarray(k_idx)]
+        return scores + np.float32(self.scale) * (u @ v.T)
+
+
+class BatchedLowRankBias(AttentionBias):
+    """:2028-2190: per-example ``scale * U[b, q] . V[b, k]`` (factors
+    ``[B, length, rank]``, a query length of 1 broadcasting); evaluated per
+    example as ``dense`` (:2154-2180) does."""
+
+    def __init__(self, query_factors, key_factors, *, scale: float = 1.0):
+        qf = np.asarray(query_factors, np.float32)
+        kf = np.asarray(key_factors, np.float32)
+        if qf.ndim != 3 or kf.ndim != 3 or qf.shape[-1] != kf.shape[-1] or qf.shape[0] != kf.shape[0]:
+            raise ValueError("factors must have shape [B, length, rank] with one rank and batch")
+        if scale < 0:
+            raise ValueError("scale must be non-negative")
+        self.query_factors, self.key_factors, self.scale = qf, kf, float(scale)
+
+    @classmethod
+    def from_key_bias(cls, key_bias, q_len=1):
+        kb = np.asarray(key_bias, np.float32)
+        return cls(np.ones((kb.shape[0], q_len, 1), np.float32), kb[..., None])
+
+    @property
+    def rank(self):
+        return self.query_factors.shape[-1]
+
+    def factors(self, q_len, kv_len, num_heads):
+        """:2089-2124 -> ``[B, length, heads, rank]``."""
+        b = self.query_factors.shape[0]
+        qf = self.query_factors if self.query_factors.shape[1] == 1 else self.query_factors[:, :q_len]
+        qf = np.broadcast_to(qf[:, :, None, :], (b, q_len, num_heads, self.rank))
+        kf = np.broadcast_to(self.key_factors[:, :kv_len, None, :], (b, kv_len, num_heads, self.rank))
+        return qf, kf
+
+    def tile_add(self, scores, b, h, q0, bq, k0, kc):
+        qf = self.query_factors[b]
+        u = np.broadcast_to(qf, (bq, self.rank)) if qf.shape[0] == 1 else qf[q0 : q0 + bq]
+        v = self.key_factors[b, k0 : k0 + kc]
+        return scores + np.float32(self.scale) * (u @ v.T)
+
+
+class LearnedAlibiBias(AttentionBias):
+    """:2258-2352: ``scores - slopes[h] * ((q + q_off) - (k + k_off))``, as
+    the rank-2 factors ``U = [-s q_pos, 1]``, ``V = [1, s k_pos]``."""
+
+    rank = 2
+    scale = 1.0
+
+    def __init__(self, slopes, *, query_offset=0, key_offset=0):
+        sl = np.asarray(slopes, np.float32)
+        if sl.ndim == 0:
+            sl = sl[None]
+        if sl.ndim != 1:
+            raise ValueError("slopes must have shape [H|1]")
+        self.slopes, self.query_offset, self.key_offset = sl, int(query_offset), int(key_offset)
+
+    def factors(self, q_len, kv_len, num_heads):
+        """:2291-2318 -> ``[1, length, heads, 2]``."""
+        sl = np.broadcast_to(self.slopes, (num_heads,))
+        qp = np.arange(q_len, dtype=np.float32) + self.query_offset
+        kp = np.arange(kv_len, dtype=np.float32) + self.key_offset
+        qf = np.stack((-sl[:, None] * qp[None], np.ones((num_heads, q_len), np.float32)), -1)
+        kf = np.stack((np.ones((num_heads, kv_len), np.float32), sl[:, None] * kp[None]), -1)
+        return np.swapaxes(qf, 0, 1)[None], np.swapaxes(kf, 0, 1)[None]
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        # :2320-2334
+        head = 0 if self.slopes.shape[0] == 1 else int(h_idx)
+        qp = np.asarray(q_idx) + self.query_offset
+        kp = np.asarray(k_idx) + self.key_offset
+        return scores - self.slopes[head] * (qp[:, None] - kp[None, :]).astype(np.float32)
+
+
 class SumBias(AttentionBias):
     def __init__(self, lhs: AttentionBias, rhs: AttentionBias):
         self.lhs, self.rhs = lhs, rhs

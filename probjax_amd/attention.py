@@ -43,7 +43,7 @@ import os
 import torch
 
 from . import hip_attention as hip
-from .masks import LoweredBias, LoweredMask, lower_bias, lower_mask
+from .masks import LoweredBias, LoweredMask, lower_bias, lower_mask, split_low_rank_bias
 
 HIP_ARCH = "gfx950"
 FLASH_HEAD_DIMS = (64, 128)
@@ -680,6 +680,16 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
         query, key, value = query[None], key[None], value[None]
     active_dropout = dropout_rate if not deterministic and dropout_rate > 0 else 0.0
     out = None
+    low_rank, rest = split_low_rank_bias(bias)
+    out_dim = None
+    if low_rank:
+        folded = _fold_low_rank(query, key, value, low_rank, float(sm_scale))
+        if folded is None:
+            raise ValueError(
+                f"implementation={implementation!r}: head_dim {query.shape[-1]} plus the low-rank "
+                f"bias ranks {[t.rank for t in low_rank]} exceeds the kernels' {FLASH_HEAD_DIMS[-1]}")
+        query, key, value, out_dim = folded
+        bias = rest
     e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=active_dropout)
     if e is not None and (implementation == "hip" or device_table_enabled()):
         out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv)
@@ -690,7 +700,47 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
             + ("" if implementation == "hip" or device_table_enabled()
                else " (the HIP route is switched off by PROBJAX_ATTENTION_HIP=0)")
         )
+    if out_dim is not None:
+        out = out[..., :out_dim]
     return out[0] if squeeze else out
+
+
+def _fold_low_rank(query, key, value, terms, sm_scale: float):
+    """Low-rank bias terms folded into Q/K (probjax ``flex_attention``,
+    layers/attention.py:1600-1635): each term's factors, scaled by
+    ``sqrt(scale / sm_scale)`` in the input dtype, are appended to the query
+    and key features (V gets zero features), so ``sm_scale * q'.k'`` carries
+    ``scale * U.V``; K/V are repeated to the query heads first.  The features
+    are zero-padded to a kernel head dim.  Returns ``(q', k', v', output
+    width)``, or None when the folded head dim exceeds the kernels'.  Torch
+    autograd carries the gradients of the concatenation to the factors."""
+    if sm_scale <= 0:
+        raise ValueError("LowRankBias requires a positive sm_scale")
+    hq = query.shape[-2]
+    if key.shape[-2] != hq:
+        rep = hq // key.shape[-2]
+        key = key.repeat_interleave(rep, dim=-2)
+        value = value.repeat_interleave(rep, dim=-2)
+    q_extra, k_extra = [], []
+    for t in terms:
+        qf, kf = t.factors(query.shape[-3], key.shape[-3], hq, dtype=query.dtype)
+        f = math.sqrt(t.scale / sm_scale)
+        q_extra.append(qf.to(query.device).expand(tuple(query.shape[:-1]) + (t.rank,)) * f)
+        k_extra.append(kf.to(key.device).expand(tuple(key.shape[:-1]) + (t.rank,)) * f)
+    extra = sum(x.shape[-1] for x in q_extra)
+    width = next((w for w in FLASH_HEAD_DIMS if w >= query.shape[-1] + extra), None)
+    if width is None:
+        return None
+    pad = width - query.shape[-1] - extra
+
+    def zeros(like, n):
+        return like.new_zeros(tuple(like.shape[:-1]) + (n,))
+
+    out_dim = value.shape[-1]
+    query = torch.cat((query, *q_extra, zeros(query, pad)), dim=-1)
+    key = torch.cat((key, *k_extra, zeros(key, pad)), dim=-1)
+    value = torch.cat((value, zeros(value, width - out_dim)), dim=-1)
+    return query, key, value, out_dim
 
 
 def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=None,

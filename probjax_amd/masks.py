@@ -26,6 +26,10 @@ attention_mask_bias.py):
   kernels (what the kernels evaluate is an AND of the above);
 * ``DenseBias``       -- :1807-1922, ``scores + bias[b|0, h|0, q, k]`` with an
   fp32 ``[B|1, H|1, Q, K]`` tensor;
+* low-rank biases     -- ``LowRankBias``, ``BatchedLowRankBias``,
+  ``LearnedAlibiBias`` (:1926-2352): ``flex_attention`` and
+  ``dot_product_attention`` fold their factors into Q/K
+  (``split_low_rank_bias``), as probjax's ``flex_attention`` does;
 * score modifiers     -- ``IdentityBias``, ``ConstantBias``, ``CausalAlibiBias``,
   ``SymmetricAlibiBias``, ``DistanceDecayBias`` (additive, composable with
   ``+`` / ``SumBias`` :553-582) and ``SoftCappingBias`` / ``PerHeadScaleBias``
@@ -189,6 +193,148 @@ class SoftCappingBias(AttentionBias):
 class PerHeadScaleBias(AttentionBias):
     def __init__(self, scales):
         self.scales = scales
+
+
+class LowRankBias(AttentionBias):
+    """``scale * U[h, q] . V[h, k]`` with factors ``[H|1, max_length, rank]``
+    (attention_mask_bias.py:1926-2024); ``flex_attention`` folds the factors
+    into Q/K."""
+
+    def __init__(self, query_factors, key_factors, *, scale: float = 1.0):
+        qf, kf = torch.as_tensor(query_factors), torch.as_tensor(key_factors)
+        if qf.ndim == 2:
+            qf = qf[None]
+        if kf.ndim == 2:
+            kf = kf[None]
+        if qf.ndim != 3 or kf.ndim != 3:
+            raise ValueError("factors must have shape [H|1, length, rank]")
+        if qf.shape[-1] != kf.shape[-1]:
+            raise ValueError("query and key factors must have the same rank")
+        if qf.shape[0] != kf.shape[0]:
+            raise ValueError("query and key factors must have the same head count")
+        if scale < 0:
+            raise ValueError("scale must be non-negative")
+        self.query_factors, self.key_factors, self.scale = qf, kf, float(scale)
+
+    @property
+    def rank(self) -> int:
+        return self.query_factors.shape[-1]
+
+    def factors(self, q_len: int, kv_len: int, num_heads: int, *, dtype=None):
+        """Factors in attention layout ``[1, length, heads, rank]`` (:1962-1995)."""
+        if q_len > self.query_factors.shape[1]:
+            raise ValueError(f"q_len={q_len} exceeds maximum {self.query_factors.shape[1]}")
+        if kv_len > self.key_factors.shape[1]:
+            raise ValueError(f"kv_len={kv_len} exceeds maximum {self.key_factors.shape[1]}")
+        fh = self.query_factors.shape[0]
+        if fh not in (1, num_heads):
+            raise ValueError(f"factor head count {fh} cannot broadcast to {num_heads}")
+        qf = self.query_factors[:, :q_len].expand(num_heads, q_len, self.rank)
+        kf = self.key_factors[:, :kv_len].expand(num_heads, kv_len, self.rank)
+        qf, kf = qf.transpose(0, 1)[None], kf.transpose(0, 1)[None]
+        if dtype is not None:
+            qf, kf = qf.to(dtype), kf.to(dtype)
+        return qf, kf
+
+
+class BatchedLowRankBias(AttentionBias):
+    """Per-example ``scale * U[b, q] . V[b, k]`` with factors ``[B, length,
+    rank]`` (a query length of 1 broadcasts; attention_mask_bias.py:2028-2190)."""
+
+    def __init__(self, query_factors, key_factors, *, scale: float = 1.0):
+        qf, kf = torch.as_tensor(query_factors), torch.as_tensor(key_factors)
+        if qf.ndim != 3 or kf.ndim != 3:
+            raise ValueError("factors must have shape [B, length, rank]")
+        if qf.shape[-1] != kf.shape[-1]:
+            raise ValueError("query and key factors must have the same rank")
+        if qf.shape[0] != kf.shape[0]:
+            raise ValueError("query and key factors must have the same batch size")
+        if scale < 0:
+            raise ValueError("scale must be non-negative")
+        self.query_factors, self.key_factors, self.scale = qf, kf, float(scale)
+
+    @classmethod
+    def from_key_bias(cls, key_bias, q_len: int = 1):
+        """Rank-1 bias adding ``key_bias[b, k]`` to every score of key ``k`` (:2069-2083)."""
+        kb = torch.as_tensor(key_bias)
+        if kb.ndim != 2:
+            raise ValueError("key_bias must have shape [B, kv_len]")
+        ones = torch.ones((kb.shape[0], q_len, 1), dtype=kb.dtype, device=kb.device)
+        return cls(ones, kb[..., None])
+
+    @property
+    def rank(self) -> int:
+        return self.query_factors.shape[-1]
+
+    def factors(self, q_len: int, kv_len: int, num_heads: int, *, dtype=None):
+        """Factors in attention layout ``[B, length, heads, rank]`` (:2089-2124)."""
+        b = self.query_factors.shape[0]
+        if self.query_factors.shape[1] == 1:
+            qf = self.query_factors[:, :, None, :]
+        elif q_len <= self.query_factors.shape[1]:
+            qf = self.query_factors[:, :q_len, None, :]
+        else:
+            raise ValueError(f"q_len={q_len} exceeds maximum {self.query_factors.shape[1]}")
+        if kv_len > self.key_factors.shape[1]:
+            raise ValueError(f"kv_len={kv_len} exceeds maximum {self.key_factors.shape[1]}")
+        kf = self.key_factors[:, :kv_len, None, :]
+        qf = qf.expand(b, q_len, num_heads, self.rank)
+        kf = kf.expand(b, kv_len, num_heads, self.rank)
+        if dtype is not None:
+            qf, kf = qf.to(dtype), kf.to(dtype)
+        return qf, kf
+
+
+class LearnedAlibiBias(AttentionBias):
+    """``-slopes[h] * ((q + query_offset) - (k + key_offset))`` as a rank-2
+    factorisation, so gradients reach ``slopes`` (attention_mask_bias.py:
+    2258-2352)."""
+
+    def __init__(self, slopes, *, query_offset: int = 0, key_offset: int = 0):
+        sl = torch.as_tensor(slopes)
+        if sl.ndim == 0:
+            sl = sl[None]
+        if sl.ndim != 1:
+            raise ValueError("slopes must have shape [H|1]")
+        self.slopes, self.query_offset, self.key_offset = sl, int(query_offset), int(key_offset)
+
+    rank = 2
+    scale = 1.0
+
+    def factors(self, q_len: int, kv_len: int, num_heads: int, *, dtype=None):
+        """``U = [-s * q_pos, 1]``, ``V = [1, s * k_pos]`` in layout
+        ``[1, length, heads, 2]`` (:2291-2318)."""
+        if self.slopes.shape[0] not in (1, num_heads):
+            raise ValueError(f"slope head count {self.slopes.shape[0]} cannot broadcast to {num_heads}")
+        sl = self.slopes.expand(num_heads)
+        qp = torch.arange(q_len, dtype=sl.dtype, device=sl.device) + self.query_offset
+        kp = torch.arange(kv_len, dtype=sl.dtype, device=sl.device) + self.key_offset
+        qf = torch.stack((-sl[:, None] * qp[None], torch.ones(num_heads, q_len, dtype=sl.dtype, device=sl.device)), -1)
+        kf = torch.stack((torch.ones(num_heads, kv_len, dtype=sl.dtype, device=sl.device), sl[:, None] * kp[None]), -1)
+        qf, kf = qf.transpose(0, 1)[None], kf.transpose(0, 1)[None]
+        if dtype is not None:
+            qf, kf = qf.to(dtype), kf.to(dtype)
+        return qf, kf
+
+
+_LOW_RANK = ("LowRankBias", "BatchedLowRankBias", "LearnedAlibiBias")
+
+
+def split_low_rank_bias(bias):
+    """``(low-rank terms, remaining bias)`` (probjax ``_split_low_rank_bias``,
+    layers/attention.py:1322-1345): the terms ``flex_attention`` folds into
+    Q/K, out of a bias or a ``SumBias`` tree."""
+    if bias is None:
+        return [], None
+    name = _name(bias)
+    if name in _LOW_RANK:
+        return [bias], None
+    if name == "SumBias":
+        lt, lhs = split_low_rank_bias(bias.lhs)
+        rt, rhs = split_low_rank_bias(bias.rhs)
+        rest = rhs if lhs is None else lhs if rhs is None else SumBias(lhs, rhs)
+        return lt + rt, rest
+    return [], bias
 
 
 def _name(obj) -> str:

@@ -265,3 +265,43 @@ def test_mla_absorb_rule():
     assert A._absorbed_cheaper(1, 4096, 512, 128, 128)
     assert not A._absorbed_cheaper(4096, 4096, 512, 128, 128)
     assert A._absorbed_cheaper(4096, 4096, 64, 128, 128)  # narrow latent
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_low_rank_fold_matches_oracle(dtype):
+    """The mirror's factor layouts and folding (torch, no kernels) against the
+    oracle's restatement of flex_attention:1600-1635."""
+    import numpy as np
+
+    import oracle
+    from oracle.lowrank import fold_low_rank
+
+    rng = np.random.default_rng(0)
+    B, L, Hq, Hkv, D = 2, 12, 4, 2, 16
+    q, k, v = (rng.standard_normal(s).astype(np.float32) for s in ((B, L, Hq, D), (B, L, Hkv, D), (B, L, Hkv, D)))
+    qf, kf = (rng.standard_normal((Hq, 14, 3)).astype(np.float32) for _ in range(2))
+    kb = rng.standard_normal((B, L)).astype(np.float32)
+    slopes = np.array([0.5, 0.25, 0.125, 0.0625], np.float32)
+    mine = [M.LowRankBias(torch.from_numpy(qf), torch.from_numpy(kf), scale=0.5),
+            M.BatchedLowRankBias.from_key_bias(torch.from_numpy(kb)),
+            M.LearnedAlibiBias(torch.from_numpy(slopes), key_offset=2)]
+    theirs = [oracle.LowRankBias(qf, kf, scale=0.5), oracle.BatchedLowRankBias.from_key_bias(kb),
+              oracle.LearnedAlibiBias(slopes, key_offset=2)]
+    terms, rest = M.split_low_rank_bias(mine[0] + M.CausalAlibiBias() + mine[1] + mine[2])
+    assert [type(t).__name__ for t in terms] == ["LowRankBias", "BatchedLowRankBias", "LearnedAlibiBias"]
+    assert type(rest).__name__ == "CausalAlibiBias"
+    tq, tk, tv = (torch.from_numpy(x).to(dtype) for x in (q, k, v))
+    q2, k2, v2, out_dim = A._fold_low_rank(tq, tk, tv, terms, 0.25)
+    assert out_dim == D and q2.shape[-1] == 64 and k2.shape == (B, L, Hq, 64)
+    dt = "bf16" if dtype == torch.bfloat16 else "f32"
+    wq, wk, wv = fold_low_rank(q, k, v, theirs, 0.25, dt)
+    n = wq.shape[-1]
+    for got, want in ((q2, wq), (k2, wk), (v2, wv)):
+        np.testing.assert_allclose(got[..., :n].float().numpy(), want, rtol=0, atol=1e-6)
+        assert not got[..., n:].float().any()
+    with pytest.raises(ValueError, match="positive sm_scale"):
+        A._fold_low_rank(tq, tk, tv, terms, 0.0)
+    assert A._fold_low_rank(torch.zeros(1, 4, 4, 128), torch.zeros(1, 4, 4, 128), torch.zeros(1, 4, 4, 128),
+                            terms[:1], 0.1) is None
+    with pytest.raises(ValueError, match="same rank"):
+        M.LowRankBias(torch.zeros(2, 4, 3), torch.zeros(2, 4, 2))
