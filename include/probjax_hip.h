@@ -140,8 +140,12 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  *
  * with s the forward's score (sm_scale * q.k + bias, masked keys excluded)
  * and fp32 accumulation; dk/dv sum the query heads of each KV head's group.
- * The dense bias gets no gradient (the reference's custom VJP returns zeros
- * for it, attention.py:3262-3263).
+ * dbias: NULL, or fp32 [B, Hq, Lq, Lk] that receives dL/d(bias) per query
+ * head, P (dP - delta) for every score (the gradient the reference's dense
+ * path gives a bias tensor, layers/attention.py:1293-1319; its kernel path's
+ * custom VJP returns zeros instead, attention.py:3262-3263).  Needs bias; the
+ * caller zero-fills it (fully masked tiles are not written) and sums it over
+ * the dimensions the bias broadcasts.
  *
  * Arguments as pjx_flash_fwd, plus: o the forward output, dout [B, Lq, Hq, D]
  * the output gradient, lse the forward's natural-log LSE [B, Hq, Lq] (+inf
@@ -154,7 +158,7 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  */
 int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                  void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
+                  float* dbias, void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
                   const float* bias, int64_t bias_batch, int64_t bias_heads, int64_t batch,
                   int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                   int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,

@@ -20,7 +20,10 @@ Follows ``probjax/nn/pallas_kernels/kernels/attention.py``:
   - GQA: per-query-head ``dk``/``dv`` in the input dtype, summed over each KV
     head's group in fp32 and cast (``_sum_gqa_group`` ``:2123-2128``);
   - the dense bias gets no cotangent (the custom VJP returns zeros for the
-    bias leaves, ``:3262-3263``);
+    bias leaves, ``:3262-3263``); ``return_dbias`` gives the gradient the
+    reference's dense ``dot_product_attention`` path gives a bias tensor
+    (``layers/attention.py:1293-1319``, autodiff of ``scores + bias``):
+    ``p * (dp - delta)`` per score, the dS before the scale;
   - score modifiers (soft capping, per-head scale) multiply ``ds`` by their
     derivative at the pre-bias score (``:1051-1056``; ``grad_tile``).
 
@@ -68,8 +71,10 @@ def attention_backward(
     sm_scale: float = 1.0,
     dtype: str = "f32",
     compute_dtype=np.float32,
+    return_dbias: bool = False,
 ):
-    """Gradients ``(dq, dk, dv)`` of the attention forward.
+    """Gradients ``(dq, dk, dv)`` of the attention forward (and ``dbias``
+    ``[B, Hq, Lq, Lk]`` per query head with ``return_dbias``).
 
     ``q/o/do [B, Lq, Hq, D]``, ``k/v [B, Lk, Hkv, D]``, ``lse [B, Hq, Lq]``
     natural log (``+inf`` for rows without a valid key).  ``mask`` is an
@@ -91,6 +96,7 @@ def attention_backward(
     span_k = np.arange(Lk, dtype=np.int32)
 
     dq = np.zeros((B, Lq, Hq, D), cdt)
+    dbias = np.zeros((B, Hq, Lq, Lk), cdt) if return_dbias else None
     dk_h = np.zeros((B, Lk, Hq, D), cdt)
     dv_h = np.zeros((B, Lk, Hq, v.shape[-1]), cdt)
     for b in range(B):
@@ -110,6 +116,8 @@ def attention_backward(
             p = np.exp(s - lse[b, h][:, None])
             dp = dob @ vb.T
             ds = p * (dp - delta[b, h][:, None])
+            if dbias is not None:
+                dbias[b, h] = ds  # d(scores + bias)/d(bias) = 1
             if sm_scale != 1.0:
                 ds = ds * cdt(sm_scale)
             if gf is not None:
@@ -127,4 +135,6 @@ def attention_backward(
     dk_h, dv_h = finish(dk_h), finish(dv_h)
     dk = np.sum(dk_h.reshape(B, Lk, Hkv, G, D).astype(cdt), axis=3)
     dv = np.sum(dv_h.reshape(B, Lk, Hkv, G, dv_h.shape[-1]).astype(cdt), axis=3)
+    if dbias is not None:
+        return finish(dq), finish(dk), finish(dv), dbias
     return finish(dq), finish(dk), finish(dv)

@@ -285,29 +285,37 @@ class _AttentionFunction(torch.autograd.Function):
     """Differentiable HIP attention, the custom VJP of probjax's ``mha``
     (kernels/attention.py:3188-3266): the forward keeps ``(q, k, v, out,
     lse)`` as residuals and the backward is ``pjx_flash_bwd``.  Mask and bias
-    data get no cotangent, as in the reference (:3262-3263): the bias tensor
-    is an argument of the kernels, not an input of this function."""
+    data get no cotangent, as in the reference (:3262-3263), unless the dense
+    bias tensor is passed as ``bias``: then it is an input and receives
+    dL/d(bias) (the gradient probjax's dense ``dot_product_attention`` path,
+    layers/attention.py:1293-1319, gives it)."""
 
     @staticmethod
-    def forward(ctx, query, key, value, run_fwd, bwd_kwargs):
+    def forward(ctx, query, key, value, bias, run_fwd, bwd_kwargs):
         out, lse = run_fwd(query, key, value)
         ctx.save_for_backward(query, key, value, out, lse)
         ctx.bwd_kwargs = bwd_kwargs
+        ctx.bias_dtype = None if bias is None else bias.dtype
         return out
 
     @staticmethod
     def backward(ctx, dout):
         q, k, v, o, lse = ctx.saved_tensors
+        if ctx.bias_dtype is not None and ctx.needs_input_grad[3]:
+            dq, dk, dv, db = hip.flash_attention_bwd(q, k, v, o, dout, lse, bias_grad=True, **ctx.bwd_kwargs)
+            return dq, dk, dv, db.to(ctx.bias_dtype), None, None
         dq, dk, dv = hip.flash_attention_bwd(q, k, v, o, dout, lse, **ctx.bwd_kwargs)
-        return dq, dk, dv, None, None
+        return dq, dk, dv, None, None, None
 
 
 def _needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
-def _run(query, key, value, lm, lb, sm_scale, split_kv):
-    grad = _needs_grad(query, key, value)
+def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False):
+    dense = None if lb is None else lb.dense
+    bias_in = dense if bias_grad and dense is not None and _needs_grad(dense) else None
+    grad = _needs_grad(query, key, value) or bias_in is not None
     if grad and query.dtype not in BACKWARD_DTYPES:
         return None
     if _splitkv_ok(query, key, lm, lb is not None, 0.0, split_kv):
@@ -318,7 +326,7 @@ def _run(query, key, value, lm, lb, sm_scale, split_kv):
             # Split-KV primal, regular backward (probjax splitkv_attention,
             # kernels/attention_splitkv.py:253-272).
             return _AttentionFunction.apply(
-                query, key, value,
+                query, key, value, None,
                 lambda q, k, v: hip.splitkv_decode(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
                 dict(sm_scale=sm_scale, kv_lengths=plan["kv_lengths"]),
             )
@@ -328,7 +336,7 @@ def _run(query, key, value, lm, lb, sm_scale, split_kv):
     if not grad:
         return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, **plan)
     return _AttentionFunction.apply(
-        query, key, value,
+        query, key, value, bias_in,
         lambda q, k, v: hip.flash_attention_fwd(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
         dict(sm_scale=sm_scale, **plan),
     )
@@ -637,7 +645,7 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
                    deterministic=True, dtype=None, precision=None, module=None,
                    sm_scale: float | None = None, enable_gqa: bool = False,
                    split_kv: bool | None = None, implementation: str | None = None,
-                   **unused_tuning):
+                   _bias_grad: bool = False, **unused_tuning):
     """Fused softmax attention with mask/bias objects (probjax
     ``flex_attention``, layers/attention.py:1426-1759).
 
@@ -692,7 +700,7 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
         bias = rest
     e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=active_dropout)
     if e is not None and (implementation == "hip" or device_table_enabled()):
-        out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv)
+        out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv, bias_grad=_bias_grad)
     if out is None:
         raise ValueError(
             f"implementation={implementation!r}: "
@@ -751,7 +759,10 @@ def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=N
     """Softmax attention with Flax ``dot_product_attention`` semantics (probjax
     layers/attention.py:1205-1319) on the HIP kernels: leading batch dims are
     flattened, K/V may have fewer heads (GQA), ``sm_scale`` defaults to
-    ``1/sqrt(D)``.  ``implementation`` in ``(None, "hip")``.
+    ``1/sqrt(D)``.  ``implementation`` in ``(None, "hip")``.  A ``DenseBias``
+    whose tensor requires grad receives its gradient, as in probjax's dense
+    path (``flex_attention`` / ``mha`` give bias data no cotangent, as the
+    reference's kernel VJP does).
     """
     if implementation not in (None, "hip"):
         raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
@@ -765,5 +776,5 @@ def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=N
     out = flex_attention(*flat, mask=mask, bias=bias, dropout_rng=dropout_rng,
                          dropout_rate=dropout_rate, deterministic=deterministic, dtype=dtype,
                          sm_scale=sm_scale, enable_gqa=enable_gqa or query.shape[-2] != key.shape[-2],
-                         implementation=implementation)
+                         implementation=implementation, _bias_grad=True)
     return out.reshape(tuple(batch_shape) + tuple(out.shape[-3:]))

@@ -44,6 +44,7 @@ struct FlashBwdArgs {
   void* dq;
   void* dk;
   void* dv;
+  float* dbias;       // [B, Hq, Lq, Lk] fp32 dL/d(bias): P (dP - delta) per score, or null
 };
 
 constexpr int kBKV = 128;  // keys per dK/dV workgroup (32 per wave)
@@ -111,11 +112,40 @@ __device__ __forceinline__ bf16x8 pack_step(const f32x16& x, int c) {
 __device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
 __device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
+// dL/d(bias) of one key tile in the S^T layout (lane = query g.qi, register
+// r of block kb = key k0 + kb*32 + 8*(r/4) + 4*half + r%4): 4 consecutive
+// keys per register group go out as one 16-byte store.  Tiles the kernel
+// skips (fully masked) are left as the caller's zeros.
+template <int NKB>
+__device__ __forceinline__ void store_dbias(const FlashBwdArgs& ba, const BlockGeom& g,
+                                            const f32x16* dbv, int k0, int half, bool row_in) {
+  const FlashArgs& a = ba.f;
+  if (!row_in) return;
+  float* row = ba.dbias + (((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi) * a.Lk;
+  const bool vec = (a.Lk & 3) == 0;
+#pragma unroll
+  for (int kb = 0; kb < NKB; ++kb)
+#pragma unroll
+    for (int gq = 0; gq < 4; ++gq) {
+      const int kk = k0 + kb * 32 + 8 * gq + 4 * half;
+      if (vec && kk + 3 < a.Lk) {
+        *(f32x4*)(row + kk) = f32x4{dbv[kb][4 * gq], dbv[kb][4 * gq + 1], dbv[kb][4 * gq + 2], dbv[kb][4 * gq + 3]};
+      } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+          if (kk + j < a.Lk) row[kk + j] = dbv[kb][4 * gq + j];
+      }
+    }
+}
+
+// ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
 // dQ (and delta): one workgroup per (128-query tile, batch, head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, int EXT>
+template <int D, int BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
+  // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
+  constexpr bool HB = BIAS != 0, DB = BIAS == 2;
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
   constexpr int BK = T::ROWS, ROWB = T::ROWB, TILE_B = T::TILE_B;
@@ -169,12 +199,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
     }
   }
   const float* brow = nullptr;
-  if constexpr (BIAS) {
+  if constexpr (HB) {
     brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
+  const float cx = (HB || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
   if constexpr (EXT > 0) er = ext_rows(a, g);
 
@@ -236,15 +266,18 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         dp[kb] = mfma32x32x16(vf, dof[st], dp[kb]);
       }
     }
+    f32x16 dbv[DB ? BK / 32 : 1];  // dL/d(bias) = P (dP - delta), kept for the store
     if constexpr (EXT == 2) {
       // modified scores, masks, P and dS = P (dP - delta) * scale * f'(s)
-      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
-                                   [&](int kb, int r, float x, float gg) {
-                                     const float p = fast_exp2(fmaf(x, cx, -lse2));
-                                     s[kb][r] = p * (dp[kb][r] - delta) * a.scale * gg;
-                                   });
+      ext_scores_sT<BK / 32, HB>(a, g, er, s, k0, half, brow, row_in,
+                                 [&](int kb, int r, float x, float gg) {
+                                   const float p = fast_exp2(fmaf(x, cx, -lse2));
+                                   const float t = p * (dp[kb][r] - delta);
+                                   if constexpr (DB) dbv[kb][r] = t;
+                                   s[kb][r] = t * a.scale * gg;
+                                 });
     } else {
-    if constexpr (BIAS) {
+    if constexpr (HB) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
@@ -276,9 +309,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
-        s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
+        const float t = p * (dp[kb][r] - delta);
+        if constexpr (DB) dbv[kb][r] = t;
+        s[kb][r] = t * a.scale;
       }
     }
+    if constexpr (DB) store_dbias<BK / 32>(ba, g, dbv, k0, half, row_in);
     bf16x8 dsf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) dsf[c] = pack_step(s[c >> 1], c & 1);
@@ -590,8 +626,9 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
 // tile.  Tiles are staged through registers into LDS rows padded to D + 4
 // floats (16-byte reads of 16 consecutive rows hit distinct banks).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, int EXT>
+template <int D, int BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdArgs ba) {
+  constexpr bool HB = BIAS != 0, DB = BIAS == 2;  // as in flash_bwd_dq_kernel
   const FlashArgs& a = ba.f;
   constexpr int BK = (D == 128) ? 32 : 64;
   constexpr int KS = D + 4;
@@ -645,12 +682,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     }
   }
   const float* brow = nullptr;
-  if constexpr (BIAS) {
+  if constexpr (HB) {
     brow = a.bias + (size_t)g.b * a.bias_bstride + (size_t)g.h * a.bias_hstride +
            (size_t)(row_in ? g.qi : 0) * a.Lk;
   }
   const bool bias_vec = (a.Lk & 3) == 0;
-  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
+  const float cx = (HB || EXT == 2) ? kLog2e : a.scale * kLog2e;
   ExtRows er;
   if constexpr (EXT > 0) er = ext_rows(a, g);
 
@@ -713,14 +750,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
         }
       }
     }
+    f32x16 dbv[DB ? BK / 32 : 1];
     if constexpr (EXT == 2) {
-      ext_scores_sT<BK / 32, BIAS>(a, g, er, s, k0, half, brow, row_in,
-                                   [&](int kb, int r, float x, float gg) {
-                                     const float p = fast_exp2(fmaf(x, cx, -lse2));
-                                     s[kb][r] = p * (dp[kb][r] - delta) * a.scale * gg;
-                                   });
+      ext_scores_sT<BK / 32, HB>(a, g, er, s, k0, half, brow, row_in,
+                                 [&](int kb, int r, float x, float gg) {
+                                   const float p = fast_exp2(fmaf(x, cx, -lse2));
+                                   const float t = p * (dp[kb][r] - delta);
+                                   if constexpr (DB) dbv[kb][r] = t;
+                                   s[kb][r] = t * a.scale * gg;
+                                 });
     } else {
-    if constexpr (BIAS) {
+    if constexpr (HB) {
 #pragma unroll
       for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
@@ -750,9 +790,12 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
-        s[kb][r] = p * (dp[kb][r] - delta) * a.scale;
+        const float t = p * (dp[kb][r] - delta);
+        if constexpr (DB) dbv[kb][r] = t;
+        s[kb][r] = t * a.scale;
       }
     }
+    if constexpr (DB) store_dbias<BK / 32>(ba, g, dbv, k0, half, row_in);
     // dQ^T[d][query] += K^T dS^T: step (kb, r) contracts keys (r, half 0/1).
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
@@ -1039,10 +1082,15 @@ template <int D, int EXT>
 static int run_bwd_t(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
     int rc;
+    const bool db = a.dbias != nullptr;
     if (f32)
-      rc = hb ? launch_dq(flash_bwd_dq_f32_kernel<D, true, EXT>, a, s) : launch_dq(flash_bwd_dq_f32_kernel<D, false, EXT>, a, s);
+      rc = db ? launch_dq(flash_bwd_dq_f32_kernel<D, 2, EXT>, a, s)
+         : hb ? launch_dq(flash_bwd_dq_f32_kernel<D, 1, EXT>, a, s)
+              : launch_dq(flash_bwd_dq_f32_kernel<D, 0, EXT>, a, s);
     else
-      rc = hb ? launch_dq(flash_bwd_dq_kernel<D, true, EXT>, a, s) : launch_dq(flash_bwd_dq_kernel<D, false, EXT>, a, s);
+      rc = db ? launch_dq(flash_bwd_dq_kernel<D, 2, EXT>, a, s)
+         : hb ? launch_dq(flash_bwd_dq_kernel<D, 1, EXT>, a, s)
+              : launch_dq(flash_bwd_dq_kernel<D, 0, EXT>, a, s);
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
@@ -1070,7 +1118,7 @@ extern "C" size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, i
 
 extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, void* dq, void* dk, void* dv,
-                             void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
+                             float* dbias, void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
                              const float* bias, int64_t bias_batch, int64_t bias_heads,
                              int64_t batch, int64_t q_len, int64_t kv_len, int64_t q_heads,
                              int64_t kv_heads, int64_t head_dim, int64_t q_valid, int64_t kv_valid,
@@ -1089,6 +1137,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sm_scale must be > 0");
   if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
+  if (dbias && !bias) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dbias needs the bias");
   const int64_t elems = std::max(batch * q_len * q_heads, batch * kv_len * kv_heads) * head_dim;
   if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30) ||
       (int64_t)q_heads * head_dim * 4 * 64 > 0xffffffffLL)
@@ -1121,6 +1170,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.delta = (float*)workspace;
   ba.lse2 = ba.delta + batch * q_heads * q_len;
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
+  ba.dbias = dbias;
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
   const bool f32 = dtype == PJX_DTYPE_F32;

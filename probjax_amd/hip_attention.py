@@ -163,9 +163,11 @@ def flash_attention_fwd(
 def flash_attention_bwd(
     q, k, v, o, do, lse, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
     q_valid: int | None = None, kv_valid: int | None = None, workspace=None,
-    mods: ScoreModsArgs | None = None,
+    mods: ScoreModsArgs | None = None, bias_grad: bool = False,
 ):
-    """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``.
+    """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``
+    (and, with ``bias_grad``, ``dbias``: dL/d(bias) summed to the bias's own
+    ``[1|B, 1|H, Lq, Lk]`` shape, fp32).
 
     ``o`` and ``lse`` are the forward's output and natural-log LSE; ``do`` the
     output gradient.  Masks, bias and scale must be the forward's.  bf16 or fp32.
@@ -200,17 +202,25 @@ def flash_attention_bwd(
         bias = bias.to(torch.float32).contiguous()
     L = _lengths(kv_lengths, B, dev)
     ms = _mods_struct(mods, B, Lq, Lk, Hq, dev)
+    if bias_grad and bias is None:
+        raise ValueError("bias_grad needs the bias")
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    dbias = torch.zeros((B, Hq, Lq, Lk), dtype=torch.float32, device=dev) if bias_grad else None
     lib = native.load()
     ws = _workspace(int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq)), dev, workspace)
     rc = lib.pjx_flash_bwd(
         code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
-        _ptr(dk), _ptr(dv), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
+        _ptr(dk), _ptr(dv), _ptr(dbias), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
         Lq if q_valid is None else int(q_valid), Lk if kv_valid is None else int(kv_valid),
         int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
     )
     native.check(rc)
-    return dq, dk, dv
+    if dbias is None:
+        return dq, dk, dv
+    dims = [d for d, n in ((0, bb), (1, bh)) if n == 1]
+    if dims:
+        dbias = dbias.sum(dim=dims, keepdim=True)
+    return dq, dk, dv, dbias
 
 
 def decode_workspace_bytes(batch, groups, rows, kv_len, v_dim, chunk=0) -> int:

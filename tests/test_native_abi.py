@@ -89,7 +89,7 @@ def test_flash_rejects_invalid_score_mods(lib, fields, msg):
 
 def _bwd_args(**over):
     a = dict(dtype=native.PJX_DTYPE_BF16, q=1, k=1, v=1, o=1, do=1, lse=1, dq=1, dk=1, dv=1,
-             ws=1, ws_bytes=1 << 20, kvl=None, bias=None, bb=1, bh=1, B=1, Lq=16, Lk=16, Hq=2,
+             dbias=None, ws=1, ws_bytes=1 << 20, kvl=None, bias=None, bb=1, bh=1, B=1, Lq=16, Lk=16, Hq=2,
              Hkv=1, D=128, qv=16, kv=16, causal=1, scale=0.1, mods=None, stream=None)
     a.update(over)
     return list(a.values())
@@ -100,6 +100,7 @@ def _bwd_args(**over):
     [
         (dict(dtype=7), "dtype", 1),
         (dict(do=None), "non-null", 1),
+        (dict(dbias=1), "dbias needs the bias", 1),
         (dict(D=96), "head_dim", 1),
         (dict(Hq=3, Hkv=2), "multiple of kv_heads", 1),
         (dict(ws=None), "workspace", 3),

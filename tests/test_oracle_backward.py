@@ -32,8 +32,10 @@ def _torch_grads(q, k, v, do, *, scale, keep=None, bias=None):
     kr = tk.repeat_interleave(G, dim=2)
     vr = tv.repeat_interleave(G, dim=2)
     s = torch.einsum("bqhd,bkhd->bhqk", tq, kr) * scale
+    tb = None
     if bias is not None:
-        s = s + torch.from_numpy(np.asarray(bias, np.float64))
+        tb = t(bias)
+        s = s + tb
     if keep is not None:
         kt = torch.from_numpy(np.asarray(keep))[:, None]  # [B, 1, Q, K]
         s = s.masked_fill(~kt, -math.inf)
@@ -44,6 +46,7 @@ def _torch_grads(q, k, v, do, *, scale, keep=None, bias=None):
         p = torch.softmax(s, dim=-1)
     o = torch.einsum("bhqk,bkhd->bqhd", p, vr)
     o.backward(torch.from_numpy(np.asarray(do, np.float64)))
+    _torch_grads.dbias = None if tb is None else tb.grad.numpy()
     return o.detach().numpy(), tq.grad.numpy(), tk.grad.numpy(), tv.grad.numpy()
 
 
@@ -81,9 +84,13 @@ def test_backward_matches_torch_autograd_float64(B, Lq, Lk, Hq, Hkv, D, causal, 
                          for b in range(B)])
     o, lse = _forward(q, k, v, mask=mask, bias=db, scale=scale)
     got = attention_backward(q, k, v, o, do, lse, mask=mask, bias=db, sm_scale=scale,
-                             compute_dtype=np.float64)
+                             compute_dtype=np.float64, return_dbias=has_bias)
     o_t, *want = _torch_grads(q, k, v, do, scale=scale, keep=keep,
                               bias=bias if has_bias else None)
+    if has_bias:
+        # dL/d(bias): per query head, summed over the batch the bias [1, H] broadcasts
+        want.append(_torch_grads.dbias)
+        got = (*got[:3], got[3].sum(axis=0, keepdims=True))
     np.testing.assert_allclose(o, o_t, atol=1e-6)  # the forward it differentiates (fp32 out)
     for g, w in zip(got, want):
         np.testing.assert_allclose(g, w, atol=2e-5, rtol=1e-5)
