@@ -132,7 +132,7 @@ def make_c2(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="C2 causal fwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_kernel<128,false,0>")
+                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<128,32,3>")
 
 
 def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
@@ -227,7 +227,7 @@ def make_c2b(dev, gen):
                                      workspace=ws)
     return dict(name="C2 causal bwd bf16 B=4 H=16 L=4096 D=128 (dq, dk, dv)", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_bwd_dq_kernel<128,false,0> + flash_bwd_dkdv_kernel<128,false,0>")
+                kernel="flash_bwd_dq_kernel<128,0,0> + flash_bwd_dkdv_kernel<128,false,0>")
 
 
 def make_c2fb(dev, gen):
@@ -248,7 +248,7 @@ def make_c2fb(dev, gen):
     nbytes = 2 * B * L * H * D * 2 * 5 + B * H * L * 4
     return dict(name="C2 causal fwd+bwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_fwd_bf16_kernel<128,false,0> + flash_bwd_*<128,false,0>")
+                kernel="flash_fwd_bf16_pipe_kernel<128,32,3> + flash_bwd_dq_kernel<128,0,0> + flash_bwd_dkdv_kernel<128,false,0>")
 
 
 def _mla_prefill_inputs(dev, gen):
@@ -291,7 +291,7 @@ def make_c5m(dev, gen):
     nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
     return dict(name="MLA materialised causal prefill bf16 B=1 L=4096 R=512 H=16 dk=dv=128", fn=fn,
                 flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="mla_project_bf16_kernel + flash_fwd_bf16_kernel<128,false,0>")
+                kernel="mla_project_bf16_kernel + flash_fwd_bf16_pipe_kernel<128,32,3>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
@@ -460,7 +460,7 @@ def main():
                        "head_dim": 128, "mask": "causal", "flop_per_step": w["flop"]},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(frac, 4),
-                         "traffic": measured_traffic("pjx::flash_fwd_bf16_kernel<128, false, 0>"),
+                         "traffic": measured_traffic("pjx::flash_fwd_bf16_pipe_kernel<128, 32, 3>"),
                          "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
                          "kernel": w["kernel"]},
         })

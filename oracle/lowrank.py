@@ -138,8 +138,9 @@ def flex_low_rank_backward(q, k, v, do, *, mask=None, bias=None, sm_scale=1.0, d
                                        dtype=dtype, compute_dtype=compute_dtype)
     dq2, dk2, dv2 = (np.asarray(x, cdt) for x in (dq2, dk2, dv2))
     G = Hq // Hkv
-    dk = dk2[..., :D].reshape(B, Lk, Hkv, G, D).sum(axis=3)
-    dv = dv2[..., :Dv].reshape(B, Lk, Hkv, G, Dv).sum(axis=3)
+    # the repeat's VJP sums each group's per-head gradients in the input dtype
+    dk = _cast(dk2[..., :D].reshape(B, Lk, Hkv, G, D).sum(axis=3), dtype).astype(cdt)
+    dv = _cast(dv2[..., :Dv].reshape(B, Lk, Hkv, G, Dv).sum(axis=3), dtype).astype(cdt)
     grads, feats, off = [], [], D
     for t in terms:
         f = cdt(math.sqrt(t.scale / sm_scale))

@@ -134,9 +134,9 @@ __device__ __forceinline__ f32x4 load_bias4(const float* row, int kk, int Lk) {
 // bytes, 16-byte chunks XOR-swizzled per row (K: chunk ^ (row & (NC-1)); V:
 // chunk ^ f(row) chosen so a transposing read of 4 rows x 32 bytes per 16
 // lanes hits distinct banks).
-template <int D>
+template <int D, int BK_ = 64>
 struct Bf16Tile {
-  static constexpr int BK = 64;             // keys per tile
+  static constexpr int BK = BK_;            // keys per tile
   static constexpr int ROWB = D * 2;        // bytes per K/V row
   static constexpr int NC = D / 8;          // 16-byte chunks per row
   static constexpr int TILE_B = BK * ROWB;  // bytes of one K (or V) tile

@@ -298,6 +298,214 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 }
 
 // ---------------------------------------------------------------------------
+// bf16 without bias or extended masks (the headline case): the same
+// decomposition with the key loop software-pipelined inside each wave.
+// Iteration t issues S_{t+1} = K_{t+1} Q^T on the MFMA pipe in the same
+// basic block as tile t's exponentials, row sums and packing, so a wave's own
+// VALU work runs while its MFMAs execute; then O += P_t V_t.
+//
+// The 2-stage ring keeps K one tile ahead of V: after the barrier that opens
+// iteration t, K_{t+2} goes into the K slot of stage t%2 (K_t was consumed by
+// iteration t-1, which formed S_t) and V_{t+1} into the V slot of stage
+// (t+1)%2 (V_{t-1} was consumed by iteration t-1).  Iteration t reads K_{t+1}
+// and V_t, both loaded during iteration t-1.  S_{t+1} is formed even where
+// this wave will not use it (past its causal diagonal, past the last tile):
+// it reads whatever the slot holds and is discarded, so the block stays
+// branch-free.
+// ---------------------------------------------------------------------------
+template <int D, int BKT, int WPC>
+__global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(FlashArgs a) {
+  using T = Bf16Tile<D, BKT>;
+  constexpr int RPW = BKT / 4;  // tile rows each wave loads
+  static_assert(BKT % 32 == 0 && RPW % T::RPI == 0 && T::NLD >= 1, "tile rows per wave");
+  constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+
+  BlockGeom g = block_geom(a);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  g.qw = __builtin_amdgcn_readfirstlane(g.qw);
+  const int col = lane & 31, half = lane >> 5;
+  const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
+  const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
+  const unsigned char* Vb = (const unsigned char*)a.v + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
+  const bool row_in = g.qi < a.Lq;
+  const bool row_ok = g.qi < g.q_hi;
+
+  bf16x8 qf[D / 16];
+  {
+    const uint16_t* qrow =
+        (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int s = 0; s < D / 16; ++s) {
+      u32x4 raw = {0u, 0u, 0u, 0u};
+      if (row_in) raw = *(const u32x4*)(qrow + 16 * s + 8 * half);
+      qf[s] = as_bf16x8(raw);
+    }
+  }
+  const float cx = a.scale * kLog2e;
+
+  uint32_t voffK[T::NLD], voffV[T::NLD];
+#pragma unroll
+  for (int j = 0; j < T::NLD; ++j) {
+    const int r = RPW * w + T::RPI * j + lane / T::NC, slot = lane % T::NC;
+    voffK[j] = r * rowstride + 16 * (slot ^ T::swz_k(r));
+    voffV[j] = r * rowstride + 16 * (slot ^ T::swz_v(r));
+  }
+  uint32_t offK[D / 16];
+#pragma unroll
+  for (int st = 0; st < D / 16; ++st) offK[st] = col * ROWB + 16 * ((2 * st + half) ^ T::swz_k(col));
+  uint32_t offV[D / 32];
+  {
+    const int s16 = lane & 15, grp = lane >> 4;
+    const int r = 4 * half + s16 / 4;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+      const int chunk = 4 * db + 2 * (grp & 1) + ((s16 & 3) >> 1);
+      offV[db] = r * ROWB + 16 * (chunk ^ T::swz_v(r)) + 8 * (s16 & 1);
+    }
+  }
+
+  f32x16 acc[D / 32];
+#pragma unroll
+  for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
+  float m_run = kMaxInit, l_run = 0.f;
+
+  const int n_tiles = max((g.kv_stop + BK - 1) / BK, 0);
+  const int q_last_w = g.qw + 31;
+  // tiles this wave uses: a causal wave stops at the tile holding its last row
+  const int n_w = a.causal ? min(n_tiles, q_last_w / BK + 1) : n_tiles;
+
+  auto issue = [&](const unsigned char* base, int t, unsigned char* dst, const uint32_t* voff) {
+    const int k0 = t * BK;
+    const int nvalid = min(BK, g.kv_stop - k0);
+    const uint32_t bytes = (uint32_t)(nvalid - 1) * rowstride + ROWB;
+    const rsrc_t rs = make_rsrc(base + (size_t)k0 * rowstride, bytes);
+#pragma unroll
+    for (int j = 0; j < T::NLD; ++j) buffer_load_lds16(rs, dst + (RPW * w + T::RPI * j) * ROWB, voff[j]);
+  };
+
+  auto qk = [&](const unsigned char* ks, f32x16* s) {
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb) {
+      s[kb] = f32x16{};
+#pragma unroll
+      for (int st = 0; st < D / 16; ++st) {
+        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
+        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+      }
+    }
+  };
+
+  // Tile t's softmax and P.V, with S_{t+1} formed from ks_next alongside.
+  auto step = [&](int t, f32x16* s, const unsigned char* vs, const unsigned char* ks_next, f32x16* sn) {
+    const int k0 = t * BK;
+    const bool need_mask = (k0 + BK > g.kv_end) || (a.causal && k0 + BK - 1 > g.qw) || (g.qw + 31 >= g.q_hi);
+    if (need_mask) {
+      const int base = k0 + 4 * half;
+      int lim = g.kv_end - 1 - base;
+      if (a.causal) lim = min(lim, g.qi - base);
+      if (!row_ok) lim = -1;
+#pragma unroll
+      for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[kb][r], s[kb][r + 1]));
+    const float mc = xor32_max(mx) * cx;
+    if (wave_any(mc > m_run + kRescaleLog2)) {
+      const float m_new = fmaxf(m_run, mc);
+      const float corr = fast_exp2(m_run - m_new);
+      m_run = m_new;
+      l_run *= corr;
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[i][r] *= corr;
+    }
+    // one basic block from here: S_{t+1} on the MFMA pipe under the exponentials
+    qk(ks_next, sn);
+    float rs = 0.f;
+#pragma unroll
+    for (int kb = 0; kb < BK / 32; ++kb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_run));
+        rs += p;
+        s[kb][r] = p;
+      }
+    l_run += rs;
+    bf16x8 pf[BK / 16];
+#pragma unroll
+    for (int c = 0; c < BK / 16; ++c) {
+      u32x4 pk;
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
+      pf[c] = as_bf16x8(pk);
+    }
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db) {
+#pragma unroll
+      for (int c = 0; c < BK / 16; ++c) {
+        const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + offV[db]);
+        const u32x2 hi = lds_read_tr16(vs + (16 * c + 8) * ROWB + offV[db]);
+        const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
+        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+      }
+    }
+  };
+
+  f32x16 sa[BK / 32], sb[BK / 32];
+  if (n_tiles > 0) {
+    issue(Kb, 0, smem0, voffK);
+    issue(Vb, 0, smem0 + TILE_B, voffV);
+    if (n_tiles > 1) issue(Kb, 1, smem1, voffK);
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    qk(smem0, sa);
+  }
+  // Tile t: K in stage t%2 until iteration t-1, V in stage t%2 from iteration t.
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(Kb, t + 2, smem0, voffK);
+    if (t + 1 < n_tiles) issue(Vb, t + 1, smem1 + TILE_B, voffV);
+    if (t < n_w) step(t, sa, smem0 + TILE_B, smem1, sb);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 3 < n_tiles) issue(Kb, t + 3, smem1, voffK);
+    if (t + 2 < n_tiles) issue(Vb, t + 2, smem0 + TILE_B, voffV);
+    if (t + 1 < n_w) step(t + 1, sb, smem1 + TILE_B, smem0, sa);
+  }
+
+  const float l_tot = xor32_sum(l_run);
+  const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
+  if (row_in) {
+    uint16_t* orow = (uint16_t*)a.o + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
+#pragma unroll
+    for (int db = 0; db < D / 32; ++db)
+#pragma unroll
+      for (int gq = 0; gq < 4; ++gq) {
+        u32x2 pk;
+        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
+      }
+    if (a.lse && half == 0)
+      a.lse[((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi] =
+          l_tot > 0.f ? (m_run + __log2f(l_tot)) * kLn2 : INFINITY;
+  }
+}
+
+// ---------------------------------------------------------------------------
 // fp32 path: v_mfma_f32_32x32x2f32 (full fp32 products) for both products.
 // The k index of one MFMA step is the wave half: half 0 contracts dim s,
 // half 1 dim D/2 + s, so each lane reads a contiguous half row of K.  For
@@ -775,10 +983,10 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
     const bool ring = hb && kv_len % 4 == 0 && q_len * kv_len * 4 < ((int64_t)1 << 31);
     if (head_dim == 128) {
       if (ring) return launch_flash_bias_ring(128, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<128, true, 0>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 0>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<128, true, 0>, a, s) : launch(flash_fwd_bf16_pipe_kernel<128, 32, 3>, a, s);
     }
     if (ring) return launch_flash_bias_ring(64, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<64, true, 0>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 0>, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<64, true, 0>, a, s) : launch(flash_fwd_bf16_pipe_kernel<64, 64, 2>, a, s);
   }
   // fp32 with fewer 128-row workgroups than CUs: split each query block's
   // keys over several waves (latency-bound sizes, like the reference's CPU

@@ -38,9 +38,12 @@ def _case(name, B, L, Hq, dev):
             mine, theirs = mine + M.CausalAlibiBias(), theirs + oracle.CausalAlibiBias()
         return mine, theirs, t, name == "sum"
     if name == "shared":
+        # scale 0.75: a fold scale near 4 makes the softmax so peaked that dS =
+        # P (dP - delta) cancels almost exactly, and one-ulp differences of the
+        # bf16 forward output move delta by more than the gradient tolerance
         qf, kf = rng_normal(71, (1, L, 4), (1, L, 4))
         t = [to_dev(x, dev, torch.float32).requires_grad_(True) for x in (qf, kf)]
-        return M.LowRankBias(*t, scale=2.0), oracle.LowRankBias(qf, kf, scale=2.0), t, False
+        return M.LowRankBias(*t, scale=0.75), oracle.LowRankBias(qf, kf, scale=0.75), t, False
     if name == "key_bias":
         (kb,) = rng_normal(72, (B, L))
         tk = to_dev(kb, dev, torch.float32).requires_grad_(True)
