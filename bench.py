@@ -291,7 +291,7 @@ def make_c5m(dev, gen):
     nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
     return dict(name="MLA materialised causal prefill bf16 B=1 L=4096 R=512 H=16 dk=dv=128", fn=fn,
                 flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="mla_project_bf16_kernel + flash_fwd_bf16_pipe_kernel<128,32,3>")
+                kernel="mla_project_bf16_kernel + flash_fwd_bf16_pipe_kernel<128,64,2>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
