@@ -39,6 +39,10 @@ from .masks import (  # noqa: F401
     LowRankBias,
     BatchedLowRankBias,
     LearnedAlibiBias,
+    LearnedRelativePositionBias,
+    MarginalizationMask,
+    NotMask,
+    T5RelativePositionBias,
     SeqLenMask,
     SoftCappingBias,
     SumBias,

@@ -93,6 +93,9 @@ class AttentionMask:
     def __xor__(self, other):
         return ComposeMask("xor", self, other)
 
+    def __invert__(self):
+        return NotMask(self)
+
 
 class NoMask(AttentionMask):
     def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
@@ -346,6 +349,54 @@ class KeyPaddingMask(AttentionMask):
 
     def tile_keep(self, b, span_q, span_k):
         return self(span_q, span_k, seg_q=self.rows(b, span_q))
+
+
+class NotMask(AttentionMask):
+    """:530-548: the complement of ``inner``."""
+
+    def __init__(self, inner):
+        self.inner = inner
+        self.stateful = inner.stateful
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        return np.logical_not(self.inner(q_idx, k_idx, seg_q, seg_k))
+
+    def tile_keep(self, b, span_q, span_k):
+        return np.logical_not(self.inner.tile_keep(b, span_q, span_k))
+
+
+def _payload_rows(vec2d_or_1d, b, span):
+    """A ``[T]`` or ``[B, T]`` per-position payload read at positions ``span``
+    of batch ``b``, zero past ``T`` (the XLA path's windowing of a
+    ``[1|B, T, 1, 1]`` payload, attention_xla.py:130-133, 146-168)."""
+    p = np.asarray(vec2d_or_1d)
+    vec = p if p.ndim == 1 else p[b]
+    span = np.asarray(span)
+    out = np.zeros(len(span), vec.dtype)
+    ok = span < len(vec)
+    out[ok] = vec[span[ok]]
+    return out
+
+
+class MarginalizationMask(AttentionMask):
+    """:1671-1778: ``(m[q] & m[k]) | (q == k)``.  ``tile_keep`` reads the
+    payload (``get_data``: ``[T]`` shared by every batch, ``[B, T]`` per
+    batch) at the query and at the key positions, as the XLA path does (the
+    key ids default to the query payload, attention_xla.py:262-263)."""
+
+    stateful = True
+
+    def __init__(self, mask):
+        self.mask = np.asarray(mask, bool)
+
+    def __call__(self, q_idx, k_idx, seg_q=None, seg_k=None):
+        q_idx, k_idx = np.asarray(q_idx), np.asarray(k_idx)
+        mq = np.asarray(seg_q, bool) if seg_q is not None else self.mask[..., q_idx]
+        mk = np.asarray(seg_k, bool) if seg_k is not None else self.mask[..., k_idx]
+        return (mq[..., :, None] & mk[..., None, :]) | (q_idx[:, None] == k_idx[None, :])
+
+    def tile_keep(self, b, span_q, span_k):
+        return self(span_q, span_k, _payload_rows(self.mask, b, span_q), _payload_rows(self.mask, b, span_k))
 
 
 class ComposeMask(AttentionMask):
@@ -650,6 +701,68 @@ class LearnedAlibiBias(AttentionBias):
         qp = np.asarray(q_idx) + self.query_offset
         kp = np.asarray(k_idx) + self.key_offset
         return scores - self.slopes[head] * (qp[:, None] - kp[None, :]).astype(np.float32)
+
+
+def relative_position_bucket(relative_position, *, num_buckets, max_distance, bidirectional):
+    """T5 bucketing of ``k - q`` (attention_mask_bias.py:2417-2449)."""
+    rp = -np.asarray(relative_position, np.int64)
+    if bidirectional:
+        half = num_buckets // 2
+        sign_bucket = (rp < 0).astype(np.int64) * half
+        rp = np.abs(rp)
+        nb = half
+    else:
+        sign_bucket = 0
+        rp = np.maximum(rp, 0)
+        nb = num_buckets
+    max_exact = nb // 2
+    small = rp < max_exact
+    rpf = rp.astype(np.float32)
+    large = np.float32(max_exact) + (
+        np.log(np.maximum(rpf, np.float32(1.0)) / np.float32(max_exact))
+        / np.log(np.float32(max_distance) / np.float32(max_exact))
+        * np.float32(nb - max_exact)
+    ).astype(np.float32)
+    large = np.minimum(nb - 1, large.astype(np.int64))
+    return np.where(small, rp, large) + sign_bucket
+
+
+class T5RelativePositionBias(AttentionBias):
+    """:2453-2517: ``scores + table[h|0, bucket(k - q)]``."""
+
+    def __init__(self, bias_table, *, num_buckets, max_distance=128, bidirectional=True):
+        bt = np.asarray(bias_table, np.float32)
+        if bt.ndim == 1:
+            bt = bt[None]
+        if bt.ndim != 2 or bt.shape[-1] != num_buckets:
+            raise ValueError("bias_table must have shape [H|1, num_buckets]")
+        self.bias_table, self.num_buckets = bt, int(num_buckets)
+        self.max_distance, self.bidirectional = int(max_distance), bool(bidirectional)
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        rel = np.asarray(k_idx)[None, :] - np.asarray(q_idx)[:, None]
+        bk = relative_position_bucket(rel, num_buckets=self.num_buckets, max_distance=self.max_distance,
+                                      bidirectional=self.bidirectional)
+        row = self.bias_table[0 if self.bias_table.shape[0] == 1 else int(h_idx)]
+        return scores + row[bk]
+
+
+class LearnedRelativePositionBias(AttentionBias):
+    """:2521-2561: ``scores + table[h|0, clip(k - q, -d, d) + d]``."""
+
+    def __init__(self, table, *, max_distance):
+        t = np.asarray(table, np.float32)
+        if t.ndim == 1:
+            t = t[None]
+        if t.ndim != 2 or t.shape[-1] != 2 * int(max_distance) + 1:
+            raise ValueError("table must have shape [H|1, 2*max_distance+1]")
+        self.table, self.max_distance = t, int(max_distance)
+
+    def __call__(self, scores, h_idx, q_idx, k_idx, data=None):
+        rel = np.asarray(k_idx)[None, :] - np.asarray(q_idx)[:, None]
+        rel = np.clip(rel, -self.max_distance, self.max_distance) + self.max_distance
+        row = self.table[0 if self.table.shape[0] == 1 else int(h_idx)]
+        return scores + row[rel]
 
 
 class SumBias(AttentionBias):

@@ -43,7 +43,8 @@ import os
 import torch
 
 from . import hip_attention as hip
-from .masks import LoweredBias, LoweredMask, lower_bias, lower_mask, split_low_rank_bias
+from .masks import (LoweredBias, LoweredMask, dense_keep, dense_relpos, dense_supported, lower_bias,
+                    lower_mask, split_low_rank_bias)
 
 HIP_ARCH = "gfx950"
 FLASH_HEAD_DIMS = (64, 128)
@@ -221,8 +222,16 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
     if key.shape[0] != B or value.shape != key.shape or key.shape[-1] != d or h_q % key.shape[2]:
         return None
     lm = lower_mask(mask)
+    mask_bias = None
     if lm is None:
-        return None
+        # no in-kernel form (NOT / OR / XOR, MarginalizationMask): an additive
+        # 0 / -inf bias of the mask's dense form is exact
+        keep = dense_keep(mask, B, l_q, key.shape[1], query.device)
+        if keep is None:
+            return None
+        lm = LoweredMask()
+        mask_bias = torch.zeros(keep.shape, dtype=torch.float32, device=query.device)
+        mask_bias = mask_bias.masked_fill_(~keep, float("-inf"))[:, None]
     if lm.row_kv_lengths is not None:
         rows = _row_kv_lengths(lm.row_kv_lengths, B, l_q, query.device)
         if rows is None:
@@ -244,6 +253,18 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
         return None
     if lb is not None and lb.dense is not None:
         lb.dense = lb.dense.to(device=query.device, dtype=torch.float32)
+    extra = [] if mask_bias is None else [mask_bias]
+    if lb is not None and lb.relpos:
+        for term in lb.relpos:
+            rows = (term.bias_table if hasattr(term, "bias_table") else term.table).shape[0]
+            if rows not in (1, h_q):
+                return None
+            extra.append(dense_relpos(term, l_q, key.shape[1], query.device))
+        lb.relpos = None
+    if extra:
+        lb = lb if lb is not None else LoweredBias()
+        for e in extra:
+            lb.dense = e if lb.dense is None else lb.dense + e
     return lm, lb
 
 
@@ -404,7 +425,7 @@ def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
         why.append(f"tensors must be on a {HIP_ARCH} ROCm device (got {getattr(q, 'device', None)})")
     if dropout_rate > 0:
         why.append("dropout is not supported")
-    if lower_mask(mask) is None:
+    if lower_mask(mask) is None and not dense_supported(mask):
         why.append(f"mask {type(mask).__name__} is not supported")
     if lower_bias(bias) is False:
         why.append(f"bias {type(bias).__name__} is not supported")

@@ -26,6 +26,11 @@ attention_mask_bias.py):
   kernels (what the kernels evaluate is an AND of the above);
 * ``DenseBias``       -- :1807-1922, ``scores + bias[b|0, h|0, q, k]`` with an
   fp32 ``[B|1, H|1, Q, K]`` tensor;
+* ``NotMask`` / OR / XOR compositions / ``MarginalizationMask`` (:530-548,
+  :324-525, :1671-1778) and ``T5RelativePositionBias`` /
+  ``LearnedRelativePositionBias`` (:2417-2561) -- no in-kernel form: the
+  route lowers them to a dense additive bias (``dense_keep``,
+  ``dense_relpos``);
 * low-rank biases     -- ``LowRankBias``, ``BatchedLowRankBias``,
   ``LearnedAlibiBias`` (:1926-2352): ``flex_attention`` and
   ``dot_product_attention`` fold their factors into Q/K
@@ -50,6 +55,7 @@ from __future__ import annotations
 
 from dataclasses import dataclass
 
+import numpy as np
 import torch
 
 
@@ -64,6 +70,9 @@ class AttentionMask:
 
     def __xor__(self, other):
         return ComposeMask("xor", self, other)
+
+    def __invert__(self):
+        return NotMask(self)
 
 
 class AttentionBias:
@@ -149,6 +158,16 @@ class KeyPaddingMask(AttentionMask):
         self.key_lengths = key_lengths
 
 
+class NotMask(AttentionMask):
+    def __init__(self, inner):
+        self.inner = inner
+
+
+class MarginalizationMask(AttentionMask):
+    def __init__(self, mask):
+        self.mask = mask
+
+
 class DenseBias(AttentionBias):
     def __init__(self, bias):
         if bias.ndim != 4:
@@ -193,6 +212,35 @@ class SoftCappingBias(AttentionBias):
 class PerHeadScaleBias(AttentionBias):
     def __init__(self, scales):
         self.scales = scales
+
+
+class T5RelativePositionBias(AttentionBias):
+    """``scores + table[h|0, bucket(k - q)]`` (attention_mask_bias.py:2453-2517)."""
+
+    def __init__(self, bias_table, *, num_buckets: int, max_distance: int = 128, bidirectional: bool = True):
+        bt = torch.as_tensor(bias_table)
+        if bt.ndim == 1:
+            bt = bt[None]
+        if bt.ndim != 2:
+            raise ValueError("bias_table must have shape [H|1, num_buckets]")
+        if int(bt.shape[-1]) != int(num_buckets):
+            raise ValueError("bias_table last dim must equal num_buckets")
+        self.bias_table, self.num_buckets = bt, int(num_buckets)
+        self.max_distance, self.bidirectional = int(max_distance), bool(bidirectional)
+
+
+class LearnedRelativePositionBias(AttentionBias):
+    """``scores + table[h|0, clip(k - q, -d, d) + d]`` (attention_mask_bias.py:2521-2561)."""
+
+    def __init__(self, table, *, max_distance: int):
+        t = torch.as_tensor(table)
+        if t.ndim == 1:
+            t = t[None]
+        if t.ndim != 2:
+            raise ValueError("table must have shape [H|1, 2*max_distance+1]")
+        if int(t.shape[-1]) != 2 * int(max_distance) + 1:
+            raise ValueError("table last dim must be 2*max_distance+1")
+        self.table, self.max_distance = t, int(max_distance)
 
 
 class LowRankBias(AttentionBias):
@@ -470,6 +518,7 @@ class LoweredBias:
     softcap: float = 0.0
     head_scales: object = None  # [H|1]
     constant: float = 0.0
+    relpos: list = None  # T5 / learned relative-position terms, added to ``dense`` per call
 
     @property
     def extended(self) -> bool:
@@ -478,7 +527,7 @@ class LoweredBias:
 
 
 _ADDITIVE = ("DenseBias", "IdentityBias", "ConstantBias", "CausalAlibiBias", "SymmetricAlibiBias",
-             "DistanceDecayBias")
+             "DistanceDecayBias", "T5RelativePositionBias", "LearnedRelativePositionBias")
 
 
 def _flatten_sum(bias, out) -> bool:
@@ -515,6 +564,8 @@ def lower_bias(bias):
             lb.dense = b if isinstance(b, torch.Tensor) else torch.as_tensor(b)
         elif pn == "ConstantBias":
             lb.constant += float(p.value)
+        elif pn in ("T5RelativePositionBias", "LearnedRelativePositionBias"):
+            lb.relpos = (lb.relpos or []) + [p]
         elif pn in ("CausalAlibiBias", "SymmetricAlibiBias", "DistanceDecayBias"):
             if lb.alibi is not None:
                 return False
@@ -522,3 +573,164 @@ def lower_bias(bias):
                         "DistanceDecayBias": "decay"}[pn]
             lb.alibi_alpha = float(getattr(p, "alpha", 1.0))
     return lb
+
+
+# ---------------------------------------------------------------------------
+# Dense forms, for the masks and biases without an in-kernel form (NOT / OR /
+# XOR compositions, MarginalizationMask, relative-position tables): the
+# kernels take them as an additive fp32 bias (0 / -inf for a mask), which is
+# exact and costs Lq * Lk floats per (batch, head) slice.
+# ---------------------------------------------------------------------------
+
+def _per_position(payload, B, n, device, dtype):
+    """A ``[T]`` (every batch) or ``[B, T]`` payload read at positions
+    ``0..n-1``, zero past ``T`` (how the reference's XLA path windows a
+    per-position payload, attention_xla.py:130-133, 146-168); None when the
+    batch does not match."""
+    t = torch.as_tensor(payload, device=device)
+    if t.ndim == 1:
+        t = t[None].expand(B, -1)
+    elif t.ndim != 2 or t.shape[0] != B:
+        return None
+    out = torch.zeros((B, n), dtype=dtype, device=device)
+    m = min(int(t.shape[1]), n)
+    out[:, :m] = t[:, :m].to(dtype)
+    return out
+
+
+def _per_batch(x, B, device):
+    t = torch.as_tensor(x, device=device).reshape(-1)
+    if t.numel() == 1:
+        t = t.expand(B)
+    return t if t.numel() == B else None
+
+
+def dense_keep(mask, B, l_q, l_k, device):
+    """``[B, Lq, Lk]`` boolean keep-mask of any mask object of the path
+    (attention_mask_bias.py semantics, stateful payloads read as the XLA path
+    reads them), or None when a payload does not fit the call."""
+    q = torch.arange(l_q, device=device)[None, :, None]
+    k = torch.arange(l_k, device=device)[None, None, :]
+    if mask is None:
+        return torch.ones((B, l_q, l_k), dtype=torch.bool, device=device)
+    name = _name(mask)
+
+    def full(x):
+        return x.expand(B, l_q, l_k)
+
+    if name == "NoMask":
+        return full(torch.ones((1, 1, 1), dtype=torch.bool, device=device))
+    if name == "CausalMask":
+        return full(k <= q)
+    if name == "CausalFromBottomRightMask":
+        return full(k <= q + (int(mask.kv_length) - int(mask.q_length)))
+    if name == "LocalWindowMask":
+        rw = 0 if mask.right_window is None else int(mask.right_window)
+        return full((k >= q - int(mask.left_window)) & (k <= q + rw))
+    if name == "CausalLocalWindowMask":
+        return full((k >= q - int(mask.left_window)) & (k <= q))
+    if name == "QKVLengthMask":
+        return full((q < int(mask.q_length)) & (k < int(mask.kv_length)))
+    if name in ("KVLenMask", "PrefixLMMask", "SeqLenMask"):
+        attr = {"KVLenMask": "kv_lengths", "PrefixLMMask": "prefix_lengths", "SeqLenMask": "seq_lengths"}[name]
+        L = _per_batch(getattr(mask, attr), B, device)
+        if L is None:
+            return None
+        L = L.to(torch.int64)[:, None, None]
+        if name == "KVLenMask":
+            return full(k < L)
+        if name == "PrefixLMMask":
+            return (k < L) | (k <= q)
+        return ((q < L) & (k < L)) | (q == k)
+    if name in ("SameSegmentMask", "BlockDiagonalMask", "BlockDiagonalCausalMask"):
+        qa = "query_segment_ids" if name == "SameSegmentMask" else "query_block_ids"
+        ka = "key_segment_ids" if name == "SameSegmentMask" else "key_block_ids"
+        kid = getattr(mask, ka) if getattr(mask, ka) is not None else getattr(mask, qa)
+        sq = torch.as_tensor(getattr(mask, qa), device=device)
+        sk = torch.as_tensor(kid, device=device)
+        if sq.shape[-1] != l_q or sk.shape[-1] != l_k:
+            return None
+        sq = sq.reshape(-1, l_q).expand(B, -1) if sq.ndim == 1 or sq.shape[0] == 1 else sq
+        sk = sk.reshape(-1, l_k).expand(B, -1) if sk.ndim == 1 or sk.shape[0] == 1 else sk
+        if sq.shape[0] != B or sk.shape[0] != B:
+            return None
+        keep = sq[:, :, None] == sk[:, None, :]
+        return keep & (k <= q) if name == "BlockDiagonalCausalMask" else keep
+    if name == "KeyPaddingMask":
+        kl = torch.as_tensor(mask.key_lengths, device=device)
+        if kl.dtype.is_floating_point:
+            return None
+        rows = (kl.to(torch.int64).reshape(1, 1).expand(B, l_q) if kl.ndim == 0
+                else _per_position(kl.to(torch.int64), B, l_q, device, torch.int64))
+        return None if rows is None else k < rows[:, :, None]
+    if name == "MarginalizationMask":
+        mq = _per_position(mask.mask, B, l_q, device, torch.bool)
+        mk = _per_position(mask.mask, B, l_k, device, torch.bool)
+        if mq is None or mk is None:
+            return None
+        return (mq[:, :, None] & mk[:, None, :]) | (q == k)
+    if name == "NotMask":
+        inner = dense_keep(mask.inner, B, l_q, l_k, device)
+        return None if inner is None else ~inner
+    if name == "ComposeMask":
+        lhs = dense_keep(mask.lhs, B, l_q, l_k, device)
+        rhs = dense_keep(mask.rhs, B, l_q, l_k, device)
+        if lhs is None or rhs is None:
+            return None
+        return {"and": torch.logical_and, "or": torch.logical_or, "xor": torch.logical_xor}[mask.op](lhs, rhs)
+    return None
+
+
+_DENSE_MASKS = ("NoMask", "CausalMask", "CausalFromBottomRightMask", "LocalWindowMask", "CausalLocalWindowMask",
+                "QKVLengthMask", "KVLenMask", "PrefixLMMask", "SeqLenMask", "SameSegmentMask", "BlockDiagonalMask",
+                "BlockDiagonalCausalMask", "KeyPaddingMask", "MarginalizationMask")
+
+
+def dense_supported(mask) -> bool:
+    """Whether ``dense_keep`` knows every node of ``mask``."""
+    if mask is None:
+        return True
+    name = _name(mask)
+    if name == "NotMask":
+        return dense_supported(mask.inner)
+    if name == "ComposeMask":
+        return getattr(mask, "op", None) in ("and", "or", "xor") and dense_supported(mask.lhs) and dense_supported(mask.rhs)
+    return name in _DENSE_MASKS
+
+
+def _t5_bucket_lut(rel, num_buckets, max_distance, bidirectional):
+    """T5 buckets of ``k - q`` values ``rel`` (attention_mask_bias.py:
+    2417-2449), float32 arithmetic as the reference."""
+    rp = -rel.astype(np.int64)
+    if bidirectional:
+        half = num_buckets // 2
+        sign = (rp < 0).astype(np.int64) * half
+        rp = np.abs(rp)
+        nb = half
+    else:
+        sign = 0
+        rp = np.maximum(rp, 0)
+        nb = num_buckets
+    max_exact = nb // 2
+    large = np.float32(max_exact) + (
+        np.log(np.maximum(rp.astype(np.float32), np.float32(1.0)) / np.float32(max_exact))
+        / np.log(np.float32(max_distance) / np.float32(max_exact)) * np.float32(nb - max_exact)
+    ).astype(np.float32)
+    large = np.minimum(nb - 1, large.astype(np.int64))
+    return np.where(rp < max_exact, rp, large) + sign
+
+
+def dense_relpos(term, l_q, l_k, device):
+    """``[1, H|1, Lq, Lk]`` fp32 values of a T5 / learned relative-position
+    term; differentiable in its table (a gather)."""
+    rel_vals = np.arange(-(l_q - 1), l_k, dtype=np.int64)  # every k - q
+    if _name(term) == "T5RelativePositionBias":
+        lut = _t5_bucket_lut(rel_vals, term.num_buckets, term.max_distance, term.bidirectional)
+        table = term.bias_table
+    else:
+        d = term.max_distance
+        lut = np.clip(rel_vals, -d, d) + d
+        table = term.table
+    lut_t = torch.as_tensor(lut, device=device)
+    idx = lut_t[torch.arange(l_k, device=device)[None, :] - torch.arange(l_q, device=device)[:, None] + (l_q - 1)]
+    return table.to(device=device, dtype=torch.float32)[:, idx][None]

@@ -101,7 +101,15 @@ def test_eligibility_rejects_without_touching_a_device(monkeypatch):
     monkeypatch.setattr(A, "hip_device", lambda t: True)
     q, k, v = _qkv()
     assert A._eligible(q, k, v, mask=None, bias=None, dropout_rate=0.1) is None
-    assert A._eligible(q, k, v, mask=M.CausalMask() | M.NoMask(), bias=None, dropout_rate=0.0) is None
+    class Unknown(M.AttentionMask):
+        pass
+
+    assert A._eligible(q, k, v, mask=Unknown(), bias=None, dropout_rate=0.0) is None
+    # an OR composition has no in-kernel form: it becomes a 0 / -inf dense bias
+    q4, k4, v4 = _qkv(lq=4, lk=4)
+    lm, lb = A._eligible(q4, k4, v4, mask=M.CausalMask() | M.LocalWindowMask(1, 0), bias=None, dropout_rate=0.0)
+    want = torch.where(torch.tril(torch.ones(4, 4, dtype=torch.bool)), 0.0, float("-inf"))
+    assert lm == M.LoweredMask() and lb.dense.shape == (1, 1, 4, 4) and torch.equal(lb.dense[0, 0], want)
     assert A._eligible(q, k, v, mask=None, bias=object(), dropout_rate=0.0) is None
     assert A._eligible(q, k, v[:, :5], mask=None, bias=None, dropout_rate=0.0) is None
     assert A._eligible(q, k, v, mask=M.KVLenMask([1, 2]), bias=None, dropout_rate=0.0) is None  # B = 1
@@ -305,3 +313,73 @@ def test_low_rank_fold_matches_oracle(dtype):
                             terms[:1], 0.1) is None
     with pytest.raises(ValueError, match="same rank"):
         M.LowRankBias(torch.zeros(2, 4, 3), torch.zeros(2, 4, 2))
+
+
+def _mask_pairs(B, lq, lk):
+    """(mirror mask, oracle mask) pairs over every mask class of the path."""
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(3)
+    lens = rng.integers(0, lk + 1, size=B).astype(np.int32)
+    seg_q = np.sort(rng.integers(0, 3, size=(B, lq)), axis=1).astype(np.int32)
+    marg = rng.random((B, lq)) < 0.6
+    kl = rng.integers(0, lk + 1, size=lq - 2).astype(np.int32)
+    t = torch.from_numpy
+    return [
+        (M.CausalMask(), oracle.CausalMask()),
+        (M.CausalFromBottomRightMask(lq, lk), oracle.CausalFromBottomRightMask(lq, lk)),
+        (M.LocalWindowMask(2, 1), oracle.LocalWindowMask(2, 1)),
+        (M.CausalLocalWindowMask(3), oracle.CausalLocalWindowMask(3)),
+        (M.QKVLengthMask(lq - 1, lk - 2), oracle.QKVLengthMask(lq - 1, lk - 2)),
+        (M.KVLenMask(t(lens)), oracle.KVLenMask(lens)),
+        (M.PrefixLMMask(t(lens)), oracle.PrefixLMMask(lens)),
+        (M.SeqLenMask(t(lens)), oracle.SeqLenMask(lens)),
+        (M.KeyPaddingMask(t(kl)), oracle.KeyPaddingMask(kl)),
+        (M.MarginalizationMask(t(marg)), oracle.MarginalizationMask(marg)),
+        (~M.CausalMask(), ~oracle.CausalMask()),
+        (M.CausalMask() | M.LocalWindowMask(1, 2), oracle.CausalMask() | oracle.LocalWindowMask(1, 2)),
+        (M.CausalMask() ^ M.KVLenMask(t(lens)), oracle.CausalMask() ^ oracle.KVLenMask(lens)),
+        (~(M.MarginalizationMask(t(marg)) & M.CausalMask()),
+         ~(oracle.MarginalizationMask(marg) & oracle.CausalMask())),
+    ] + ([(M.SameSegmentMask(t(seg_q)), oracle.SameSegmentMask(seg_q)),
+          (M.BlockDiagonalCausalMask(t(seg_q)), oracle.BlockDiagonalCausalMask(seg_q))] if lq == lk else [])
+
+
+@pytest.mark.parametrize("lq,lk", [(6, 6), (5, 9)])
+def test_dense_keep_matches_oracle(lq, lk):
+    """The dense forms the route falls back to agree with the oracle's tile
+    evaluation of every mask class (stateful payloads included)."""
+    import numpy as np
+
+    B = 2
+    for mine, theirs in _mask_pairs(B, lq, lk):
+        got = M.dense_keep(mine, B, lq, lk, "cpu")
+        want = np.stack([theirs.tile_keep(b, np.arange(lq), np.arange(lk)) for b in range(B)])
+        assert got is not None and got.shape == (B, lq, lk), type(mine).__name__
+        np.testing.assert_array_equal(got.numpy(), want, err_msg=type(mine).__name__)
+        assert M.dense_supported(mine)
+
+
+def test_dense_relpos_matches_oracle():
+    import numpy as np
+
+    import oracle
+
+    rng = np.random.default_rng(4)
+    for lq, lk in ((7, 7), (3, 40)):
+        t5 = rng.standard_normal((3, 16)).astype(np.float32)
+        lr = rng.standard_normal((1, 9)).astype(np.float32)
+        pairs = [(M.T5RelativePositionBias(torch.from_numpy(t5), num_buckets=16, max_distance=10),
+                  oracle.T5RelativePositionBias(t5, num_buckets=16, max_distance=10)),
+                 (M.T5RelativePositionBias(torch.from_numpy(t5[:1]), num_buckets=16, max_distance=20,
+                                           bidirectional=False),
+                  oracle.T5RelativePositionBias(t5[:1], num_buckets=16, max_distance=20, bidirectional=False)),
+                 (M.LearnedRelativePositionBias(torch.from_numpy(lr), max_distance=4),
+                  oracle.LearnedRelativePositionBias(lr, max_distance=4))]
+        for mine, theirs in pairs:
+            got = M.dense_relpos(mine, lq, lk, "cpu")[0]
+            for h in range(got.shape[0]):
+                want = theirs(np.zeros((lq, lk), np.float32), h, np.arange(lq), np.arange(lk))
+                np.testing.assert_array_equal(got[h].numpy(), want)

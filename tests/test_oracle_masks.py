@@ -274,3 +274,58 @@ def test_key_padding_payload_rows():
     # boolean payloads compare as 0 / 1
     mb = oracle.KeyPaddingMask(np.array([True, False]))
     np.testing.assert_array_equal(mb.tile_keep(0, _idx(2), _idx(3)).sum(axis=1), [1, 0])
+
+
+def test_marginalization_and_not_masks():
+    """tests/test_attention_mask_bias.py:173-179 (rect plus diagonal) and the
+    NotMask / OR / XOR compositions (:191-209); the payload read per query and
+    key position in the XLA path, per batch for a [B, T] payload."""
+    m = np.array([True, False, True, False])
+    got = oracle.MarginalizationMask(m)(_idx(4), _idx(4))
+    np.testing.assert_array_equal(got, (m[:, None] & m[None, :]) | np.eye(4, dtype=bool))
+    np.testing.assert_array_equal(oracle.MarginalizationMask(m).tile_keep(0, _idx(4), _idx(4)), got)
+    mb = np.array([[True, True, False], [False, True, True]])
+    for b in range(2):
+        want = (mb[b][:, None] & mb[b][None, :]) | np.eye(3, dtype=bool)
+        np.testing.assert_array_equal(oracle.MarginalizationMask(mb).tile_keep(b, _idx(3), _idx(3)), want)
+    # positions past the payload read the zero fill: only the diagonal survives
+    tail = oracle.MarginalizationMask(np.array([True, True])).tile_keep(0, _idx(4), _idx(4))
+    np.testing.assert_array_equal(tail[2:], np.eye(4, dtype=bool)[2:])
+    c = oracle.CausalMask()
+    np.testing.assert_array_equal((~c).tile_keep(0, _idx(5), _idx(5)), ~np.tril(np.ones((5, 5), bool)))
+    w = oracle.LocalWindowMask(1, 0)
+    got = (c | w).tile_keep(0, _idx(5), _idx(6)) ^ (c ^ w).tile_keep(0, _idx(5), _idx(6))
+    np.testing.assert_array_equal(got, (c & w).tile_keep(0, _idx(5), _idx(6)))
+
+
+def test_relative_position_buckets():
+    """T5 bucketing (attention_mask_bias.py:2417-2449) against hand-computed
+    values: 16 bidirectional buckets, max_distance 8 -> 8 per direction,
+    exact below 4, then 4 + floor(log(rp/4) / log(2) * 4) capped at 7; keys
+    after the query (k > q) in the upper half."""
+    rel_k_minus_q = np.array([0, -1, -3, -4, -5, -6, -7, -8, -50, 1, 3, 5, 100])
+    want = np.array([0, 1, 3, 4, 5, 6, 7, 7, 7, 9, 11, 13, 15])
+    got = oracle.masks.relative_position_bucket(rel_k_minus_q, num_buckets=16, max_distance=8, bidirectional=True)
+    np.testing.assert_array_equal(got, want)
+    # unidirectional: keys after the query share bucket 0
+    got = oracle.masks.relative_position_bucket(np.array([2, 0, -2, -9]), num_buckets=8, max_distance=16,
+                                                bidirectional=False)
+    # (k - q = -9: rp 9 >= 4 exact buckets, 4 + floor(log(9/4) / log(16/4) * 4) = 6)
+    np.testing.assert_array_equal(got, [0, 0, 2, 6])
+
+
+def test_relative_position_biases():
+    """tests/test_attention_mask_bias.py:323-350: the T5 table per head, and
+    the learned clipped-distance table."""
+    table = np.arange(32, dtype=np.float32).reshape(2, 16)
+    b = oracle.T5RelativePositionBias(table, num_buckets=16, max_distance=8, bidirectional=True)
+    z = np.zeros((4, 4), np.float32)
+    bk = oracle.masks.relative_position_bucket(_idx(4)[None, :] - _idx(4)[:, None], num_buckets=16,
+                                               max_distance=8, bidirectional=True)
+    for h in range(2):
+        np.testing.assert_array_equal(b(z, h, _idx(4), _idx(4)), table[h][bk])
+    max_d = 2
+    t = np.arange(2 * max_d + 1, dtype=np.float32)
+    lb = oracle.LearnedRelativePositionBias(t, max_distance=max_d)
+    rel = np.clip(_idx(5)[None, :] - _idx(3)[:, None], -max_d, max_d) + max_d
+    np.testing.assert_array_equal(lb(np.zeros((3, 5), np.float32), 0, _idx(3), _idx(5)), t[rel])
