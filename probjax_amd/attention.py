@@ -276,7 +276,7 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return False
-    if q.dtype != torch.bfloat16 or q.shape[-1] not in DECODE_HEAD_DIMS:
+    if q.dtype != torch.bfloat16 or _kernel_width(q.shape[-1]) is None:
         return False
     if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or (q.shape[2] // k.shape[2]) * q.shape[1] > DECODE_MAX_ROWS:
         return False
@@ -294,7 +294,8 @@ def use_splitkv(q, k, *, mask=None, bias=None, dropout_rate: float = 0.0,
     forces it when exact; ``None`` picks it for ``Lq <= 64`` and
     ``Lkv >= 1024``.  The HIP decode is also exact with a ``KVLenMask`` (keys
     past each length are skipped), so a length mask does not disable it here;
-    it needs bf16, head_dim 64/128 and ``(Hq/Hkv)*Lq <= 16``.
+    it needs bf16, head_dim <= 128 (zero-padded to 64 or 128) and
+    ``(Hq/Hkv)*Lq <= 16``.
     """
     lm = lower_mask(mask)
     if lm is not None and lm.row_kv_lengths is not None and getattr(q, "ndim", 0) == 4 and q.shape[1] == 1:
@@ -333,7 +334,28 @@ def _needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
+def _kernel_width(d: int):
+    """The kernels' head dim that carries head dim ``d`` (None: too wide)."""
+    return next((w for w in FLASH_HEAD_DIMS if w >= d), None)
+
+
+def _pad_features(x, width):
+    """``x`` with zero features appended up to ``width`` (autograd slices the
+    gradient back)."""
+    return torch.nn.functional.pad(x, (0, width - x.shape[-1]))
+
+
 def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False):
+    d = query.shape[-1]
+    width = _kernel_width(d)
+    if width is not None and width != d:
+        # Zero features change no q.k product and add only zero output
+        # columns: every kept score, weight and output element is the one the
+        # width-d computation gives (the reference pads its blocks to
+        # next_power_of_2(head_dim) with masked loads, kernels/attention.py:2168).
+        out = _run(_pad_features(query, width), _pad_features(key, width), _pad_features(value, width),
+                   lm, lb, sm_scale, split_kv, bias_grad)
+        return None if out is None else out[..., :d]
     dense = None if lb is None else lb.dense
     bias_in = dense if bias_grad and dense is not None and _needs_grad(dense) else None
     grad = _needs_grad(query, key, value) or bias_in is not None
@@ -433,8 +455,8 @@ def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
         why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp32)")
     if _needs_grad(q, k) and getattr(q, "dtype", None) not in BACKWARD_DTYPES:
         why.append(f"gradients need {BACKWARD_DTYPES} inputs (got {getattr(q, 'dtype', None)})")
-    if q.ndim == 4 and q.shape[-1] not in FLASH_HEAD_DIMS:
-        why.append(f"head_dim {q.shape[-1]} is not supported {FLASH_HEAD_DIMS}")
+    if q.ndim == 4 and _kernel_width(q.shape[-1]) is None:
+        why.append(f"head_dim {q.shape[-1]} is not supported (at most {FLASH_HEAD_DIMS[-1]})")
     detail = "; ".join(why) or "unsupported shape combination"
     return f"the HIP attention kernels cannot compute this call exactly: {detail}"
 
@@ -453,14 +475,21 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
     """
     del block_k, unused_tuning
     _gqa_group(q.shape[-2], k.shape[-2])
+    d = q.shape[-1]
+    width = _kernel_width(d)
+    if width is not None and width != d:
+        q, k, v = (_pad_features(x, width) for x in (q, k, v))
     chunk = 0
     if num_splits is not None:
         if num_splits < 1:
             raise ValueError(f"num_splits must be >= 1, got {num_splits}")
         per = -(-k.shape[1] // num_splits)
         chunk = max(128, -(-per // 128) * 128)
-    return hip.splitkv_decode(q, k, v, sm_scale=float(sm_scale), kv_lengths=kv_lengths,
-                              chunk=chunk, return_lse=return_lse)
+    res = hip.splitkv_decode(q, k, v, sm_scale=float(sm_scale), kv_lengths=kv_lengths,
+                             chunk=chunk, return_lse=return_lse)
+    if width == d or width is None:
+        return res
+    return (res[0][..., :d], res[1]) if return_lse else res[..., :d]
 
 
 class _MaterializedMLAFunction(torch.autograd.Function):

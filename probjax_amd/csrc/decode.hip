@@ -102,6 +102,82 @@ __device__ __forceinline__ void emit_row_elem(const DecodeArgs& a, int b, int g,
   }
 }
 
+// Work item of a decode workgroup: (batch b, kv group g, chunk chunk_id).
+// The hardware starts workgroups in index order as slots free up, so the
+// index order is the schedule.  With per-sequence lengths (B <=
+// kSchedMaxBatch) the items run longest first: every full chunk (sequence by
+// sequence, or chunk-major where every sequence has as many), then each
+// sequence's partial last chunk in decreasing size, then
+// the empty items, which exit at once.  The plain chunk-major order scatters
+// the partial chunks through the grid and leaves a tail of full chunks that
+// start late.  Every thread calls this (it holds two barriers); L receives
+// the sequence's clamped length; false: the item has no keys.
+constexpr int kSchedMaxBatch = 256;
+static_assert(kSchedMaxBatch <= kDecThreads, "one length per thread");
+__device__ bool decode_item(const DecodeArgs& a, int* sched, int& b, int& g, int& chunk_id, int& L) {
+  if (!a.lengths || a.B > kSchedMaxBatch) {
+    const int BG = a.B * a.G;
+    chunk_id = blockIdx.x / BG;
+    const int bg = blockIdx.x % BG;
+    b = bg / a.G;
+    g = bg % a.G;
+    L = seq_len(a, b);
+    return chunk_id * a.chunk < L;
+  }
+  const int q = blockIdx.x / a.G, t = threadIdx.x;
+  g = blockIdx.x % a.G;
+  int* nfs = sched + 4;                 // full chunks per sequence
+  int* rms = nfs + kSchedMaxBatch;      // keys of the partial last chunk
+  int Lt = 0, nf = 0, rt = 0;
+  if (t < a.B) {
+    Lt = seq_len(a, t);
+    nf = Lt / a.chunk;
+    rt = Lt - nf * a.chunk;
+    nfs[t] = nf;
+    rms[t] = rt;
+  }
+  if (t == 0) sched[0] = -1;
+  __syncthreads();
+  if (t < a.B) {
+    // sequence t: its full chunks are rows [pre, pre + nf) of the full part;
+    // its partial chunk (rt > 0) has the rank of rt among the partial chunks
+    // (ties by sequence index)
+    int pre = 0, full = 0, rank = 0, nf_min = nf, nf_max = nf;
+#pragma unroll 8
+    for (int u = 0; u < a.B; ++u) {
+      const int nu = nfs[u], ru = rms[u];
+      full += nu;
+      pre += u < t ? nu : 0;
+      nf_min = min(nf_min, nu);
+      nf_max = max(nf_max, nu);
+      rank += (ru > 0 && (ru > rt || (ru == rt && u < t))) ? 1 : 0;
+    }
+    int c = -1;
+    if (nf_min == nf_max) {
+      // as many full chunks in every sequence: chunk-major, as without lengths
+      if (q < full && q % a.B == t) c = q / a.B;
+    } else if (q >= pre && q < pre + nf) {
+      c = q - pre;
+    }
+    if (rt > 0 && q >= full && q - full == rank) c = nf;
+    if (c >= 0) {
+      sched[0] = t;
+      sched[1] = c;
+      sched[2] = Lt;
+    }
+  }
+  __syncthreads();
+  b = sched[0];
+  chunk_id = sched[1];
+  L = sched[2];
+  if (b < 0) {
+    b = 0;
+    L = 0;
+    return false;
+  }
+  return true;
+}
+
 // emit_row_elem for 4 consecutive dims d..d+3 (d a multiple of 4).
 __device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g, int r, int d,
                                               size_t part, bool final_out, float M, float Ls,
@@ -151,14 +227,15 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int BG = a.B * a.G;
-  const int chunk_id = blockIdx.x / BG;
-  const int bg = blockIdx.x % BG;
-  const int b = bg / a.G, g = bg % a.G;
-  const int L = seq_len(a, b);
+  __shared__ int sched[4 + 2 * kSchedMaxBatch];
+  int b, g, chunk_id, L;
+  if (!decode_item(a, sched, b, g, chunk_id, L)) return;  // nothing past the length is read
+  const int bg = b * a.G + g;
   const int c0 = chunk_id * a.chunk;
-  if (c0 >= L) return;  // the whole workgroup: nothing past the length is read
-  const int per_wave = a.chunk >> 2;
+  // the item's keys split evenly over the 4 waves (32-key steps), so a
+  // partial chunk takes a quarter of its length, not up to a full quarter
+  // chunk on one wave
+  const int per_wave = ((min(L - c0, a.chunk) + 127) >> 7) << 5;
   const int w0 = c0 + w * per_wave;
   const int w1 = min(w0 + per_wave, L);
 
@@ -387,11 +464,10 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int c16 = lane & 15, q4 = lane >> 4;
-  const int chunk_id = blockIdx.x / a.B;
-  const int b = blockIdx.x % a.B;
-  const int L = seq_len(a, b);
+  __shared__ int sched[4 + 2 * kSchedMaxBatch];
+  int b, g, chunk_id, L;
+  if (!decode_item(a, sched, b, g, chunk_id, L)) return;  // nothing past the length is read
   const int c0 = chunk_id * a.chunk;
-  if (c0 >= L) return;  // the whole workgroup: nothing past the length is read
   const int c1 = min(c0 + a.chunk, L);
   const int n_tiles = (c1 - c0 + BK - 1) / BK;
 
@@ -653,10 +729,13 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
 // two in [128, 2048] that leaves at most `items` (chunk, batch, group) work
 // items at full capacity.  Longer items amortise the per-item start-up (Q
 // fragments, the cross-wave combine, partial writes); the item target keeps
-// short batches spread over every CU.  Measured on MI355X: the GQA decode is
-// fastest with ~512 items at capacity (2048-key chunks for 32 x 8 x 8192), the
-// latent decode with ~256 (256-key chunks for 16 x 4096).
-constexpr int64_t kGqaItems = 512;
+// short batches spread over every CU.  Measured on MI355X (GQA, 32 query
+// heads over 8 KV heads, D = 128, ragged lengths): ~1024 items at capacity is
+// best or within 1% of best for 32 x 8192, 64 x 4096 and full-length 32 x
+// 8192 (2048-key chunks) and for 4 x 32768 (1024-key chunks; 2048-key chunks
+// leave too few items and take 1.75x as long); the latent decode is fastest
+// with ~256 (256-key chunks for 16 x 4096).
+constexpr int64_t kGqaItems = 1024;
 constexpr int64_t kMlaItems = 256;
 
 static int64_t auto_chunk(int64_t batch, int64_t groups, int64_t kv_len, int64_t items) {

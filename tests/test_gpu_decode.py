@@ -26,6 +26,11 @@ BF16_TOL = 2e-2
         (4, 1, 8192, 8, 2, 128, [1, 2, 3, 0], 128),      # chunks past every length: empty partials
         (16, 1, 300, 8, 2, 64, [7, 300, 1, 150, 299, 2, 64, 65, 0, 33, 120, 17, 280, 5, 9, 211], 128),
         (2, 1, 5000, 16, 4, 128, [5000, 4999], 0),
+        # longest-first item order: equal remainders (ties), exact multiples of
+        # the chunk, lengths past the cache and negative lengths (clamped)
+        (12, 1, 640, 8, 2, 64, [640, 600, 600, 128, 129, 0, -3, 9999, 600, 256, 1, 383], 128),
+        # more sequences than the in-kernel scheduler orders: chunk-major order
+        (300, 1, 256, 4, 1, 64, [(37 * i) % 300 - 20 for i in range(300)], 128),
     ],
 )
 def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, chunk):
@@ -60,6 +65,7 @@ def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, ch
         (2, 1, 16, 777, 128, 128, [777, 5], 0),
         (1, 1, 16, 4096, 576, 512, [4096], 8192),            # one chunk: the chunk kernel writes the output
         (5, 1, 3, 257, 576, 576, [257, 256, 2, 128, 129], 128),  # 3 rows
+        (6, 1, 4, 600, 512, 512, [600, 320, 320, 5, -1, 700], 128),  # ties, clamped lengths
     ],
 )
 def test_mla_decode_matches_oracle(device, b, lq, h, s, r, dv, lengths, chunk):

@@ -78,6 +78,21 @@ def test_use_splitkv_only_for_exact_cases():
     assert not A.use_splitkv(q4, k4, split_kv=True)
     q5, k5, _ = _qkv(dtype=torch.float32)
     assert not A.use_splitkv(q5, k5)
+    # head dims up to 128 are zero-padded to a kernel width; wider ones are not
+    q6, k6 = torch.zeros(1, 1, 8, 96, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 96, dtype=torch.bfloat16)
+    assert A.use_splitkv(q6, k6)
+    q7, k7 = torch.zeros(1, 1, 8, 160, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 160, dtype=torch.bfloat16)
+    assert not A.use_splitkv(q7, k7, split_kv=True)
+
+
+def test_kernel_width_and_padding():
+    assert [A._kernel_width(d) for d in (1, 32, 64, 65, 96, 128, 129, 256)] == [64, 64, 64, 128, 128, 128, None,
+                                                                                 None]
+    x = torch.randn(2, 3, 4, 40, requires_grad=True)
+    y = A._pad_features(x, 64)
+    assert y.shape == (2, 3, 4, 64) and torch.equal(y[..., :40], x) and not y[..., 40:].any()
+    y.sum().backward()
+    assert x.grad.shape == x.shape
 
 
 def test_route_falls_through_off_device():
@@ -192,6 +207,10 @@ def test_splitkv_forward_num_splits_to_chunk(monkeypatch):
     assert seen["chunk"] == 384  # ceil(1000/3) = 334 -> 3 x 128
     A.splitkv_forward(q, k, v, sm_scale=0.1)
     assert seen["chunk"] == 0
+    # a 48-wide head runs the kernel at 64 and comes back 48 wide
+    q48, k48, v48 = (x[..., :48] for x in (q, k, v))
+    out = A.splitkv_forward(q48, k48, v48, sm_scale=0.1)
+    assert out.shape[-1] == 48
     with pytest.raises(ValueError):
         A.splitkv_forward(q, k, v, sm_scale=0.1, num_splits=0)
     assert np.isclose(A._SPLITKV_MIN_KV_LEN, 1024)
