@@ -812,19 +812,76 @@ def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=N
     ``1/sqrt(D)``.  ``implementation`` in ``(None, "hip")``.  A ``DenseBias``
     whose tensor requires grad receives its gradient, as in probjax's dense
     path (``flex_attention`` / ``mha`` give bias data no cotangent, as the
-    reference's kernel VJP does).
+    reference's kernel VJP does).  Flax-style arrays are taken too: a boolean
+    ``mask`` (True = attend) and an additive ``bias``, broadcastable to
+    ``batch + [H, Lq, Lk]`` (probjax hands them to Flax's einsum,
+    layers/attention.py:1298-1319); a row the mask drops entirely gets Flax's
+    equal weights over every key.
     """
     if implementation not in (None, "hip"):
         raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
-    if isinstance(mask, torch.Tensor) or isinstance(bias, torch.Tensor):
-        raise ValueError(
-            "array masks/biases are not taken by the HIP kernels; pass mask/bias objects "
-            "(CausalMask, KVLenMask, QKVLengthMask, DenseBias)"
-        )
-    batch_shape = query.shape[:-3]
+    batch_shape = tuple(query.shape[:-3])
     flat = [x.reshape((-1,) + tuple(x.shape[-3:])) for x in (query, key, value)]
+    full_rows = None
+    if isinstance(mask, torch.Tensor) or isinstance(bias, torch.Tensor):
+        mask, bias, full_rows = _flax_arrays(mask, bias, batch_shape, flat[0], flat[1])
     out = flex_attention(*flat, mask=mask, bias=bias, dropout_rng=dropout_rng,
                          dropout_rate=dropout_rate, deterministic=deterministic, dtype=dtype,
                          sm_scale=sm_scale, enable_gqa=enable_gqa or query.shape[-2] != key.shape[-2],
                          implementation=implementation, _bias_grad=True)
-    return out.reshape(tuple(batch_shape) + tuple(out.shape[-3:]))
+    if full_rows is not None:
+        # Flax gives a row whose keys are all masked equal weights over every
+        # key (big_neg everywhere): the mean of V over the keys; the kernels
+        # give such a row zeros.
+        v = flat[2] if dtype is None else flat[2].to(dtype)
+        vmean = v.float().mean(dim=1)  # [B, Hkv, D]
+        vmean = vmean.repeat_interleave(out.shape[2] // vmean.shape[1], dim=1)[:, None]
+        out = torch.where(full_rows[..., None], vmean.to(out.dtype), out)
+    return out.reshape(batch_shape + tuple(out.shape[-3:]))
+
+
+def _flax_arrays(mask, bias, batch_shape, q, k):
+    """Flax array mask / bias (layers/attention.py:1298-1319 hands arrays to
+    ``flax.linen.dot_product_attention``): a boolean ``mask`` (True = attend)
+    and an additive ``bias``, each broadcastable to ``batch + [H, Lq, Lk]``.
+    Returns ``(mask object, bias object, rows)``: the bias as a ``DenseBias``
+    ``[B, H|1, Lq, Lk]`` over the flattened batch (its tensor keeps its
+    autograd history), the mask as a 0 / -inf ``DenseBias`` term, and the
+    ``[B, Lq, Hq]`` rows whose keys the array mask drops entirely (None when
+    there are none)."""
+    from .masks import AttentionBias, DenseBias
+
+    B, l_q, h_q = q.shape[0], q.shape[1], q.shape[2]
+    l_k = k.shape[1]
+
+    def dense(x, what):
+        t = torch.as_tensor(x, device=q.device)
+        if t.ndim < 2:
+            raise ValueError(f"array {what} needs at least [Lq, Lk] dims, got shape {tuple(t.shape)}")
+        t = t.reshape((1,) * max(0, len(batch_shape) + 3 - t.ndim) + tuple(t.shape))
+        heads = t.shape[-3]
+        if heads not in (1, h_q):
+            raise ValueError(f"array {what} has {heads} heads for {h_q} query heads")
+        try:
+            t = t.expand(batch_shape + (heads, l_q, l_k))
+        except RuntimeError as e:
+            raise ValueError(f"array {what} of shape {tuple(x.shape)} does not broadcast to "
+                             f"{batch_shape + (h_q, l_q, l_k)}") from e
+        return t.reshape((B, heads, l_q, l_k))
+
+    rows = None
+    terms = []
+    if isinstance(bias, torch.Tensor):
+        terms.append(dense(bias, "bias").float())
+        bias = None
+    if isinstance(mask, torch.Tensor):
+        keep = dense(mask, "mask").bool()
+        terms.append(torch.zeros(keep.shape, device=q.device).masked_fill_(~keep, float("-inf")))
+        empty = ~keep.any(dim=-1)  # [B, H|1, Lq]
+        if bool(empty.any()):
+            rows = empty.expand(B, h_q, l_q).transpose(1, 2)
+        mask = None
+    if terms:
+        extra = DenseBias(terms[0] if len(terms) == 1 else terms[0] + terms[1])
+        bias = extra if bias is None else (bias + extra if isinstance(bias, AttentionBias) else extra)
+    return mask, bias, rows

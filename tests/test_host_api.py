@@ -188,10 +188,12 @@ def test_mha_and_mla_refuse_off_device():
         A.mla(qd, c, wk, wv, dropout_rate=0.1)
 
 
-def test_dot_product_attention_refuses_array_masks():
+def test_dot_product_attention_array_masks_need_the_device():
     q, k, v = _qkv()
-    with pytest.raises(ValueError, match="array masks"):
+    with pytest.raises(ValueError, match="ROCm device"):
         A.dot_product_attention(q, k, v, mask=torch.ones(1, 1, 1, 2048, dtype=torch.bool))
+    with pytest.raises(ValueError, match="broadcast"):
+        A.dot_product_attention(q, k, v, bias=torch.zeros(3, 1, 1, 2048))
 
 
 def test_splitkv_forward_num_splits_to_chunk(monkeypatch):
@@ -402,3 +404,27 @@ def test_dense_relpos_matches_oracle():
             for h in range(got.shape[0]):
                 want = theirs(np.zeros((lq, lk), np.float32), h, np.arange(lq), np.arange(lk))
                 np.testing.assert_array_equal(got[h].numpy(), want)
+
+
+def test_flax_array_mask_and_bias_lowering():
+    q, k = torch.zeros(6, 5, 4, 8), torch.zeros(6, 7, 2, 8)
+    mask = torch.ones(3, 1, 5, 7, dtype=torch.bool)  # batch dims (2, 3) broadcast over the first
+    mask[1, 0, 2] = False                              # row 2 of batch (*, 1) drops every key
+    mask[0, 0, 0, 3] = False
+    bias = torch.randn(4, 5, 7, requires_grad=True)
+    m, b, rows = A._flax_arrays(mask, bias, (2, 3), q, k)
+    assert m is None and isinstance(b, M.DenseBias) and b.bias.shape == (6, 4, 5, 7)
+    d = b.bias
+    assert torch.isinf(d[1, :, 2]).all() and torch.isinf(d[4, :, 2]).all() and torch.isinf(d[0, :, 0, 3]).all()
+    fin = torch.isfinite(d)
+    assert torch.equal(d[fin], bias.expand(6, 4, 5, 7)[fin])
+    assert rows.shape == (6, 5, 4) and rows.sum() == 2 * 4 and rows[1, 2].all() and rows[4, 2].all()
+    # an object mask stays; an object bias takes the array mask as one more term
+    m2, b2, rows2 = A._flax_arrays(None, bias, (2, 3), q, k)
+    assert rows2 is None and b2.bias.requires_grad
+    m3, b3, _ = A._flax_arrays(mask, None, (2, 3), q, k)
+    assert b3.bias.shape == (6, 1, 5, 7)
+    with pytest.raises(ValueError, match="heads"):
+        A._flax_arrays(None, torch.zeros(3, 5, 7), (2, 3), q, k)
+    with pytest.raises(ValueError, match="broadcast"):
+        A._flax_arrays(None, torch.zeros(4, 4, 5, 7), (2, 3), q, k)
