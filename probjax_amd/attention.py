@@ -318,10 +318,12 @@ class _AttentionFunction(torch.autograd.Function):
         ctx.save_for_backward(query, key, value, out, lse)
         ctx.bwd_kwargs = bwd_kwargs
         ctx.bias_dtype = None if bias is None else bias.dtype
-        return out
+        ctx.mark_non_differentiable(lse)
+        return out, lse
 
     @staticmethod
-    def backward(ctx, dout):
+    def backward(ctx, dout, dlse=None):
+        del dlse  # the LSE output is a residual, not differentiated
         q, k, v, o, lse = ctx.saved_tensors
         if ctx.bias_dtype is not None and ctx.needs_input_grad[3]:
             dq, dk, dv, db = hip.flash_attention_bwd(q, k, v, o, dout, lse, bias_grad=True, **ctx.bwd_kwargs)
@@ -345,7 +347,10 @@ def _pad_features(x, width):
     return torch.nn.functional.pad(x, (0, width - x.shape[-1]))
 
 
-def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False):
+def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False, want_lse=False):
+    """Output of the HIP route for an eligible call (None: not computable
+    exactly); with ``want_lse`` ``(output, lse [B, Hq, Lq])``, where rows
+    without a valid key have ``lse = +inf``."""
     d = query.shape[-1]
     width = _kernel_width(d)
     if width is not None and width != d:
@@ -353,9 +358,11 @@ def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False):
         # columns: every kept score, weight and output element is the one the
         # width-d computation gives (the reference pads its blocks to
         # next_power_of_2(head_dim) with masked loads, kernels/attention.py:2168).
-        out = _run(_pad_features(query, width), _pad_features(key, width), _pad_features(value, width),
-                   lm, lb, sm_scale, split_kv, bias_grad)
-        return None if out is None else out[..., :d]
+        res = _run(_pad_features(query, width), _pad_features(key, width), _pad_features(value, width),
+                   lm, lb, sm_scale, split_kv, bias_grad, want_lse)
+        if res is None:
+            return None
+        return (res[0][..., :d], res[1]) if want_lse else res[..., :d]
     dense = None if lb is None else lb.dense
     bias_in = dense if bias_grad and dense is not None and _needs_grad(dense) else None
     grad = _needs_grad(query, key, value) or bias_in is not None
@@ -365,24 +372,26 @@ def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False):
         plan = _decode_plan(query, key, value, lm, lb)
         if plan is not None:
             if not grad:
-                return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, **plan)
+                return hip.splitkv_decode(query, key, value, sm_scale=sm_scale, return_lse=want_lse, **plan)
             # Split-KV primal, regular backward (probjax splitkv_attention,
             # kernels/attention_splitkv.py:253-272).
-            return _AttentionFunction.apply(
+            res = _AttentionFunction.apply(
                 query, key, value, None,
                 lambda q, k, v: hip.splitkv_decode(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
                 dict(sm_scale=sm_scale, kv_lengths=plan["kv_lengths"]),
             )
+            return res if want_lse else res[0]
     plan = _flash_plan(query, key, value, lm, lb)
     if plan is None:
         return None
     if not grad:
-        return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, **plan)
-    return _AttentionFunction.apply(
+        return hip.flash_attention_fwd(query, key, value, sm_scale=sm_scale, return_lse=want_lse, **plan)
+    res = _AttentionFunction.apply(
         query, key, value, bias_in,
         lambda q, k, v: hip.flash_attention_fwd(q, k, v, sm_scale=sm_scale, return_lse=True, **plan),
         dict(sm_scale=sm_scale, **plan),
     )
+    return res if want_lse else res[0]
 
 
 # ---------------------------------------------------------------------------
@@ -695,7 +704,7 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
                    deterministic=True, dtype=None, precision=None, module=None,
                    sm_scale: float | None = None, enable_gqa: bool = False,
                    split_kv: bool | None = None, implementation: str | None = None,
-                   _bias_grad: bool = False, **unused_tuning):
+                   _bias_grad: bool = False, _flax_fill: bool = False, **unused_tuning):
     """Fused softmax attention with mask/bias objects (probjax
     ``flex_attention``, layers/attention.py:1426-1759).
 
@@ -750,7 +759,10 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
         bias = rest
     e = _eligible(query, key, value, mask=mask, bias=bias, dropout_rate=active_dropout)
     if e is not None and (implementation == "hip" or device_table_enabled()):
-        out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv, bias_grad=_bias_grad)
+        out = _run(query, key, value, e[0], e[1], float(sm_scale), split_kv, bias_grad=_bias_grad,
+                   want_lse=_flax_fill)
+        if out is not None and _flax_fill:
+            out = _flax_empty_rows(out[0], out[1], value)
     if out is None:
         raise ValueError(
             f"implementation={implementation!r}: "
@@ -761,6 +773,25 @@ def flex_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
     if out_dim is not None:
         out = out[..., :out_dim]
     return out[0] if squeeze else out
+
+
+def _flax_empty_rows(out, lse, value):
+    """Flax's output for rows whose keys are all masked: ``where(mask,
+    logits, big_neg)`` gives such a row equal weights over every key, so the
+    mean of V (and dV = dO / Lk through autograd; no gradient reaches q, k or
+    the bias there).  The kernels leave such rows at zero with ``lse = +inf``,
+    so the fill is one device-side select, with no host synchronisation.
+    With no keys at all the einsum over an empty key axis gives zeros, which
+    the kernels already return."""
+    l_k = value.shape[1]
+    if l_k == 0:
+        return out
+    empty = torch.isinf(lse).transpose(1, 2)[..., None]  # [B, Lq, Hq, 1]
+    vmean = value.float().mean(dim=1)  # [B, Hkv, Dv]
+    vmean = vmean.repeat_interleave(out.shape[2] // vmean.shape[1], dim=1)[:, None]
+    if vmean.shape[-1] != out.shape[-1]:
+        vmean = vmean[..., : out.shape[-1]]
+    return torch.where(empty, vmean.to(out.dtype), out)
 
 
 def _fold_low_rank(query, key, value, terms, sm_scale: float):
@@ -815,28 +846,27 @@ def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=N
     reference's kernel VJP does).  Flax-style arrays are taken too: a boolean
     ``mask`` (True = attend) and an additive ``bias``, broadcastable to
     ``batch + [H, Lq, Lk]`` (probjax hands them to Flax's einsum,
-    layers/attention.py:1298-1319); a row the mask drops entirely gets Flax's
-    equal weights over every key.
+    layers/attention.py:1298-1319).
+
+    Rows whose keys the mask drops entirely follow the reference's two
+    paths: with a bias (array or object) or an array mask, probjax computes
+    the call with Flax's einsum over ``mask.dense()`` (``bias is not None``
+    disables its fused route, layers/attention.py:1173, and the device routes
+    refuse a bias, attention_device.py:128), whose masking by the dtype's most
+    negative value gives such a row equal weights over every key: the mean of
+    V.  Without a bias the fused kernel's zeros stand, as in ``flex_attention``.
     """
     if implementation not in (None, "hip"):
         raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
     batch_shape = tuple(query.shape[:-3])
     flat = [x.reshape((-1,) + tuple(x.shape[-3:])) for x in (query, key, value)]
-    full_rows = None
+    flax_path = bias is not None or isinstance(mask, torch.Tensor)
     if isinstance(mask, torch.Tensor) or isinstance(bias, torch.Tensor):
-        mask, bias, full_rows = _flax_arrays(mask, bias, batch_shape, flat[0], flat[1])
+        mask, bias = _flax_arrays(mask, bias, batch_shape, flat[0], flat[1])
     out = flex_attention(*flat, mask=mask, bias=bias, dropout_rng=dropout_rng,
                          dropout_rate=dropout_rate, deterministic=deterministic, dtype=dtype,
                          sm_scale=sm_scale, enable_gqa=enable_gqa or query.shape[-2] != key.shape[-2],
-                         implementation=implementation, _bias_grad=True)
-    if full_rows is not None:
-        # Flax gives a row whose keys are all masked equal weights over every
-        # key (big_neg everywhere): the mean of V over the keys; the kernels
-        # give such a row zeros.
-        v = flat[2] if dtype is None else flat[2].to(dtype)
-        vmean = v.float().mean(dim=1)  # [B, Hkv, D]
-        vmean = vmean.repeat_interleave(out.shape[2] // vmean.shape[1], dim=1)[:, None]
-        out = torch.where(full_rows[..., None], vmean.to(out.dtype), out)
+                         implementation=implementation, _bias_grad=True, _flax_fill=flax_path)
     return out.reshape(batch_shape + tuple(out.shape[-3:]))
 
 
@@ -844,11 +874,10 @@ def _flax_arrays(mask, bias, batch_shape, q, k):
     """Flax array mask / bias (layers/attention.py:1298-1319 hands arrays to
     ``flax.linen.dot_product_attention``): a boolean ``mask`` (True = attend)
     and an additive ``bias``, each broadcastable to ``batch + [H, Lq, Lk]``.
-    Returns ``(mask object, bias object, rows)``: the bias as a ``DenseBias``
+    Returns ``(mask object, bias object)``: the bias as a ``DenseBias``
     ``[B, H|1, Lq, Lk]`` over the flattened batch (its tensor keeps its
-    autograd history), the mask as a 0 / -inf ``DenseBias`` term, and the
-    ``[B, Lq, Hq]`` rows whose keys the array mask drops entirely (None when
-    there are none)."""
+    autograd history) and the mask as a 0 / -inf ``DenseBias`` term.  Rows
+    the mask drops entirely are found from the kernels' ``+inf`` LSE."""
     from .masks import AttentionBias, DenseBias
 
     B, l_q, h_q = q.shape[0], q.shape[1], q.shape[2]
@@ -869,7 +898,6 @@ def _flax_arrays(mask, bias, batch_shape, q, k):
                              f"{batch_shape + (h_q, l_q, l_k)}") from e
         return t.reshape((B, heads, l_q, l_k))
 
-    rows = None
     terms = []
     if isinstance(bias, torch.Tensor):
         terms.append(dense(bias, "bias").float())
@@ -877,11 +905,8 @@ def _flax_arrays(mask, bias, batch_shape, q, k):
     if isinstance(mask, torch.Tensor):
         keep = dense(mask, "mask").bool()
         terms.append(torch.zeros(keep.shape, device=q.device).masked_fill_(~keep, float("-inf")))
-        empty = ~keep.any(dim=-1)  # [B, H|1, Lq]
-        if bool(empty.any()):
-            rows = empty.expand(B, h_q, l_q).transpose(1, 2)
         mask = None
     if terms:
         extra = DenseBias(terms[0] if len(terms) == 1 else terms[0] + terms[1])
         bias = extra if bias is None else (bias + extra if isinstance(bias, AttentionBias) else extra)
-    return mask, bias, rows
+    return mask, bias

@@ -24,6 +24,14 @@ int check_launch(const char* where) {
   return PJX_ERR_LAUNCH;
 }
 
+int device_cu_count() {
+  int dev = 0, n = 0;
+  if (hipGetDevice(&dev) == hipSuccess &&
+      hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+    return n;
+  return 256;
+}
+
 int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) {
   ScoreMods& m = a.m;
   m.causal_shift = 0;

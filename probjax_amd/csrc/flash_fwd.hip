@@ -909,14 +909,7 @@ static int launch(K kernel, const FlashArgs& a, hipStream_t stream) {
 // 87 us against 113 us at B=1, H=16, L=4096 causal; 1-1.5% slower than
 // 32-key tiles from 1024 workgroups up).
 static int launch_pipe128(const FlashArgs& a, hipStream_t stream) {
-  static int cus = 0;
-  if (cus == 0) {
-    int dev = 0, n = 256;
-    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
-      cus = n;
-    else
-      cus = 256;
-  }
+  const int cus = device_cu_count();
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   if (blocks < 3L * cus) return launch(flash_fwd_bf16_pipe_kernel<128, 64, 2>, a, stream);
   return launch(flash_fwd_bf16_pipe_kernel<128, 32, 3>, a, stream);

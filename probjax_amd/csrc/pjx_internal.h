@@ -22,4 +22,9 @@ inline int fail(int code, const char* msg) {
 // instead of aborting.
 int check_launch(const char* where);
 
+// Compute units of the calling thread's current device, queried on every call
+// (no cached state: the library holds no mutable globals besides the
+// thread-local error string); 256 if the query fails.
+int device_cu_count();
+
 }  // namespace pjx

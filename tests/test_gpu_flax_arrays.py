@@ -19,7 +19,7 @@ import math
 import numpy as np
 import pytest
 
-from tests._helpers import rng_normal, to_dev, to_np
+from tests._helpers import max_abs, rng_normal, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -85,5 +85,107 @@ def test_array_mask_and_bias(device, dtype):
     else:
         assert o_err <= 1e-5
         for nm, g, w in zip(("dq", "dk", "dv", "dbias"), got, want):
+            err = float(np.max(np.abs(g - w)))
+            assert err <= 1e-5 * max(1.0, float(np.max(np.abs(w)))), f"{nm}: max err {err:.3e}"
+
+
+def _alibi_dense(Hq, Lq, Lk):
+    """CausalAlibiBias as a dense [Hq, Lq, Lk] bias: -2^-(h+1) * max(q - k, 0)
+    (attention_mask_bias.py:2230-2255)."""
+    d = np.maximum(np.arange(Lq)[:, None] - np.arange(Lk)[None, :], 0).astype(np.float64)
+    return np.stack([-(2.0 ** -(h + 1.0)) * d for h in range(Hq)])
+
+
+# (name, Lq, Lk, Hq, Hkv, D, mask kind, bias kind)
+_CASES = [
+    ("mask_only_per_head", 80, 112, 4, 4, 64, "array_per_head", None),
+    ("bias_only_d128", 64, 96, 4, 2, 128, None, "array"),
+    ("array_mask_object_alibi", 72, 72, 4, 2, 64, "array", "alibi"),
+    ("kvlen_zero_array_bias", 48, 80, 4, 2, 64, "kvlen0", "array"),
+    ("kvlen_zero_dense_object", 48, 80, 2, 1, 128, "kvlen0", "dense_object"),
+    ("padded_d96", 64, 64, 2, 2, 96, "array", "array"),
+]
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f32"])
+@pytest.mark.parametrize("case", _CASES, ids=[c[0] for c in _CASES])
+def test_flax_semantics_cases(device, dtype, case):
+    """Array masks alone, biases alone, Lq != Lk, per-head masks, an object
+    bias with an array mask, and object masks whose rows drop every key
+    (KVLenMask with a zero length) together with a bias: wherever probjax
+    takes the Flax einsum (a bias, or an array mask), such rows are the mean
+    of V, with dV = dO / Lk and no gradient to q, k or the bias there."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd import masks as M
+
+    name, Lq, Lk, Hq, Hkv, D, mkind, bkind = case
+    bf16 = dtype == "bf16"
+    B = 3
+    print(f"flax case {name} {dtype}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} D={D}", flush=True)
+    seed = 130 + _CASES.index(case)
+    q, k, v, do = rng_normal(seed, (B, Lq, Hq, D), (B, Lk, Hkv, D), (B, Lk, Hkv, D), (B, Lq, Hq, D))
+    rng = np.random.default_rng(seed + 1000)
+    tdt = torch.bfloat16 if bf16 else torch.float32
+    tq, tk, tv = (to_dev(x, device, tdt).requires_grad_(True) for x in (q, k, v))
+    keep = None
+    mask_arg = None
+    if mkind == "array":
+        keep = rng.random((B, 1, Lq, Lk)) < 0.8
+        keep[1, 0, 3] = False
+        mask_arg = torch.from_numpy(keep).to(device)
+    elif mkind == "array_per_head":
+        keep = rng.random((Hq, Lq, Lk)) < 0.75
+        keep[2, 7] = False
+        mask_arg = torch.from_numpy(keep).to(device)
+        keep = np.broadcast_to(keep[None], (B, Hq, Lq, Lk))
+    elif mkind == "kvlen0":
+        lengths = np.array([Lk, 0, Lk - 17], np.int32)
+        keep = np.broadcast_to((np.arange(Lk)[None, :] < lengths[:, None])[:, None, None, :], (B, 1, Lq, Lk))
+        mask_arg = M.KVLenMask(torch.from_numpy(lengths).to(device))
+    bias_ref = None
+    bias_arg = None
+    tb = None
+    if bkind == "array":
+        (bias,) = rng_normal(seed + 2000, (Hq, Lq, Lk), scale=0.5)
+        tb = to_dev(bias, device, torch.float32).requires_grad_(True)
+        bias_arg, bias_ref = tb, bias.astype(np.float64)
+    elif bkind == "dense_object":
+        (bias,) = rng_normal(seed + 2000, (B, Hq, Lq, Lk), scale=0.5)
+        tb = to_dev(bias, device, torch.float32).requires_grad_(True)
+        bias_arg, bias_ref = M.DenseBias(tb), bias.astype(np.float64)
+    elif bkind == "alibi":
+        bias_arg, bias_ref = M.CausalAlibiBias(), _alibi_dense(Hq, Lq, Lk)
+
+    out = A.dot_product_attention(tq, tk, tv, mask=mask_arg, bias=bias_arg)
+    assert out.shape == (B, Lq, Hq, D)
+    (out.float() * to_dev(do, device, torch.float32)).sum().backward()
+    torch.cuda.synchronize()
+
+    cdt = torch.float32 if bf16 else torch.float64
+    rq, rk, rv = (torch.from_numpy(np.asarray(to_np(t), np.float64)).to(cdt).requires_grad_(True) for t in (tq, tk, tv))
+    rb = None
+    if bias_ref is not None:
+        rb = torch.from_numpy(np.ascontiguousarray(bias_ref)).to(cdt).requires_grad_(tb is not None)
+    rm = None if keep is None else torch.from_numpy(np.ascontiguousarray(keep))
+    ro = _flax_reference(rq, rk, rv, rm, rb, torch.bfloat16 if bf16 else None)
+    (ro * torch.from_numpy(do.astype(np.float64)).to(cdt)).sum().backward()
+
+    got_o = to_np(out).astype(np.float64)
+    want_o = ro.detach().double().numpy()
+    pairs = [("dq", tq, rq), ("dk", tk, rk), ("dv", tv, rv)]
+    if tb is not None:
+        pairs.append(("dbias", tb, rb))
+    if bf16:
+        assert max_abs(got_o, want_o) <= 2e-2, f"out: {max_abs(got_o, want_o):.3e}"
+        for nm, g, w in pairs:
+            g, w = to_np(g.grad).astype(np.float64), w.grad.double().numpy()
+            atol = 2e-2 * max(1.0, float(np.max(np.abs(w))) / 4.0)
+            err = np.abs(g - w)
+            assert (err <= atol + 1e-2 * np.abs(w)).all(), f"{nm}: max err {err.max():.3e}"
+    else:
+        assert max_abs(got_o, want_o) <= 1e-5, f"out: {max_abs(got_o, want_o):.3e}"
+        for nm, g, w in pairs:
+            g, w = to_np(g.grad).astype(np.float64), w.grad.double().numpy()
             err = float(np.max(np.abs(g - w)))
             assert err <= 1e-5 * max(1.0, float(np.max(np.abs(w)))), f"{nm}: max err {err:.3e}"

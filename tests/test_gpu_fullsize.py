@@ -1,9 +1,8 @@
 """Parity at the BASELINE configurations' full sizes.
 
-Prefill configs (2, 4) are checked against the oracle on sampled query rows
-(causal row i is exactly attention of that row over keys 0..i, so a row
-subset is an unmasked oracle call); decode configs (3, 5) are small enough for
-the oracle in full.  Inputs are seeded numpy N(0,1) rounded to bf16 as the
+Every configuration is compared with the oracle over its whole output: all
+(batch, head) slices and all query rows (the oracle runs config 2 in about
+10 s of host time).  Inputs are seeded numpy N(0,1) rounded to bf16 as the
 configurations specify.  Tolerance: bf16 max-abs <= 2e-2 vs the fp32 oracle.
 """
 
@@ -24,21 +23,21 @@ def _bf16_inputs(seed, *shapes, scale=1.0):
     return [oracle.round_bf16(rng.standard_normal(s, dtype=np.float32) * np.float32(scale)) for s in shapes]
 
 
-def test_config2_full_size_sampled_rows(device):
+def test_config2_full_size(device):
     import torch
     from probjax_amd.attention import flex_attention
     from probjax_amd.masks import CausalMask
 
     B, L, H, D = 4, 4096, 16, 128
     q, k, v = _bf16_inputs(0, (B, L, H, D), (B, L, H, D), (B, L, H, D))
+    print(f"config 2 full size: B={B} L={L} H={H} D={D} causal", flush=True)
     out = to_np(flex_attention(*(to_dev(x, device, torch.bfloat16) for x in (q, k, v)), mask=CausalMask()))
-    rng = np.random.default_rng(1)
-    rows = np.unique(np.concatenate([[0, 1, 127, 128, 4095], rng.integers(0, L, 27)]))
-    for b, h in [(0, 0), (3, 15), (2, 7)]:
-        for i in rows:
-            want = oracle.xla_attention(q[b : b + 1, i : i + 1, h : h + 1], k[b : b + 1, : i + 1, h : h + 1],
-                                        v[b : b + 1, : i + 1, h : h + 1], sm_scale=1 / math.sqrt(D))
-            assert max_abs(out[b, i, h], want[0, 0, 0]) <= BF16_TOL, (b, h, i)
+    for b in range(B):
+        want = oracle.xla_attention(q[b : b + 1], k[b : b + 1], v[b : b + 1], mask=oracle.CausalMask(),
+                                    sm_scale=1 / math.sqrt(D))
+        err = max_abs(out[b], want[0])
+        print(f"  batch {b}: max-abs {err:.3e}", flush=True)
+        assert err <= BF16_TOL, (b, err)
     # causal row 0 attends to key 0 only: output = v0 exactly (up to bf16 output rounding)
     np.testing.assert_array_equal(out[:, 0], v[:, 0])
 
@@ -65,7 +64,7 @@ def test_config3_full_size(device):
     assert torch.equal(got, got2)
 
 
-def test_config4_full_size_sampled_rows(device):
+def test_config4_full_size(device):
     import torch
     from probjax_amd.attention import flex_attention
     from probjax_amd.masks import DenseBias, KVLenMask
@@ -76,19 +75,25 @@ def test_config4_full_size_sampled_rows(device):
     bias = (rng.standard_normal((H, L, L), dtype=np.float32) * np.float32(0.5))
     drop = int(round(0.1 * L)) + np.random.default_rng(0).integers(-16, 17, size=B)
     lengths = (L - drop).astype(np.int32)
-    out = to_np(flex_attention(*(to_dev(x, device, torch.bfloat16) for x in (q, k, v)),
-                               mask=KVLenMask(torch.from_numpy(lengths).to(device)),
-                               bias=DenseBias(to_dev(bias[None], device, torch.float32))))
-    rows = np.unique(np.concatenate([[0, L - 1], rng.integers(0, L, 14)]))
+    print(f"config 4 full size: B={B} L={L} H={H} D={D} lengths={lengths.tolist()}", flush=True)
+    tq, tk, tv = (to_dev(x, device, torch.bfloat16) for x in (q, k, v))
+    tb = to_dev(bias[None], device, torch.float32)
+    tl = torch.from_numpy(lengths).to(device)
+    got = flex_attention(tq, tk, tv, mask=KVLenMask(tl), bias=DenseBias(tb))
+    out = to_np(got)
+    want = oracle.xla_attention(q, k, v, mask=oracle.KVLenMask(lengths), bias=oracle.DenseBias(bias[None]),
+                                sm_scale=1 / 8)
+    err = max_abs(out, want)
+    print(f"  max-abs {err:.3e}", flush=True)
+    assert err <= BF16_TOL
+    # keys past each length and their bias columns never matter
+    k2, v2, b2 = tk.clone(), tv.clone(), tb.clone()
     for b in range(B):
-        n = lengths[b]
-        for h in (0, 5):
-            for i in rows:
-                want = oracle.xla_attention(q[b : b + 1, i : i + 1, h : h + 1], k[b : b + 1, :n, h : h + 1],
-                                            v[b : b + 1, :n, h : h + 1],
-                                            bias=oracle.DenseBias(bias[None, h : h + 1, i : i + 1, :n]),
-                                            sm_scale=1 / 8)
-                assert max_abs(out[b, i, h], want[0, 0, 0]) <= BF16_TOL, (b, h, i)
+        k2[b, lengths[b]:] = 100.0
+        v2[b, lengths[b]:] = -50.0
+    b2[..., int(lengths.max()):] = 1e4
+    got2 = flex_attention(tq, k2, v2, mask=KVLenMask(tl), bias=DenseBias(b2))
+    assert torch.equal(got, got2)
 
 
 def test_config5_full_size(device):

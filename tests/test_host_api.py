@@ -412,19 +412,38 @@ def test_flax_array_mask_and_bias_lowering():
     mask[1, 0, 2] = False                              # row 2 of batch (*, 1) drops every key
     mask[0, 0, 0, 3] = False
     bias = torch.randn(4, 5, 7, requires_grad=True)
-    m, b, rows = A._flax_arrays(mask, bias, (2, 3), q, k)
+    m, b = A._flax_arrays(mask, bias, (2, 3), q, k)
     assert m is None and isinstance(b, M.DenseBias) and b.bias.shape == (6, 4, 5, 7)
     d = b.bias
     assert torch.isinf(d[1, :, 2]).all() and torch.isinf(d[4, :, 2]).all() and torch.isinf(d[0, :, 0, 3]).all()
     fin = torch.isfinite(d)
     assert torch.equal(d[fin], bias.expand(6, 4, 5, 7)[fin])
-    assert rows.shape == (6, 5, 4) and rows.sum() == 2 * 4 and rows[1, 2].all() and rows[4, 2].all()
     # an object mask stays; an object bias takes the array mask as one more term
-    m2, b2, rows2 = A._flax_arrays(None, bias, (2, 3), q, k)
-    assert rows2 is None and b2.bias.requires_grad
-    m3, b3, _ = A._flax_arrays(mask, None, (2, 3), q, k)
+    m2, b2 = A._flax_arrays(None, bias, (2, 3), q, k)
+    assert b2.bias.requires_grad
+    m3, b3 = A._flax_arrays(mask, None, (2, 3), q, k)
     assert b3.bias.shape == (6, 1, 5, 7)
     with pytest.raises(ValueError, match="heads"):
         A._flax_arrays(None, torch.zeros(3, 5, 7), (2, 3), q, k)
     with pytest.raises(ValueError, match="broadcast"):
         A._flax_arrays(None, torch.zeros(4, 4, 5, 7), (2, 3), q, k)
+
+
+def test_flax_empty_rows_fill():
+    """Rows with lse = +inf (no valid key) take the mean of V, per query head
+    of each KV group; the others keep the kernel output.  No keys at all keep
+    the zeros (Flax's einsum over an empty key axis)."""
+    torch.manual_seed(0)
+    B, Lq, Lk, Hq, Hkv, D = 2, 3, 5, 4, 2, 8
+    out = torch.randn(B, Lq, Hq, D)
+    v = torch.randn(B, Lk, Hkv, D)
+    lse = torch.randn(B, Hq, Lq)
+    lse[1, 3, 2] = float("inf")
+    got = A._flax_empty_rows(out, lse, v)
+    want = out.clone()
+    want[1, 2, 3] = v[1, :, 1].mean(dim=0)
+    assert torch.equal(got, want)
+    v0 = torch.randn(B, 0, Hkv, D)
+    lse0 = torch.full((B, Hq, Lq), float("inf"))
+    z = torch.zeros(B, Lq, Hq, D)
+    assert torch.equal(A._flax_empty_rows(z, lse0, v0), z)
