@@ -113,8 +113,9 @@ const char* pjx_last_error(void);
  *
  * mods: extended masks / score modifiers (pjx_score_mods) or NULL.
  *
- * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim in {64, 128}
- * (k and v share it).  sm_scale must be > 0.
+ * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim in {64, 128},
+ * or 256 in bf16 (k and v share it; the reference's fused path takes
+ * head_dim <= 256, layers/attention.py:1193-1195).  sm_scale must be > 0.
  */
 int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
                   float* lse, const int32_t* kv_lengths, const float* bias,
@@ -154,7 +155,7 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.  mods: the
  * forward's (pjx_score_mods) or NULL.
  * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 (all fp32 products, no roundings).
- * head_dim in {64, 128}.
+ * head_dim in {64, 128}, or 256 in bf16.
  */
 int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
@@ -217,6 +218,67 @@ int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* k
                    int64_t batch, int64_t q_len, int64_t heads, int64_t kv_len,
                    int64_t rank, int64_t v_dim, float sm_scale, int64_t chunk,
                    void* stream);
+
+/*
+ * Latent (MLA) attention forward, absorbed form K = V = cache, any query
+ * length.  Replaces the absorbed `mla_forward` kernel and its launch
+ * (probjax/nn/pallas_kernels/kernels/latent_attention.py: _mla_forward_kernel
+ * 79-197 with wk = wv = None, _mla_build 247-377, mla_fwd_absorbed_p 380-388,
+ * called from mla 636-766) with the masks and bias of pjx_flash_fwd:
+ *
+ *   s = sm_scale * q.c (fp32) [+ bias] then masked -> -inf;
+ *   o = softmax(s) . c[:, :v_dim], P rounded to bf16 before the product.
+ *
+ * q [B, Lq, H, R] bf16 (all H heads share the one latent head; folded calls
+ * pass [B, Lq*H, 1, R] with H = 1); cache [B, S, R] bf16; o [B, Lq, H, v_dim]
+ * bf16 = the first v_dim columns of mla(q, cache, None, None) (v_dim == R
+ * gives the API-exact output); lse optional fp32 [B, H, Lq] natural log.
+ * kv_lengths, bias ([1|B, 1|H, Lq, S] fp32), q_valid / kv_valid, causal and
+ * mods as for pjx_flash_fwd (with Lk = S, Hq = H).
+ * (rank, v_dim) in {(576, 512), (576, 576), (512, 512)}, or rank in
+ * {64, 128, 256} with v_dim == rank (the flash kernels with one K = V head).
+ */
+int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o, float* lse,
+                const int32_t* kv_lengths, const float* bias, int64_t bias_batch,
+                int64_t bias_heads, int64_t batch, int64_t q_len, int64_t kv_len,
+                int64_t heads, int64_t rank, int64_t v_dim, int64_t q_valid, int64_t kv_valid,
+                int causal, float sm_scale, const pjx_score_mods* mods, void* stream);
+
+/*
+ * Bytes of workspace pjx_mla_bwd needs for these sizes: delta and the base-2
+ * LSE per query row, plus fp32 partial cache gradients of the query-head
+ * groups the key-side kernel splits the heads into (a function of the sizes
+ * only).
+ */
+size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64_t q_len, int64_t kv_len,
+                                  int64_t rank);
+
+/*
+ * Backward of pjx_mla_fwd: dq and dcache.  Replaces the custom VJP of the
+ * absorbed `mla` (probjax/nn/pallas_kernels/kernels/latent_attention.py:
+ * 752-766), which differentiates the materialised computation: mha over
+ * K = V = the latent broadcast to every head (_materialize_kv :396-410,
+ * _materialized_mla :413-468), so that
+ *
+ *   delta = sum_d o*do;  p = exp(s - lse);  ds = p * (do.c[:, :v_dim]^T - delta) * sm_scale
+ *   dq = sum_k bf16(ds) c,
+ *   dcache = sum over heads and queries of bf16(ds)^T q + bf16(p)^T do (first v_dim dims)
+ *
+ * with fp32 accumulation (the sum over heads in fp32 before one rounding).
+ * The bias gets no gradient, as the reference's VJP returns none for mask
+ * and bias leaves.  Arguments as pjx_mla_fwd, plus o (the forward output
+ * [B, Lq, H, v_dim]), dout (its gradient, same shape), lse (the forward's
+ * [B, H, Lq] natural-log LSE); dq [B, Lq, H, rank] and dcache [B, S, rank] are
+ * fully written.  workspace: at least pjx_mla_bwd_workspace_size(batch, heads,
+ * q_len, kv_len, rank) bytes.  (rank, v_dim) in {(576, 512), (576, 576),
+ * (512, 512)}; bf16.
+ */
+int pjx_mla_bwd(int dtype, const void* q, const void* cache, const void* o, const void* dout,
+                const float* lse, void* dq, void* dcache, void* workspace, size_t workspace_bytes,
+                const int32_t* kv_lengths, const float* bias, int64_t bias_batch,
+                int64_t bias_heads, int64_t batch, int64_t q_len, int64_t kv_len, int64_t heads,
+                int64_t rank, int64_t v_dim, int64_t q_valid, int64_t kv_valid, int causal,
+                float sm_scale, const pjx_score_mods* mods, void* stream);
 
 /*
  * Latent up-projection of materialised latent attention (mla with wk / wv).

@@ -47,8 +47,10 @@ from .masks import (LoweredBias, LoweredMask, dense_keep, dense_relpos, dense_su
                     lower_mask, split_low_rank_bias)
 
 HIP_ARCH = "gfx950"
-FLASH_HEAD_DIMS = (64, 128)
+FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 only
+FLASH_HEAD_DIMS_F32 = (64, 128)
 DECODE_HEAD_DIMS = (64, 128)
+LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (bfloat16)
 DECODE_MAX_ROWS = 16
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
 BACKWARD_DTYPES = (torch.bfloat16, torch.float32)  # dtypes pjx_flash_bwd takes
@@ -187,13 +189,14 @@ def _score_mods(lm: LoweredMask, lb: LoweredBias | None, B, l_q, l_k, h_q, devic
     return m
 
 
-def _flash_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
-    """Arguments of the flash forward for this call, or None."""
+def _flash_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None, check_dim: bool = True):
+    """Arguments of the flash forward for this call, or None (``check_dim``:
+    the head dim must be a flash kernel width)."""
     if query.dtype not in (torch.bfloat16, torch.float32):
         return None
     B, l_q, h_q, d = query.shape
     l_k = key.shape[1]
-    if d not in FLASH_HEAD_DIMS:
+    if check_dim and _kernel_width(d, query.dtype) != d:
         return None
     dense = None if lb is None else lb.dense
     if dense is not None:
@@ -276,7 +279,7 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return False
-    if q.dtype != torch.bfloat16 or _kernel_width(q.shape[-1]) is None:
+    if q.dtype != torch.bfloat16 or _decode_width(q.shape[-1]) is None:
         return False
     if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or (q.shape[2] // k.shape[2]) * q.shape[1] > DECODE_MAX_ROWS:
         return False
@@ -336,9 +339,16 @@ def _needs_grad(*ts) -> bool:
     return torch.is_grad_enabled() and any(t.requires_grad for t in ts)
 
 
-def _kernel_width(d: int):
-    """The kernels' head dim that carries head dim ``d`` (None: too wide)."""
-    return next((w for w in FLASH_HEAD_DIMS if w >= d), None)
+def _kernel_width(d: int, dtype=torch.bfloat16):
+    """The flash kernels' head dim that carries head dim ``d`` in ``dtype``
+    (None: too wide): 64, 128, or 256 in bfloat16."""
+    widths = FLASH_HEAD_DIMS if dtype == torch.bfloat16 else FLASH_HEAD_DIMS_F32
+    return next((w for w in widths if w >= d), None)
+
+
+def _decode_width(d: int):
+    """The split-KV decode's head dim that carries head dim ``d`` (None: too wide)."""
+    return next((w for w in DECODE_HEAD_DIMS if w >= d), None)
 
 
 def _pad_features(x, width):
@@ -352,7 +362,7 @@ def _run(query, key, value, lm, lb, sm_scale, split_kv, bias_grad=False, want_ls
     exactly); with ``want_lse`` ``(output, lse [B, Hq, Lq])``, where rows
     without a valid key have ``lse = +inf``."""
     d = query.shape[-1]
-    width = _kernel_width(d)
+    width = _kernel_width(d, query.dtype)
     if width is not None and width != d:
         # Zero features change no q.k product and add only zero output
         # columns: every kept score, weight and output element is the one the
@@ -464,8 +474,9 @@ def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
         why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp32)")
     if _needs_grad(q, k) and getattr(q, "dtype", None) not in BACKWARD_DTYPES:
         why.append(f"gradients need {BACKWARD_DTYPES} inputs (got {getattr(q, 'dtype', None)})")
-    if q.ndim == 4 and _kernel_width(q.shape[-1]) is None:
-        why.append(f"head_dim {q.shape[-1]} is not supported (at most {FLASH_HEAD_DIMS[-1]})")
+    if q.ndim == 4 and _kernel_width(q.shape[-1], getattr(q, "dtype", None)) is None:
+        why.append(f"head_dim {q.shape[-1]} is not supported (at most {FLASH_HEAD_DIMS[-1]} in bfloat16, "
+                   f"{FLASH_HEAD_DIMS_F32[-1]} in float32)")
     detail = "; ".join(why) or "unsupported shape combination"
     return f"the HIP attention kernels cannot compute this call exactly: {detail}"
 
@@ -485,7 +496,7 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
     del block_k, unused_tuning
     _gqa_group(q.shape[-2], k.shape[-2])
     d = q.shape[-1]
-    width = _kernel_width(d)
+    width = _decode_width(d)
     if width is not None and width != d:
         q, k, v = (_pad_features(x, width) for x in (q, k, v))
     chunk = 0
@@ -555,10 +566,10 @@ def _mla_materialized(q, cache, wk, wv, *, mask, bias, sm_scale):
     kernels; ValueError when they cannot compute the call exactly."""
     B, l_q, H, dk_dim = q.shape
     dv_dim = wv.shape[1]
-    width = max(dk_dim, dv_dim)
-    width = next((w for w in FLASH_HEAD_DIMS if w >= width), None)
+    width = _kernel_width(max(dk_dim, dv_dim), q.dtype)
     if width is None:
-        raise ValueError(f"materialised mla supports head dims up to {FLASH_HEAD_DIMS[-1]}, "
+        top = (FLASH_HEAD_DIMS if q.dtype == torch.bfloat16 else FLASH_HEAD_DIMS_F32)[-1]
+        raise ValueError(f"materialised mla supports head dims up to {top} in {q.dtype}, "
                          f"got qk {dk_dim}, v {dv_dim}")
     if not (q.dtype == cache.dtype == wk.dtype == wv.dtype) or q.dtype not in BACKWARD_DTYPES:
         raise ValueError("materialised mla takes q, cache, wk and wv of one dtype (bfloat16 or float32)")
@@ -642,7 +653,14 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     Absorbed form (``wk = wv = None``, ``K = V = cache``): ``q [B, Q, H, R]``,
     ``cache [B, S, R]`` -> ``[B, Q, H, R]`` (or the first ``v_dim`` columns,
     which is all a caller that multiplies by ``W_UV`` of width ``v_dim``
-    needs); ``mask``: ``None`` / ``NoMask`` / ``KVLenMask``, no bias.
+    needs), any query length, every mask and bias of the flash route,
+    differentiable in ``q`` and ``cache`` (bias data gets no gradient, as in
+    the reference's VJP); latent widths up to 576 in bfloat16 (up to 128 in
+    float32).  Decode steps (``Q * H <= 16``, no gradient, no bias,
+    ``None`` / ``KVLenMask``) run the split-KV latent kernel; the rest the
+    latent flash kernels, whose heads share one K = V head (the folded
+    ``[B, Q*H, 1, R]`` form of the reference layer is the same call with
+    ``H = 1``).
 
     Materialised form (``wk [H, qk_head_dim, R]``, ``wv [H, v_head_dim, R]``):
     ``q [B, Q, H, qk_head_dim]`` -> ``[B, Q, H, v_head_dim]``, every mask and
@@ -685,14 +703,119 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
         if lengths is not None:
             return _mla_absorbed(q, cache, wk, wv, lengths, sm_scale)
         return _mla_materialized(q, cache, wk, wv, mask=mask, bias=bias, sm_scale=sm_scale)
-    if bias is not None or dropout_rate > 0:
-        raise ValueError("the HIP latent-attention kernel takes no bias or dropout")
+    if dropout_rate > 0:
+        raise ValueError("the HIP latent-attention kernels take no dropout")
+    if not hip_device(q) or cache.device != q.device:
+        raise ValueError(f"the HIP latent-attention kernels need tensors on a {HIP_ARCH} ROCm device")
+    R = q.shape[-1]
+    dv = R if v_dim is None else int(v_dim)
+    if not 1 <= dv <= R:
+        raise ValueError(f"v_dim must be in [1, {R}], got {dv}")
+    lengths = _latent_decode_lengths(q, cache, mask, bias, dv)
+    if lengths is not None:
+        return hip.mla_decode(q, cache, sm_scale=float(sm_scale), v_dim=dv,
+                              kv_lengths=None if isinstance(lengths, str) else lengths)
+    return _mla_latent(q, cache, mask=mask, bias=bias, sm_scale=float(sm_scale), v_dim=dv)
+
+
+def _latent_decode_lengths(q, cache, mask, bias, dv):
+    """Per-batch KV lengths ("all" for none) when an absorbed call is a decode
+    step the split-KV latent kernel computes exactly (no gradient, no bias,
+    ``None`` / ``KVLenMask`` / one-row ``KeyPaddingMask``, bf16, a rank and
+    output width it carries, ``Lq * H <= 16``); else None."""
+    B, l_q, H, R = q.shape
+    if bias is not None or _needs_grad(q, cache):
+        return None
+    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
+        return None
+    if (R, dv) not in MLA_SHAPES or l_q * H > DECODE_MAX_ROWS:
+        return None
     lm = lower_mask(mask)
-    if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
-        raise ValueError(f"the HIP latent-attention kernel takes None / NoMask / KVLenMask, got {type(mask).__name__}")
-    if not hip_device(q):
-        raise ValueError(f"the HIP latent-attention kernel needs tensors on a {HIP_ARCH} ROCm device")
-    return hip.mla_decode(q, cache, sm_scale=float(sm_scale), v_dim=v_dim, kv_lengths=lm.kv_lengths)
+    if lm is None:
+        return None
+    if lm.row_kv_lengths is not None and l_q == 1:
+        rows = _row_kv_lengths(lm.row_kv_lengths, B, 1, q.device)
+        if rows is None:
+            return None
+        lm.row_kv_lengths, lm.kv_lengths = None, rows[:, 0]
+    if lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
+        return None
+    if lm.kv_lengths is None:
+        return "all"
+    return _lengths_tensor(lm.kv_lengths, B, q.device)
+
+
+def _latent_width(r: int, dtype):
+    """The kernel rank that carries latent width ``r`` (zero-padded): a flash
+    head width up to 256, else 512 or 576 (bfloat16); None when too wide."""
+    w = _kernel_width(r, dtype)
+    if w is not None:
+        return w
+    if dtype != torch.bfloat16:
+        return None
+    return next((x for x in LATENT_WIDTHS if x >= r), None)
+
+
+class _LatentFunction(torch.autograd.Function):
+    """Absorbed latent attention on the wide latent kernels, differentiable in
+    ``q`` and ``cache``: the forward is ``pjx_mla_fwd``, the backward
+    ``pjx_mla_bwd`` (probjax's custom VJP of ``mla``, latent_attention.py:
+    752-766: the VJP of ``mha`` over K = V = the latent broadcast to every
+    head, so the cache gets the head sum of dK + dV; the bias none)."""
+
+    @staticmethod
+    def forward(ctx, q, cache, st):
+        o, lse = hip.mla_fwd(q, cache, sm_scale=st["sm_scale"], v_dim=st["dv"], return_lse=True, **st["plan"])
+        ctx.save_for_backward(q, cache, o, lse)
+        ctx.st = st
+        return o
+
+    @staticmethod
+    def backward(ctx, dout):
+        q, cache, o, lse = ctx.saved_tensors
+        st = ctx.st
+        dq, dc = hip.mla_bwd(q, cache, o, dout.to(o.dtype), lse, sm_scale=st["sm_scale"], **st["plan"])
+        return dq, dc, None
+
+
+def _mla_latent(q, cache, *, mask, bias, sm_scale, v_dim):
+    """Absorbed ``mla`` for any query length, mask and bias (latent_attention.py:
+    79-197, 636-766), with the reference's gradient.  Latent widths up to 256
+    run the flash kernels with the latent as one shared K = V head (torch
+    autograd adds the dK and dV of that one tensor); 512 and 576 (bfloat16)
+    run the wide latent kernels.  A width between kernel ranks is zero-padded
+    (zero features change no score and add zero output columns)."""
+    B, l_q, H, R = q.shape
+    if q.dtype != cache.dtype:
+        raise ValueError(f"q and cache must share a dtype, got {q.dtype} and {cache.dtype}")
+    width = _latent_width(R, q.dtype)
+    if width is None:
+        raise ValueError(f"absorbed mla supports latent widths up to {FLASH_HEAD_DIMS_F32[-1]} in float32 and "
+                         f"{LATENT_WIDTHS[-1]} in bfloat16, got {R} ({q.dtype})")
+    if width <= FLASH_HEAD_DIMS[-1]:
+        c4 = cache[:, :, None, :]
+        e = _eligible(q, c4, c4, mask=mask, bias=bias, dropout_rate=0.0)
+        out = None if e is None else _run(q, c4, c4, e[0], e[1], sm_scale, False)
+        if out is None:
+            raise ValueError("the HIP latent-attention kernels cannot compute this call exactly: "
+                             + _unsupported_message(q, c4, mask, bias, 0.0))
+        return out if v_dim == R else out[..., :v_dim]
+    qp = q if width == R else _pad_features(q, width)
+    cp = cache if width == R else _pad_features(cache, width)
+    cp4 = cp[:, :, None, :]
+    e = _eligible(qp, cp4, cp4, mask=mask, bias=bias, dropout_rate=0.0)
+    plan = None if e is None else _flash_plan(qp, cp4, cp4, e[0], e[1], check_dim=False)
+    if plan is None:
+        raise ValueError("the HIP latent-attention kernels cannot compute this call exactly: "
+                         + _unsupported_message(qp, cp4, mask, bias, 0.0))
+    dvk = 512 if v_dim <= 512 else 576
+    st = dict(sm_scale=sm_scale, dv=dvk, plan=plan)
+    if not _needs_grad(q, cache):
+        with torch.no_grad():
+            out = hip.mla_fwd(qp, cp, sm_scale=sm_scale, v_dim=dvk, **plan)
+    else:
+        out = _LatentFunction.apply(qp, cp, st)
+    return out if v_dim == dvk else out[..., :v_dim]
 
 
 # ---------------------------------------------------------------------------
@@ -817,7 +940,7 @@ def _fold_low_rank(query, key, value, terms, sm_scale: float):
         q_extra.append(qf.to(query.device).expand(tuple(query.shape[:-1]) + (t.rank,)) * f)
         k_extra.append(kf.to(key.device).expand(tuple(key.shape[:-1]) + (t.rank,)) * f)
     extra = sum(x.shape[-1] for x in q_extra)
-    width = next((w for w in FLASH_HEAD_DIMS if w >= query.shape[-1] + extra), None)
+    width = _kernel_width(query.shape[-1] + extra, query.dtype)
     if width is None:
         return None
     pad = width - query.shape[-1] - extra

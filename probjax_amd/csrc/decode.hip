@@ -63,14 +63,6 @@ __device__ __forceinline__ int seq_len(const DecodeArgs& a, int b) {
   return L;
 }
 
-__device__ __forceinline__ float xor16_max(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-}
-__device__ __forceinline__ float xor16_sum(float x) {
-  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
 
 // Keeps the compiler from moving LDS accesses of one wave across this point;
 // the LDS itself executes one wave's accesses in program order.

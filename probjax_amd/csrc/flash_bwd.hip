@@ -1132,8 +1132,8 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: negative or zero size");
   if (q_heads % kv_heads != 0)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q_heads must be a multiple of kv_heads");
-  if (head_dim != 64 && head_dim != 128)
-    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128");
+  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype == PJX_DTYPE_BF16))
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128 (or 256 in bf16)");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sm_scale must be > 0");
   if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
@@ -1172,6 +1172,20 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
   ba.dbias = dbias;
   hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 256) {
+    // the 16-row / 16-key wide kernels, one head group per KV head (no partials)
+    WideBwdArgs wa;
+    wa.f = a;
+    wa.f.dv = 256;
+    wa.dout = dout;
+    wa.delta = ba.delta;
+    wa.lse2 = ba.lse2;
+    wa.dq = dq; wa.dk = dk; wa.dv = dv;
+    wa.dbias = dbias;
+    wa.part = nullptr;
+    wa.nsplit = 1;
+    return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
+  }
   const bool hb = bias != nullptr;
   const bool f32 = dtype == PJX_DTYPE_F32;
   return head_dim == 128 ? run_bwd<128>(ba, f32, hb, s) : run_bwd<64>(ba, f32, hb, s);

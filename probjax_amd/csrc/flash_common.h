@@ -23,6 +23,7 @@ struct FlashArgs {
   int q_valid, kv_valid, causal;
   float scale;
   int n_qtiles;
+  int dv;       // output row width (elements per head); the wide kernels' V width
   int ext;      // 0: none; 1: interval masks in `m`; 2: also segment ids / score modifiers
   ScoreMods m;
 };
@@ -39,10 +40,11 @@ struct BlockGeom {
   int kv_begin; // first key the block visits (a multiple of the key tile)
 };
 
-__device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) {
+// idx: the block's index in the (q tile, batch, head) grid (blockIdx.x unless
+// the grid carries a further factor).
+__device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a, int idx) {
   BlockGeom g;
   const int BH = a.B * a.Hq;
-  const int idx = blockIdx.x;
   const int bh = idx % BH;
   const int qt = a.n_qtiles - 1 - idx / BH;
   g.b = bh / a.Hq;
@@ -66,6 +68,8 @@ __device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) {
   g.kv_begin = 0;
   return g;
 }
+
+__device__ __forceinline__ BlockGeom block_geom(const FlashArgs& a) { return block_geom(a, blockIdx.x); }
 
 // With extended masks: the block's key range [kv_begin, kv_stop) from the
 // interval bounds of its first and last row (both bounds are monotone in the
@@ -156,6 +160,29 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who);
 // Launches the bf16 dense-bias kernel (flash_bias_ring.hip); returns a PJX_*
 // status.
 int launch_flash_bias_ring(int head_dim, const FlashArgs& a, hipStream_t stream);
+
+// Arguments of the wide-head backward kernels (flash_wide_bwd.hip).
+struct WideBwdArgs {
+  FlashArgs f;        // q, k, v, o (forward output), lse, masks, bias, sizes; f.dv = DV
+  const void* dout;   // dO [B, Lq, Hq, DV]
+  float* delta;       // workspace [B, Hq, Lq]
+  float* lse2;        // workspace [B, Hq, Lq]: lse * log2e
+  void* dq;           // [B, Lq, Hq, D]
+  void* dk;           // [B, Lk, Hkv, D]; with the shared latent dC [B, Lk, D]
+  void* dv;           // [B, Lk, Hkv, DV] (separate K / V only)
+  float* dbias;       // [B, Hq, Lq, Lk] fp32 dL/d(bias) or null
+  float* part;        // [nsplit][B][Lk][Hkv][D (+ DV)] fp32 partials when nsplit > 1
+  int nsplit;         // query-head groups per KV head in the dK/dV kernel
+};
+
+// Runs the wide backward (dQ, then dK/dV or the latent's dC, then the partial
+// sum when nsplit > 1); returns a PJX_* status.
+int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who);
+
+// Wide-head bf16 forward kernels (flash_wide.hip): D = 256 with separate K/V,
+// and the absorbed latent (K = V, rank 512 / 576, output width a.dv).
+int launch_flash_wide256(FlashArgs& a, hipStream_t stream);
+int launch_mla_wide(FlashArgs& a, int rank, hipStream_t stream);
 
 }  // namespace pjx
 

@@ -928,31 +928,47 @@ static int launch_split(K kernel, const FlashArgs& a, hipStream_t stream) {
 
 using namespace pjx;
 
-extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
-                             float* lse, const int32_t* kv_lengths, const float* bias,
-                             int64_t bias_batch, int64_t bias_heads, int64_t batch,
-                             int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
-                             int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
-                             float sm_scale, const pjx_score_mods* mods, void* stream) {
-  clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
-  if (!q || !k || !v || !o) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: q, k, v, o must be non-null");
-  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: negative or zero size");
-  if (q_heads % kv_heads != 0)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: q_heads must be a multiple of kv_heads");
-  if (head_dim != 64 && head_dim != 128)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128");
-  if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: sm_scale must be > 0");
-  if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: bias must be [1|B, 1|Hq, Lq, Lk]");
-  const int64_t elems = batch * q_len * q_heads * head_dim;
-  if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30))
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: sizes out of range");
-  if (batch == 0 || q_len == 0) return PJX_OK;
-
-  FlashArgs a;
+// Checks the arguments shared by pjx_flash_fwd and pjx_mla_fwd and fills the
+// argument block; returns PJX_OK, or an error (message set).  *empty is set
+// when there is nothing to compute.
+static int make_flash_args(FlashArgs& a, const char* who, const void* q, const void* k,
+                           const void* v, void* o, float* lse, const int32_t* kv_lengths,
+                           const float* bias, int64_t bias_batch, int64_t bias_heads, int64_t batch,
+                           int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                           int64_t head_dim, int64_t v_dim, int64_t q_valid, int64_t kv_valid,
+                           int causal, float sm_scale, const pjx_score_mods* mods, bool* empty) {
+  char buf[256];
+  *empty = false;
+  if (!q || !k || !v || !o) {
+    snprintf(buf, sizeof(buf), "%s: input and output pointers must be non-null", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0) {
+    snprintf(buf, sizeof(buf), "%s: negative or zero size", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (q_heads % kv_heads != 0) {
+    snprintf(buf, sizeof(buf), "%s: q_heads must be a multiple of kv_heads", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (!(sm_scale > 0.f)) {
+    snprintf(buf, sizeof(buf), "%s: sm_scale must be > 0", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads))) {
+    snprintf(buf, sizeof(buf), "%s: bias must be [1|B, 1|Hq, Lq, Lk]", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  const int64_t elems = batch * q_len * q_heads * std::max(head_dim, v_dim);
+  if (elems > (int64_t)1 << 40 || q_len > (1 << 30) || kv_len > (1 << 30) ||
+      kv_len * kv_heads * head_dim * 2 > ((int64_t)1 << 40)) {
+    snprintf(buf, sizeof(buf), "%s: sizes out of range", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  if (batch == 0 || q_len == 0) {
+    *empty = true;
+    return PJX_OK;
+  }
   a.q = q; a.k = k; a.v = v; a.o = o; a.lse = lse;
   a.kv_lengths = kv_lengths;
   a.bias = bias;
@@ -965,12 +981,34 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   a.causal = causal ? 1 : 0;
   a.scale = sm_scale;
   a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
-  if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: grid too large");
-  const int mrc = lower_score_mods(mods, a, "pjx_flash_fwd");
-  if (mrc != PJX_OK) return mrc;
+  a.dv = (int)v_dim;
+  if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL) {
+    snprintf(buf, sizeof(buf), "%s: grid too large", who);
+    return fail(PJX_ERR_INVALID, buf);
+  }
+  return lower_score_mods(mods, a, who);
+}
+
+extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
+                             float* lse, const int32_t* kv_lengths, const float* bias,
+                             int64_t bias_batch, int64_t bias_heads, int64_t batch,
+                             int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                             int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
+                             float sm_scale, const pjx_score_mods* mods, void* stream) {
+  clear_error();
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
+  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype == PJX_DTYPE_BF16))
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128 (or 256 in bf16)");
+  FlashArgs a;
+  bool empty;
+  int rc = make_flash_args(a, "pjx_flash_fwd", q, k, v, o, lse, kv_lengths, bias, bias_batch,
+                           bias_heads, batch, q_len, kv_len, q_heads, kv_heads, head_dim, head_dim,
+                           q_valid, kv_valid, causal, sm_scale, mods, &empty);
+  if (rc != PJX_OK || empty) return rc;
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
+  if (head_dim == 256) return launch_flash_wide256(a, s);
   if (a.ext) {
     // Extended masks / score modifiers: the one-pass kernels' EXT variants
     // (1: interval masks, 2: segment ids / score modifiers as well).
@@ -1013,4 +1051,31 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   }
   if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true, 0>, a, s) : launch(flash_fwd_f32_kernel<128, false, 0>, a, s);
   return hb ? launch(flash_fwd_f32_kernel<64, true, 0>, a, s) : launch(flash_fwd_f32_kernel<64, false, 0>, a, s);
+}
+
+extern "C" int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o, float* lse,
+                           const int32_t* kv_lengths, const float* bias, int64_t bias_batch,
+                           int64_t bias_heads, int64_t batch, int64_t q_len, int64_t kv_len,
+                           int64_t heads, int64_t rank, int64_t v_dim, int64_t q_valid,
+                           int64_t kv_valid, int causal, float sm_scale,
+                           const pjx_score_mods* mods, void* stream) {
+  clear_error();
+  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_mla_fwd: dtype must be PJX_DTYPE_BF16");
+  const bool wide = (rank == 576 && (v_dim == 512 || v_dim == 576)) || (rank == 512 && v_dim == 512);
+  const bool narrow = (rank == 64 || rank == 128 || rank == 256) && v_dim == rank;
+  if (!wide && !narrow)
+    return fail(PJX_ERR_INVALID,
+                "pjx_mla_fwd: (rank, v_dim) must be (576, 512), (576, 576), (512, 512) or rank in "
+                "{64, 128, 256} with v_dim == rank");
+  if (narrow)  // the latent as one shared K = V head of the flash kernels
+    return pjx_flash_fwd(dtype, q, cache, cache, o, lse, kv_lengths, bias, bias_batch, bias_heads,
+                         batch, q_len, kv_len, heads, 1, rank, q_valid, kv_valid, causal, sm_scale,
+                         mods, stream);
+  FlashArgs a;
+  bool empty;
+  int rc = make_flash_args(a, "pjx_mla_fwd", q, cache, cache, o, lse, kv_lengths, bias, bias_batch,
+                           bias_heads, batch, q_len, kv_len, heads, 1, rank, v_dim, q_valid,
+                           kv_valid, causal, sm_scale, mods, &empty);
+  if (rc != PJX_OK || empty) return rc;
+  return launch_mla_wide(a, (int)rank, (hipStream_t)stream);
 }

@@ -1,0 +1,768 @@
+// Flash-attention backward for wide heads on gfx950 (MI355X), bf16: D = 256,
+// and the absorbed latent of probjax's `mla` (K = V = one shared latent row of
+// R = 512 or 576 values per key, Hkv = 1, output width DV <= R).
+//
+// probjax differentiates absorbed `mla` through the materialised computation
+// (kernels/latent_attention.py:752-766): `mha` over K = V = the latent
+// broadcast to every head, so the cache gradient is the sum over heads of
+// dK + dV.  The math is the flash backward's (flash_bwd.hip; probjax
+// attention.py:853-1160): delta = sum_d o*do, p = exp2(s*log2e - lse*log2e),
+// ds = p (do.v^T - delta) sm_scale, dq = sum_k bf16(ds) k,
+// dk = sum_q bf16(ds)^T q, dv = sum_q bf16(p)^T do, fp32 accumulation.
+//
+// At these widths a wave cannot hold 32 rows of Q^T and dO^T and a 32-row dQ
+// accumulator (1.5 K registers at R = 576), so both kernels put 16 rows (or
+// 16 keys) on each wave and use v_mfma_f32_16x16x32_bf16:
+//   A lane l holds A[l%16][8*(l/16) + j], B lane l holds B[8*(l/16) + j][l%16],
+//   C register r of lane l is C[4*(l/16) + r][l%16].
+// Writing c = l%16 and qd = l/16:
+//   wide_bwd_dq_kernel -- one workgroup per (64-query tile, batch, head); a wave
+//     owns rows qw + c.  K (and V) tiles of 32 keys stream HBM -> LDS.
+//     S^T = K Q^T and dP^T = V dO^T (keys on the MFMA rows, so register r of
+//     block kb is key k0 + 16kb + 4qd + r of the lane's row); with the shared
+//     latent one K-fragment read feeds both products.  dQ^T += K^T dS^T takes
+//     dS^T from registers as the B operand (k slot 8qd + j <-> key
+//     16(j/4) + 4qd + j%4) and K^T from transposing LDS reads in that key
+//     order.  It writes delta and lse*log2e for the second kernel.
+//   wide_bwd_dkdv_kernel -- one workgroup per (64-key tile, batch, KV head,
+//     head group); a wave owns keys kw + c with K^T (and V^T) in registers.
+//     Q and dO tiles of 32 rows stream through LDS.  S = Q K^T, dP = dO V^T
+//     (rows on the MFMA rows), then dK^T += Q^T dS and dV^T += dO^T P with
+//     Q^T / dO^T from transposing reads.  With the shared latent both land in
+//     one accumulator (dC = dK + dV).  A KV head's query heads are split into
+//     groups over workgroups when one group per head-tile would leave the chip
+//     idle (MQA: 16 heads over one latent); each group writes an fp32 partial
+//     and wide_bwd_reduce_kernel sums them in a fixed order (deterministic).
+//
+// LDS rows are row-major [row][dim] with 16-byte chunks XOR-swizzled within
+// aligned groups of G chunks so that both read patterns of the 16x16 layout
+// are free of bank conflicts: 16 lanes reading one chunk of 16 consecutive
+// rows (b128 row fragments), and 32 lanes reading a 32-byte chunk pair of 8
+// consecutive rows (transposing reads).  Rows of whole 256-byte bank lines
+// (D = 256, 512; G = 16): swz(r) = 2(r&7) + ((r>>3)&1).  Rows of an odd
+// number of half lines (D = 576; G = 8), odd rows starting half a line later:
+// swz(r) = 2((r>>1)&3) + ((r>>3)&1).
+#include "flash_common.h"
+
+namespace pjx {
+
+constexpr int kWQ = 64;   // query rows per dQ workgroup (16 per wave)
+constexpr int kWK = 64;   // keys per dK/dV workgroup (16 per wave)
+constexpr int kWT = 32;   // rows (keys) per streamed LDS tile
+
+template <int D>
+struct Row16 {
+  static constexpr int ROWB = 2 * D;
+  static constexpr int NC = D / 8;
+  static constexpr bool FULL_LINES = (ROWB % 256) == 0;
+  static constexpr int G = FULL_LINES ? 16 : 8;
+  static constexpr int TILE_B = kWT * ROWB;
+  static constexpr int NLD = kWT * NC / 256;  // 1 KiB loads per wave per tile
+  static_assert(ROWB % 256 == 0 || ROWB % 256 == 128, "rows of whole or half bank lines");
+  static_assert(NC % G == 0 && (kWT * NC) % 256 == 0, "tile shape");
+  __device__ static int swz(int r) {
+    return FULL_LINES ? (((r & 7) << 1) | ((r >> 3) & 1)) : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
+  }
+};
+
+// Per-lane LDS offsets of one tile layout's two read patterns.
+template <int D>
+struct Offs16 {
+  using R = Row16<D>;
+  static constexpr int PR = R::G / 4;  // period (in 32-dim steps) of row reads
+  static constexpr int PT = R::G / 2;  // period (in 16-dim blocks) of transposing reads
+  uint32_t row[PR];  // A = X[16 rows][32 dims]: row c, chunk 4*st + qd
+  uint32_t tr[PT];   // A = X^T[16 dims][32 rows]: rows 4qd + s/4 (+16), dims 16i + 4(s%4)
+  uint32_t voff[R::NLD];  // buffer->LDS sources: unit p = (NLD*w + j)*64 + lane
+  __device__ void init(int lane, int w, uint32_t rowstride) {
+    const int c = lane & 15, qd = lane >> 4;
+#pragma unroll
+    for (int e = 0; e < PR; ++e) row[e] = c * R::ROWB + 16 * ((4 * e + qd) ^ R::swz(c));
+    const int rl = 4 * qd + (c >> 2), b = (c & 3) >> 1;
+#pragma unroll
+    for (int e = 0; e < PT; ++e) tr[e] = rl * R::ROWB + 16 * ((2 * e + b) ^ R::swz(rl)) + 8 * (c & 1);
+#pragma unroll
+    for (int j = 0; j < R::NLD; ++j) {
+      const int p = (R::NLD * w + j) * 64 + lane, r = p / R::NC, slot = p % R::NC;
+      voff[j] = r * rowstride + 16 * (slot ^ R::swz(r));
+    }
+  }
+  // Row fragment of 32-dim step st, rows 16*rb .. +15 of the tile.
+  __device__ bf16x8 rows(const unsigned char* tile, int rb, int st) const {
+    return as_bf16x8(*(const u32x4*)(tile + 16 * rb * R::ROWB + 16 * R::G * (st / PR) + row[st % PR]));
+  }
+  // Transposed fragment of dims 16i .. +15 over the tile's 32 rows in k-slot
+  // order (slot 8qd + j <-> row 16(j/4) + 4qd + j%4).
+  __device__ bf16x8 trans(const unsigned char* tile, int i) const {
+    const unsigned char* p = tile + 16 * R::G * (i / PT) + tr[i % PT];
+    const u32x2 lo = lds_read_tr16(p);
+    const u32x2 hi = lds_read_tr16(p + 16 * R::ROWB);
+    const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+    return as_bf16x8(v);
+  }
+  // Copies rows [r0, r0 + n) (n >= 1) of a global tensor with row stride
+  // `rowstride` into a tile; rows past n read as zero.
+  __device__ void load(unsigned char* tile, const unsigned char* base, uint32_t rowstride, int n, int w) const {
+    const uint32_t bytes = (uint32_t)(n - 1) * rowstride + R::ROWB;
+    const rsrc_t rs = make_rsrc(base, bytes);
+#pragma unroll
+    for (int j = 0; j < R::NLD; ++j) buffer_load_lds16(rs, tile + (R::NLD * w + j) * 1024, voff[j]);
+  }
+};
+
+// Two f32x4 C blocks (k slots j < 4 from a, j >= 4 from b) as a bf16 B operand.
+__device__ __forceinline__ bf16x8 pack_slots(const f32x4& a, const f32x4& b) {
+  const u32x4 pk = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
+                    pack_bf16x2(b[2], b[3])};
+  return as_bf16x8(pk);
+}
+
+__device__ __forceinline__ float bf16_lo16(uint32_t x) { return __uint_as_float(x << 16); }
+__device__ __forceinline__ float bf16_hi16(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+
+// ---------------------------------------------------------------------------
+// dQ (and delta, lse*log2e): one workgroup per (64-query tile, batch, head).
+// ---------------------------------------------------------------------------
+template <int D, int DV, bool SHARED, int BIAS, int EXT>
+__global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba) {
+  // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
+  constexpr bool HB = BIAS != 0, DB = BIAS == 2;
+  const FlashArgs& a = ba.f;
+  using OK = Offs16<D>;
+  using OV = Offs16<DV>;
+  constexpr int KT_B = Row16<D>::TILE_B;
+  constexpr int STAGE_B = SHARED ? KT_B : KT_B + Row16<DV>::TILE_B;
+  constexpr int KS = D / 32, VS = DV / 32, ND = D / 16;
+  static_assert(!SHARED || DV <= D, "values are a prefix of the latent row");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, qd = lane >> 4;
+  const int BH = a.B * a.Hq;
+  const int n_qt = (a.Lq + kWQ - 1) / kWQ;
+  const int bh = (int)blockIdx.x % BH;
+  const int qt = n_qt - 1 - (int)blockIdx.x / BH;  // heaviest causal tile first
+  const int b = bh / a.Hq, h = bh % a.Hq, hkv = h / (a.Hq / a.Hkv);
+  const int q0 = qt * kWQ;
+  const int qw = __builtin_amdgcn_readfirstlane(q0 + 16 * w);
+  const int qi = qw + c;
+  const int q_hi = min(a.Lq, a.q_valid);
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  const bool row_in = qi < a.Lq, row_ok = qi < q_hi;
+  // keys this block visits: [kv_begin, kv_stop)
+  int kv_begin = 0, kv_stop = kv_end;
+  if (q0 >= q_hi) {
+    kv_stop = 0;
+  } else if constexpr (EXT > 0) {
+    int lo0, hi0, lo1, hi1;
+    row_bounds(a.m, a.causal, b, kv_end, q_hi, q0, lo0, hi0);
+    row_bounds(a.m, a.causal, b, kv_end, q_hi, min(q0 + kWQ, q_hi) - 1, lo1, hi1);
+    kv_begin = (max(lo0, 0) / kWT) * kWT;
+    kv_stop = max(min(hi1 + 1, kv_end), 0);
+  } else if (a.causal) {
+    kv_stop = min(kv_stop, min(q0 + kWQ, q_hi));
+  }
+  // this lane's key interval and the wave's (extended masks)
+  int lo = 0, hi = -1, lo_first = 0, hi_last = -1, segq = 0;
+  HeadMods hm = {0.f, 1.f};
+  if constexpr (EXT > 0) {
+    int t0, t1;
+    row_bounds(a.m, a.causal, b, kv_end, q_hi, qi, lo, hi);
+    row_bounds(a.m, a.causal, b, kv_end, q_hi, qw, lo_first, t0);
+    row_bounds(a.m, a.causal, b, kv_end, q_hi, min(qw + 15, q_hi - 1), t1, hi_last);
+    if (a.m.seg_q && row_in) segq = a.m.seg_q[(size_t)b * a.Lq + qi];
+    hm = head_mods(a.m, h);
+  }
+  const bool wave_any_row = qw < q_hi;
+
+  // Q^T, dO^T as B operands (lane: row qi, dims 32*st + 8*qd + [0,8)) and
+  // delta = sum_d o*do over the DV output dims.
+  bf16x8 qf[KS], dof[VS];
+  float dsum = 0.f;
+  {
+    const uint16_t* qrow = (const uint16_t*)a.q + ((size_t)(b * a.Lq + (row_in ? qi : 0)) * a.Hq + h) * D;
+    const size_t ooff = ((size_t)(b * a.Lq + (row_in ? qi : 0)) * a.Hq + h) * DV;
+    const uint16_t* drow = (const uint16_t*)ba.dout + ooff;
+    const uint16_t* orow = (const uint16_t*)a.o + ooff;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      u32x4 r = {0u, 0u, 0u, 0u};
+      if (row_in) r = *(const u32x4*)(qrow + 32 * st + 8 * qd);
+      qf[st] = as_bf16x8(r);
+    }
+#pragma unroll
+    for (int st = 0; st < VS; ++st) {
+      u32x4 rd = {0u, 0u, 0u, 0u}, ro = rd;
+      if (row_in) {
+        rd = *(const u32x4*)(drow + 32 * st + 8 * qd);
+        ro = *(const u32x4*)(orow + 32 * st + 8 * qd);
+      }
+      dof[st] = as_bf16x8(rd);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dsum = fmaf(bf16_lo16(ro[j]), bf16_lo16(rd[j]), fmaf(bf16_hi16(ro[j]), bf16_hi16(rd[j]), dsum));
+    }
+  }
+  const float delta = xor32_sum(xor16_sum(dsum));
+  float lse2 = 0.f;
+  const size_t lidx = ((size_t)b * a.Hq + h) * a.Lq + qi;
+  if (row_in) {
+    lse2 = a.lse[lidx] * kLog2e;
+    if (qd == 0) {
+      ba.delta[lidx] = delta;
+      ba.lse2[lidx] = lse2;
+    }
+  }
+  const float* brow = nullptr;
+  if constexpr (HB)
+    brow = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride + (size_t)(row_in ? qi : 0) * a.Lk;
+  const float cx = (HB || EXT == 2) ? kLog2e : a.scale * kLog2e;
+  const uint32_t rowstride = (uint32_t)a.Hkv * 2 * D;  // K / V rows (Hkv heads of D dims)
+  const uint32_t vrowstride = (uint32_t)a.Hkv * 2 * DV;
+  const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)b * a.Lk * a.Hkv + hkv) * (2 * D);
+  const unsigned char* Vb = (const unsigned char*)a.v + ((size_t)b * a.Lk * a.Hkv + hkv) * (2 * DV);
+
+  OK ok;
+  ok.init(lane, w, rowstride);
+  OV ov;
+  if constexpr (!SHARED) ov.init(lane, w, vrowstride);
+
+  f32x4 acc[ND];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) acc[i] = f32x4{};
+
+  const int t_begin = kv_begin / kWT;
+  const int n_tiles = max((kv_stop + kWT - 1) / kWT - t_begin, 0);
+
+  auto issue = [&](int t, unsigned char* st) {
+    const int k0 = (t_begin + t) * kWT;
+    const int n = min(kWT, kv_stop - k0);
+    ok.load(st, Kb + (size_t)k0 * rowstride, rowstride, n, w);
+    if constexpr (!SHARED) ov.load(st + KT_B, Vb + (size_t)k0 * vrowstride, vrowstride, n, w);
+  };
+
+  auto compute = [&](int t, const unsigned char* ks) {
+    const int k0 = (t_begin + t) * kWT;
+    if constexpr (EXT > 0) {
+      if (!wave_any_row || k0 > hi_last || k0 + kWT - 1 < lo_first) return;
+    } else {
+      if (!wave_any_row || (a.causal && k0 > qw + 15)) return;
+    }
+    const unsigned char* vs = ks + KT_B;
+    // s[kb][r] = S^T[key k0 + 16kb + 4qd + r][row qi]; dp likewise.
+    f32x4 s[2], dp[2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      s[kb] = f32x4{};
+      dp[kb] = f32x4{};
+#pragma unroll
+      for (int st = 0; st < KS; ++st) {
+        const bf16x8 kf = ok.rows(ks, kb, st);
+        s[kb] = mfma16x16x32(kf, qf[st], s[kb]);
+        if constexpr (SHARED) {
+          if (st < VS) dp[kb] = mfma16x16x32(kf, dof[st], dp[kb]);
+        }
+      }
+      if constexpr (!SHARED) {
+#pragma unroll
+        for (int st = 0; st < VS; ++st) dp[kb] = mfma16x16x32(ov.rows(vs, kb, st), dof[st], dp[kb]);
+      }
+    }
+    f32x4 dbv[2];
+    const int kbase = k0 + 4 * qd;
+    if constexpr (EXT == 2) {
+      const bool soft = a.m.softcap > 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int kk = kbase + 16 * kb;
+        f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+        if constexpr (HB) {
+          if (row_in) bv = ((a.Lk & 3) == 0) ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+        }
+        int4 sg = {0, 0, 0, 0};
+        if (a.m.seg_k) sg = seg4(a.m.seg_k, b, kk, a.Lk);
+        const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int kj = kk + r;
+          float gg;
+          const float raw = s[kb][r] * a.scale;
+          const float x = soft ? modify_score<true>(a.m, hm, raw, bv[r], qi, kj, gg)
+                               : modify_score<false>(a.m, hm, raw, bv[r], qi, kj, gg);
+          const bool keep = kj >= lo && kj <= hi &&
+                            (!a.m.seg_q || (a.m.seg_lt ? kj < segq : sgv[r] == segq));
+          const float p = keep ? fast_exp2(fmaf(x, cx, -lse2)) : 0.f;
+          const float tt = p * (dp[kb][r] - delta);
+          if constexpr (DB) dbv[kb][r] = tt;
+          s[kb][r] = tt * a.scale * gg;
+        }
+      }
+    } else {
+      if constexpr (HB) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int kk = kbase + 16 * kb;
+          f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+          if (row_in) bv = ((a.Lk & 3) == 0) ? load_bias4<true>(brow, kk, a.Lk) : load_bias4<false>(brow, kk, a.Lk);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) s[kb][r] = fmaf(s[kb][r], a.scale, bv[r]);
+        }
+      }
+      const bool need_mask = (k0 + kWT > kv_end) || (a.causal && k0 + kWT - 1 > qw) || (qw + 15 >= q_hi);
+      if (need_mask) {
+        int lim = kv_end - 1 - kbase;
+        if (a.causal) lim = min(lim, qi - kbase);
+        if (!row_ok) lim = -1;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (16 * kb + r > lim) s[kb][r] = -INFINITY;
+      }
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
+          const float tt = p * (dp[kb][r] - delta);
+          if constexpr (DB) dbv[kb][r] = tt;
+          s[kb][r] = tt * a.scale;
+        }
+    }
+    if constexpr (DB) {
+      if (row_in) {
+        float* row = ba.dbias + (((size_t)b * a.Hq + h) * a.Lq + qi) * a.Lk;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          const int kk = kbase + 16 * kb;
+          if ((a.Lk & 3) == 0 && kk + 3 < a.Lk) {
+            *(f32x4*)(row + kk) = dbv[kb];
+          } else {
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (kk + r < a.Lk) row[kk + r] = dbv[kb][r];
+          }
+        }
+      }
+    }
+    // dQ^T[16i + 4qd + r][row] += K^T dS^T
+    const bf16x8 dsb = pack_slots(s[0], s[1]);
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acc[i] = mfma16x16x32(ok.trans(ks, i), dsb, acc[i]);
+  };
+
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
+  }
+
+  if (row_in) {
+    uint16_t* drow = (uint16_t*)ba.dq + ((size_t)(b * a.Lq + qi) * a.Hq + h) * D;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      u32x2 pk;
+      pk[0] = pack_bf16x2(acc[i][0], acc[i][1]);
+      pk[1] = pack_bf16x2(acc[i][2], acc[i][3]);
+      *(u32x2*)(drow + 16 * i + 4 * qd) = pk;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dK, dV (or dC = dK + dV of the shared latent): one workgroup per (64-key
+// tile, batch, KV head, query-head group).
+// ---------------------------------------------------------------------------
+template <int D, int DV, bool SHARED, bool BIAS, int EXT>
+__global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  using OQ = Offs16<D>;
+  using OD = Offs16<DV>;
+  constexpr int QT_B = Row16<D>::TILE_B, DT_B = Row16<DV>::TILE_B;
+  // lse*log2e and delta of the tile's rows, one 64-float slot each (the
+  // 4-byte buffer->LDS load writes one float per lane; lanes 32..63 fill the
+  // unused upper half)
+  constexpr int SMALL_B = 2 * 64 * 4;
+  constexpr int STAGE_B = QT_B + DT_B + SMALL_B;
+  constexpr int KS = D / 32, VS = DV / 32, ND = D / 16, NV = DV / 16;
+  static_assert(!SHARED || DV <= D, "values are a prefix of the latent row");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, qd = lane >> 4;
+  const int nsplit = ba.nsplit;
+  const int split = (int)blockIdx.x % nsplit;
+  const int rest = (int)blockIdx.x / nsplit;
+  const int BH = a.B * a.Hkv;
+  const int bh = rest % BH;
+  const int k0 = (rest / BH) * kWK;
+  const int b = bh / a.Hkv, hkv = bh % a.Hkv;
+  const int G = a.Hq / a.Hkv;
+  const int gs = G / nsplit;              // query heads of this group
+  const int h_first = hkv * G + split * gs;
+  const int kw = __builtin_amdgcn_readfirstlane(k0 + 16 * w);
+  const int key = kw + c;
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  const int q_hi = min(a.Lq, a.q_valid);
+  // query rows that can see a key of this tile: [q_begin, q_end)
+  int q_begin = a.causal ? (k0 / kWT) * kWT : 0;
+  int q_end = q_hi;
+  int qlo = 0, qhi = q_hi - 1, wq_first = 0, wq_last = q_hi - 1, segk = 0;
+  if constexpr (EXT > 0) {
+    q_end = q_begin = 0;
+    if (k0 < kv_end) {
+      int a0, a1, b0, b1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, k0, a0, a1);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(k0 + kWK, kv_end) - 1, b0, b1);
+      q_begin = (max(a0, 0) / kWT) * kWT;
+      q_end = b1 + 1;
+    }
+    key_bounds(a.m, a.causal, b, kv_end, q_hi, key, qlo, qhi);
+    if (kw < kv_end) {
+      int t0, t1;
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, kw, wq_first, t0);
+      key_bounds(a.m, a.causal, b, kv_end, q_hi, min(kw + 16, kv_end) - 1, t1, wq_last);
+    }
+    if (a.m.seg_k && key < a.Lk) segk = a.m.seg_k[(size_t)b * a.Lk + key];
+  }
+  const int n_qt = (k0 < kv_end && q_end > q_begin) ? (q_end - q_begin + kWT - 1) / kWT : 0;
+  const int n_tiles = gs * n_qt;
+
+  // K^T (and V^T) as B operands: lane holds key `key`, dims 32*st + 8*qd + [0,8).
+  bf16x8 kf[KS], vf[SHARED ? 1 : VS];
+  {
+    const bool kin = key < a.Lk;
+    const uint16_t* krow = (const uint16_t*)a.k + ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * D;
+    const uint16_t* vrow = (const uint16_t*)a.v + ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * DV;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      u32x4 r = {0u, 0u, 0u, 0u};
+      if (kin) r = *(const u32x4*)(krow + 32 * st + 8 * qd);
+      kf[st] = as_bf16x8(r);
+    }
+    if constexpr (!SHARED) {
+#pragma unroll
+      for (int st = 0; st < VS; ++st) {
+        u32x4 r = {0u, 0u, 0u, 0u};
+        if (kin) r = *(const u32x4*)(vrow + 32 * st + 8 * qd);
+        vf[st] = as_bf16x8(r);
+      }
+    }
+  }
+  const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
+  const uint32_t qrowstride = (uint32_t)a.Hq * 2 * D;
+  const uint32_t drowstride = (uint32_t)a.Hq * 2 * DV;
+  OQ oq;
+  oq.init(lane, w, qrowstride);
+  OD od;
+  od.init(lane, w, drowstride);
+
+  f32x4 acck[ND], accv[SHARED ? 1 : NV];
+#pragma unroll
+  for (int i = 0; i < ND; ++i) acck[i] = f32x4{};
+  if constexpr (!SHARED) {
+#pragma unroll
+    for (int i = 0; i < NV; ++i) accv[i] = f32x4{};
+  }
+
+  auto tile_head = [&](int t) { return h_first + t / n_qt; };
+  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * kWT; };
+
+  auto issue = [&](int t, unsigned char* st) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    const int n = max(min(kWT, a.Lq - q0), 1);
+    oq.load(st, (const unsigned char*)a.q + ((size_t)(b * a.Lq + q0) * a.Hq + h) * (2 * D), qrowstride, n, w);
+    od.load(st + QT_B, (const unsigned char*)ba.dout + ((size_t)(b * a.Lq + q0) * a.Hq + h) * (2 * DV),
+            drowstride, n, w);
+    if (w < 2) {
+      const size_t loff = ((size_t)b * a.Hq + h) * a.Lq + q0;
+      const rsrc_t rl = make_rsrc((w == 0 ? ba.lse2 : ba.delta) + loff, (uint32_t)n * 4);
+      buffer_load_lds4(rl, st + QT_B + DT_B + w * 256, 4 * (lane & 31));
+    }
+  };
+
+  auto compute = [&](int t, const unsigned char* st) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    if (kw >= kv_end || q0 >= q_hi) return;
+    if constexpr (EXT > 0) {
+      if (q0 > wq_last || q0 + kWT - 1 < wq_first) return;
+    } else {
+      if (a.causal && q0 + kWT - 1 < kw) return;  // every row before the wave's first key
+    }
+    const unsigned char* qs = st;
+    const unsigned char* dos = st + QT_B;
+    const float* lsm = (const float*)(st + QT_B + DT_B);
+    const float* dlm = lsm + 64;
+    // sx[rb][r] = S[row q0 + 16rb + 4qd + r][key]; dpx likewise.
+    f32x4 sx[2], dpx[2];
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      sx[rb] = f32x4{};
+      dpx[rb] = f32x4{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) sx[rb] = mfma16x16x32(oq.rows(qs, rb, s), kf[s], sx[rb]);
+#pragma unroll
+      for (int s = 0; s < VS; ++s)
+        dpx[rb] = mfma16x16x32(od.rows(dos, rb, s), SHARED ? kf[s] : vf[s], dpx[rb]);
+    }
+    const float* bbase = nullptr;
+    if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
+    HeadMods hm = {0.f, 1.f};
+    if constexpr (EXT == 2) hm = head_mods(a.m, h);
+    const bool soft = EXT == 2 && a.m.softcap > 0.f;
+#pragma unroll
+    for (int rb = 0; rb < 2; ++rb) {
+      const int q4 = q0 + 16 * rb + 4 * qd;
+      const f32x4 l4 = *(const f32x4*)(lsm + 16 * rb + 4 * qd);
+      const f32x4 d4 = *(const f32x4*)(dlm + 16 * rb + 4 * qd);
+      int4 sg = {0, 0, 0, 0};
+      if (EXT == 2 && a.m.seg_q) sg = seg4(a.m.seg_q, b, q4, a.Lq);
+      const int sgv[4] = {sg.x, sg.y, sg.z, sg.w};
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int qr = q4 + r;
+        float bv = 0.f;
+        if constexpr (BIAS) bv = (qr < a.Lq && key < a.Lk) ? bbase[(size_t)qr * a.Lk + key] : 0.f;
+        float x, gg = 1.f;
+        bool keep;
+        if constexpr (EXT == 2) {
+          const float raw = sx[rb][r] * a.scale;
+          x = soft ? modify_score<true>(a.m, hm, raw, bv, qr, key, gg) : modify_score<false>(a.m, hm, raw, bv, qr, key, gg);
+          keep = qr >= qlo && qr <= qhi && (!a.m.seg_q || (a.m.seg_lt ? key < sgv[r] : sgv[r] == segk));
+        } else {
+          x = BIAS ? fmaf(sx[rb][r], a.scale, bv) : sx[rb][r];
+          keep = key < kv_end && qr < q_hi && (!a.causal || qr >= key);
+        }
+        const float p = keep ? fast_exp2(fmaf(x, cx, -l4[r])) : 0.f;
+        sx[rb][r] = p;
+        dpx[rb][r] = p * (dpx[rb][r] - d4[r]) * a.scale * gg;
+      }
+    }
+    const bf16x8 pb = pack_slots(sx[0], sx[1]);
+    const bf16x8 dsb = pack_slots(dpx[0], dpx[1]);
+    // dK^T[16i + 4qd + r][key] += Q^T dS;  dV^T += dO^T P (into dK^T with the latent)
+#pragma unroll
+    for (int i = 0; i < ND; ++i) acck[i] = mfma16x16x32(oq.trans(qs, i), dsb, acck[i]);
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+      if constexpr (SHARED)
+        acck[i] = mfma16x16x32(od.trans(dos, i), pb, acck[i]);
+      else
+        accv[i] = mfma16x16x32(od.trans(dos, i), pb, accv[i]);
+    }
+  };
+
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
+  }
+
+  if (key >= a.Lk) return;
+  const size_t krow = (size_t)(b * a.Lk + key) * a.Hkv + hkv;
+  if (nsplit == 1) {
+    uint16_t* dkrow = (uint16_t*)ba.dk + krow * D;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) {
+      const u32x2 pk = {pack_bf16x2(acck[i][0], acck[i][1]), pack_bf16x2(acck[i][2], acck[i][3])};
+      *(u32x2*)(dkrow + 16 * i + 4 * qd) = pk;
+    }
+    if constexpr (!SHARED) {
+      uint16_t* dvrow = (uint16_t*)ba.dv + krow * DV;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const u32x2 pv = {pack_bf16x2(accv[i][0], accv[i][1]), pack_bf16x2(accv[i][2], accv[i][3])};
+        *(u32x2*)(dvrow + 16 * i + 4 * qd) = pv;
+      }
+    }
+  } else {
+    // fp32 partial of this head group: [split][B*Lk*Hkv][D] then (separate
+    // K / V) [split][B*Lk*Hkv][DV] after all K partials.
+    const size_t nrows = (size_t)a.B * a.Lk * a.Hkv;
+    float* pk = ba.part + ((size_t)split * nrows + krow) * D;
+#pragma unroll
+    for (int i = 0; i < ND; ++i) *(f32x4*)(pk + 16 * i + 4 * qd) = acck[i];
+    if constexpr (!SHARED) {
+      float* pv = ba.part + (size_t)nsplit * nrows * D + ((size_t)split * nrows + krow) * DV;
+#pragma unroll
+      for (int i = 0; i < NV; ++i) *(f32x4*)(pv + 16 * i + 4 * qd) = accv[i];
+    }
+  }
+}
+
+// Sums the head-group partials in split order and rounds to bf16:
+// out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
+__global__ __launch_bounds__(256) void wide_bwd_reduce_kernel(const float* part, int nsplit, size_t n,
+                                                                uint16_t* out) {
+  const size_t e = 4 * ((size_t)blockIdx.x * 256 + threadIdx.x);
+  if (e >= n) return;
+  f32x4 acc = *(const f32x4*)(part + e);
+  for (int s = 1; s < nsplit; ++s) acc += *(const f32x4*)(part + (size_t)s * n + e);
+  const u32x2 pk = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+  *(u32x2*)(out + e) = pk;
+}
+
+// ---------------------------------------------------------------------------
+// Launch.
+// ---------------------------------------------------------------------------
+size_t wide_bwd_workspace(int64_t B, int64_t Hq, int64_t Lq, int64_t Lk, int64_t Hkv, int64_t D,
+                          int64_t DV, int nsplit, bool shared) {
+  size_t bytes = 8 * (size_t)B * Hq * Lq;
+  bytes = (bytes + 255) & ~(size_t)255;
+  if (nsplit > 1) bytes += (size_t)nsplit * B * Lk * Hkv * (D + (shared ? 0 : DV)) * 4;
+  return bytes;
+}
+
+// Query-head groups per KV head for the dK/dV kernel: split the group (into
+// a divisor of G) until the grid holds about 512 workgroups, two per CU of an
+// MI355X.  A function of the shapes only, so that the workspace size is known
+// without a device.
+int wide_bwd_nsplit(int64_t B, int64_t Lk, int64_t Hq, int64_t Hkv) {
+  const int64_t G = Hq / Hkv;
+  const int64_t base = ((Lk + kWK - 1) / kWK) * B * Hkv;
+  int ns = 1;
+  while (base * ns < 512 && ns < G) {
+    int next = ns + 1;
+    while (next <= G && G % next) ++next;
+    if (next > G) break;
+    ns = next;
+  }
+  return ns;
+}
+
+template <int D, int DV, bool SHARED>
+static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
+  const FlashArgs& a = ba.f;
+  const bool hb = a.bias != nullptr, db = ba.dbias != nullptr, ext = a.ext != 0;
+  const long dq_blocks = (long)((a.Lq + kWQ - 1) / kWQ) * a.B * a.Hq;
+  const long kv_blocks = (long)((a.Lk + kWK - 1) / kWK) * a.B * a.Hkv * ba.nsplit;
+  if (dq_blocks > 0x7fffffffL || kv_blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "wide backward: grid too large");
+  const dim3 blk(kThreads);
+#define PJX_DQ(BI, EX) hipLaunchKernelGGL((wide_bwd_dq_kernel<D, DV, SHARED, BI, EX>), dim3((unsigned)dq_blocks), blk, 0, s, ba)
+  if (ext) {
+    if (db) PJX_DQ(2, 2); else if (hb) PJX_DQ(1, 2); else PJX_DQ(0, 2);
+  } else {
+    if (db) PJX_DQ(2, 0); else if (hb) PJX_DQ(1, 0); else PJX_DQ(0, 0);
+  }
+#undef PJX_DQ
+  int rc = check_launch(who);
+  if (rc != PJX_OK) return rc;
+  if (kv_blocks > 0) {
+#define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
+    if (ext) {
+      if (hb) PJX_KV(true, 2); else PJX_KV(false, 2);
+    } else {
+      if (hb) PJX_KV(true, 0); else PJX_KV(false, 0);
+    }
+#undef PJX_KV
+    rc = check_launch(who);
+    if (rc != PJX_OK) return rc;
+  }
+  if (ba.nsplit > 1) {
+    const size_t nk = (size_t)a.B * a.Lk * a.Hkv * D;
+    hipLaunchKernelGGL(wide_bwd_reduce_kernel, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
+                       (const float*)ba.part, ba.nsplit, nk, (uint16_t*)ba.dk);
+    if constexpr (!SHARED) {
+      const size_t nv = (size_t)a.B * a.Lk * a.Hkv * DV;
+      hipLaunchKernelGGL(wide_bwd_reduce_kernel, dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
+                         (const float*)(ba.part + (size_t)ba.nsplit * nk), ba.nsplit, nv, (uint16_t*)ba.dv);
+    }
+    rc = check_launch(who);
+  }
+  return rc;
+}
+
+int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
+  if (!shared && D == 256 && DV == 256) return run_wide_bwd_t<256, 256, false>(ba, s, who);
+  if (shared && D == 576 && DV == 512) return run_wide_bwd_t<576, 512, true>(ba, s, who);
+  if (shared && D == 576 && DV == 576) return run_wide_bwd_t<576, 576, true>(ba, s, who);
+  if (shared && D == 512 && DV == 512) return run_wide_bwd_t<512, 512, true>(ba, s, who);
+  return fail(PJX_ERR_INVALID, "wide backward: unsupported head widths");
+}
+
+}  // namespace pjx
+
+using namespace pjx;
+
+extern "C" size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64_t q_len,
+                                             int64_t kv_len, int64_t rank) {
+  if (batch <= 0 || heads <= 0 || q_len < 0 || kv_len < 0 || rank <= 0) return 0;
+  return wide_bwd_workspace(batch, heads, q_len, kv_len, 1, rank, 0,
+                            wide_bwd_nsplit(batch, kv_len, heads, 1), true);
+}
+
+extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const void* o,
+                           const void* dout, const float* lse, void* dq, void* dcache,
+                           void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
+                           const float* bias, int64_t bias_batch, int64_t bias_heads, int64_t batch,
+                           int64_t q_len, int64_t kv_len, int64_t heads, int64_t rank,
+                           int64_t v_dim, int64_t q_valid, int64_t kv_valid, int causal,
+                           float sm_scale, const pjx_score_mods* mods, void* stream) {
+  clear_error();
+  const char* who = "pjx_mla_bwd";
+  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_mla_bwd: dtype must be PJX_DTYPE_BF16");
+  if (!((rank == 576 && (v_dim == 512 || v_dim == 576)) || (rank == 512 && v_dim == 512)))
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: (rank, v_dim) must be (576, 512), (576, 576) or (512, 512)");
+  if (!q || !cache || !o || !dout || !lse || !dq || !dcache)
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: q, cache, o, dout, lse, dq, dcache must be non-null");
+  if (batch < 0 || q_len < 0 || kv_len < 0 || heads <= 0)
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: negative or zero size");
+  if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_mla_bwd: sm_scale must be > 0");
+  if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == heads)))
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: bias must be [1|B, 1|H, Lq, S]");
+  if (batch * q_len * heads * rank > ((int64_t)1 << 40) || q_len > (1 << 30) || kv_len > (1 << 30) ||
+      batch * kv_len * rank * 4 * heads > ((int64_t)1 << 46))
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: sizes out of range");
+  if (batch == 0 || (q_len == 0 && kv_len == 0)) return PJX_OK;
+  const int nsplit = wide_bwd_nsplit(batch, kv_len, heads, 1);
+  const size_t need = wide_bwd_workspace(batch, heads, q_len, kv_len, 1, rank, 0, nsplit, true);
+  if (!workspace || workspace_bytes < need)
+    return fail(PJX_ERR_WORKSPACE, "pjx_mla_bwd: workspace missing or smaller than pjx_mla_bwd_workspace_size()");
+  WideBwdArgs ba;
+  FlashArgs& a = ba.f;
+  a.q = q; a.k = cache; a.v = cache; a.o = const_cast<void*>(o); a.lse = const_cast<float*>(lse);
+  a.kv_lengths = kv_lengths;
+  a.bias = bias;
+  a.bias_hstride = (bias && bias_heads != 1) ? q_len * kv_len : 0;
+  a.bias_bstride = (bias && bias_batch != 1) ? bias_heads * q_len * kv_len : 0;
+  a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len;
+  a.Hq = (int)heads; a.Hkv = 1;
+  a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
+  a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
+  a.causal = causal ? 1 : 0;
+  a.scale = sm_scale;
+  a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
+  a.dv = (int)v_dim;
+  const int mrc = lower_score_mods(mods, a, who);
+  if (mrc != PJX_OK) return mrc;
+  ba.dout = dout;
+  ba.delta = (float*)workspace;
+  ba.lse2 = ba.delta + batch * heads * q_len;
+  ba.part = (float*)((unsigned char*)workspace + ((8 * (size_t)batch * heads * q_len + 255) & ~(size_t)255));
+  ba.nsplit = nsplit;
+  ba.dq = dq;
+  ba.dk = dcache;
+  ba.dv = nullptr;
+  ba.dbias = nullptr;
+  return run_wide_bwd(ba, (int)rank, (int)v_dim, true, (hipStream_t)stream, who);
+}

@@ -131,8 +131,8 @@ def flash_attention_fwd(
         raise ValueError("q, k, v must share a dtype")
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128):
-        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if D not in (64, 128) and not (D == 256 and q.dtype == torch.bfloat16):
+        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     code = _dtype_code(q)
@@ -186,8 +186,8 @@ def flash_attention_bwd(
     code = _dtype_code(q)
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128):
-        raise ValueError(f"head_dim {D} not supported (64 or 128)")
+    if D not in (64, 128) and not (D == 256 and q.dtype == torch.bfloat16):
+        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))
@@ -295,6 +295,94 @@ def mla_decode(
     )
     native.check(rc)
     return (o, lse) if return_lse else o
+
+
+def mla_fwd(
+    q, cache, *, sm_scale: float, v_dim: int | None = None, causal: bool = False, kv_lengths=None,
+    bias=None, q_valid: int | None = None, kv_valid: int | None = None, return_lse: bool = False,
+    mods: ScoreModsArgs | None = None,
+):
+    """``pjx_mla_fwd``: absorbed latent attention ``q [B, Lq, H, R]`` over
+    ``cache [B, S, R]`` (K = V = cache) -> ``o [B, Lq, H, v_dim]`` (the first
+    ``v_dim`` columns; ``None`` = R), any query length, with the masks, bias
+    and modifiers of ``flash_attention_fwd`` (bias ``[1|B, 1|H, Lq, S]``)."""
+    dev = _on_device(q, cache, bias)
+    if q.ndim != 4 or cache.ndim != 3:
+        raise ValueError("q must be [B, Lq, H, R] and cache [B, S, R]")
+    B, Lq, H, R = q.shape
+    if cache.shape[0] != B or cache.shape[2] != R:
+        raise ValueError(f"incompatible shapes q {tuple(q.shape)}, cache {tuple(cache.shape)}")
+    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
+        raise ValueError("the latent flash kernel takes bfloat16 q and cache")
+    dv = R if v_dim is None else int(v_dim)
+    S = cache.shape[1]
+    if not sm_scale > 0:
+        raise ValueError("sm_scale must be > 0")
+    q, cache = q.contiguous(), cache.contiguous()
+    bb = bh = 1
+    if bias is not None:
+        if bias.ndim != 4 or tuple(bias.shape[-2:]) != (Lq, S):
+            raise ValueError(f"bias must be [1|B, 1|H, {Lq}, {S}], got {tuple(bias.shape)}")
+        bb, bh = bias.shape[:2]
+        if bb not in (1, B) or bh not in (1, H):
+            raise ValueError(f"bias {tuple(bias.shape)} does not broadcast to B={B}, H={H}")
+        bias = bias.to(torch.float32).contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    ms = _mods_struct(mods, B, Lq, S, H, dev)
+    o = torch.empty((B, Lq, H, dv), dtype=torch.bfloat16, device=dev)
+    lse = torch.empty((B, H, Lq), dtype=torch.float32, device=dev) if return_lse else None
+    rc = native.load().pjx_mla_fwd(
+        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(o), _ptr(lse), _ptr(L), _ptr(bias), bb, bh,
+        B, Lq, S, H, R, dv, Lq if q_valid is None else int(q_valid), S if kv_valid is None else int(kv_valid),
+        int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
+    )
+    native.check(rc)
+    return (o, lse) if return_lse else o
+
+
+def mla_bwd(
+    q, cache, o, do, lse, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
+    q_valid: int | None = None, kv_valid: int | None = None, mods: ScoreModsArgs | None = None,
+    workspace=None,
+):
+    """``pjx_mla_bwd``: ``(dq, dcache)`` of ``mla_fwd`` (absorbed latent, bf16,
+    rank 512 / 576).  ``o`` / ``do`` are the forward output and its gradient
+    ``[B, Lq, H, v_dim]``, ``lse`` the forward's natural-log LSE ``[B, H, Lq]``;
+    masks, bias and scale must be the forward's."""
+    dev = _on_device(q, cache, o, do, lse, bias)
+    if q.ndim != 4 or cache.ndim != 3:
+        raise ValueError("q must be [B, Lq, H, R] and cache [B, S, R]")
+    B, Lq, H, R = q.shape
+    S = cache.shape[1]
+    dv = o.shape[-1]
+    if cache.shape[0] != B or cache.shape[2] != R or tuple(o.shape) != (B, Lq, H, dv) or do.shape != o.shape:
+        raise ValueError("incompatible shapes for the latent backward")
+    if tuple(lse.shape) != (B, H, Lq):
+        raise ValueError(f"lse must be [B, H, Lq] = {(B, H, Lq)}")
+    if not all(t.dtype == torch.bfloat16 for t in (q, cache, o, do)):
+        raise ValueError("the latent backward takes bfloat16 q, cache, o, do")
+    q, cache, o, do = (t.contiguous() for t in (q, cache, o, do))
+    lse = lse.to(torch.float32).contiguous()
+    bb = bh = 1
+    if bias is not None:
+        if bias.ndim != 4 or tuple(bias.shape[-2:]) != (Lq, S):
+            raise ValueError(f"bias must be [1|B, 1|H, {Lq}, {S}], got {tuple(bias.shape)}")
+        bb, bh = bias.shape[:2]
+        bias = bias.to(torch.float32).contiguous()
+    L = _lengths(kv_lengths, B, dev)
+    ms = _mods_struct(mods, B, Lq, S, H, dev)
+    lib = native.load()
+    ws = _workspace(int(lib.pjx_mla_bwd_workspace_size(B, H, Lq, S, R)), dev, workspace)
+    dq = torch.empty_like(q)
+    dc = torch.empty_like(cache)
+    rc = lib.pjx_mla_bwd(
+        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dc),
+        _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, S, H, R, dv,
+        Lq if q_valid is None else int(q_valid), S if kv_valid is None else int(kv_valid),
+        int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
+    )
+    native.check(rc)
+    return dq, dc
 
 
 def mla_project(cache, wk, wv, *, width: int):

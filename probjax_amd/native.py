@@ -69,6 +69,17 @@ _SIGNATURES = {
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64, _I64, _I64,
          _I64, _I64, ctypes.c_float, _I64, _P],
     ),
+    "pjx_mla_fwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         _I64, _I64, ctypes.c_int, ctypes.c_float, _MODS, _P],
+    ),
+    "pjx_mla_bwd_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64, _I64, _I64]),
+    "pjx_mla_bwd": (
+        ctypes.c_int,
+        [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P, _P, _I64, _I64, _I64,
+         _I64, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _MODS, _P],
+    ),
     "pjx_mla_project": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _P],

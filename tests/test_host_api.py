@@ -86,8 +86,13 @@ def test_use_splitkv_only_for_exact_cases():
 
 
 def test_kernel_width_and_padding():
-    assert [A._kernel_width(d) for d in (1, 32, 64, 65, 96, 128, 129, 256)] == [64, 64, 64, 128, 128, 128, None,
-                                                                                 None]
+    ds = (1, 32, 64, 65, 96, 128, 129, 256, 257)
+    assert [A._kernel_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
+    assert [A._kernel_width(d, torch.float32) for d in ds] == [64, 64, 64, 128, 128, 128, None, None, None]
+    assert [A._decode_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, None, None, None]
+    assert [A._latent_width(r, torch.bfloat16) for r in (100, 200, 300, 512, 513, 576, 577)] == \
+        [128, 256, 512, 512, 576, 576, None]
+    assert [A._latent_width(r, torch.float32) for r in (100, 200, 576)] == [128, None, None]
     x = torch.randn(2, 3, 4, 40, requires_grad=True)
     y = A._pad_features(x, 64)
     assert y.shape == (2, 3, 4, 64) and torch.equal(y[..., :40], x) and not y[..., 40:].any()
