@@ -20,6 +20,9 @@ and ``C2FB`` forward + backward, both as TFLOP/s with the reference
 benchmark's FlashAttention convention (fwd+bwd = 3.5x the forward's FLOPs).
 ``C5P`` is the materialised-MLA up-projection alone (``pjx_mla_project``) and
 ``C5M`` a materialised-MLA causal prefill (projection + flash forward).
+``C5A`` is the absorbed-MLA causal prefill (``pjx_mla_fwd``, B=1, L=4096,
+H=16, R=576, 512 value columns) and ``C5AB`` its backward (``pjx_mla_bwd``);
+``C2W`` a head-dim-256 causal forward.
 
 ``cpu_baseline`` times the numpy restatement of probjax's XLA CPU path
 (``oracle.xla_attention``, 256x256 tiles with causal tile skipping) on one
@@ -294,8 +297,69 @@ def make_c5m(dev, gen):
                 kernel="mla_project_bf16_kernel + flash_fwd_bf16_pipe_kernel<128,64,2>")
 
 
+def _latent_prefill_inputs(dev, gen):
+    import torch
+
+    B, L, H, R, DV = 1, 4096, 16, 576, 512
+    q = _randn((B, L, H, R), gen, dev, torch.bfloat16)
+    cache = _randn((B, L, R), gen, dev, torch.bfloat16)
+    return B, L, H, R, DV, q, cache
+
+
+def make_c5a(dev, gen):
+    """Absorbed latent attention, causal prefill (mla(q, cache, mask=CausalMask())
+    sliced to the 512 value columns, as the config-5 harness uses it):
+    pjx_mla_fwd.  FLOPs by the reference convention, 2 * (R + DV) per
+    (query row, head, visible key): the scores over the 576-wide latent and
+    P.V over its first 512 columns; the kernel forms each score twice (once per
+    256-column half of the output), which is not counted."""
+    from probjax_amd.hip_attention import mla_fwd
+
+    B, L, H, R, DV, q, cache = _latent_prefill_inputs(dev, gen)
+    flop = 2 * B * H * L * L / 2 * (R + DV)
+    nbytes = B * L * H * R * 2 + B * L * R * 2 + B * L * H * DV * 2
+    fn = lambda: mla_fwd(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, causal=True)  # noqa: E731
+    return dict(name="MLA absorbed causal prefill bf16 B=1 L=4096 H=16 R=576 Dv=512", fn=fn, flop=flop,
+                bytes=nbytes, bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<576,256,32,true,false,0>")
+
+
+def make_c5ab(dev, gen):
+    """Backward of C5A (pjx_mla_bwd: dq and the cache gradient).  FLOPs: the
+    five products per visible (row, key) pair -- scores (R) and dP (DV)
+    recomputed, dQ (R), dK (R), dV (DV) -- at 2 FLOPs per multiply-add."""
+    import torch
+    from probjax_amd.hip_attention import mla_bwd, mla_fwd
+
+    B, L, H, R, DV, q, cache = _latent_prefill_inputs(dev, gen)
+    sc = 1 / math.sqrt(192)
+    o, lse = mla_fwd(q, cache, sm_scale=sc, v_dim=DV, causal=True, return_lse=True)
+    do = _randn(tuple(o.shape), gen, dev, torch.bfloat16)
+    flop = 2 * B * H * L * L / 2 * (3 * R + 2 * DV)
+    nbytes = 2 * B * L * H * R * 2 + 2 * B * L * R * 2 + 2 * B * L * H * DV * 2
+    fn = lambda: mla_bwd(q, cache, o, do, lse, sm_scale=sc, causal=True)  # noqa: E731
+    return dict(name="MLA absorbed causal prefill backward bf16 B=1 L=4096 H=16 R=576 Dv=512 (dq, dcache)",
+                fn=fn, flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
+                kernel="wide_bwd_dq_kernel<576,512,true,0,0> + wide_bwd_dkdv_kernel<576,512,true,false,0> + wide_bwd_reduce_kernel")
+
+
+def make_c2w(dev, gen):
+    """Head dim 256 causal flash forward (the widest head the reference's fused
+    route takes), B=2, H=16, L=4096."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 2, 4096, 16, 256
+    q, k, v = (_randn((B, L, H, D), gen, dev, torch.bfloat16) for _ in range(3))
+    flop = 4 * B * H * L * L * D / 2
+    nbytes = 4 * B * L * H * D * 2
+    fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
+    return dict(name="causal fwd bf16 B=2 H=16 L=4096 D=256", fn=fn, flop=flop, bytes=nbytes,
+                bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<256,256,32,false,false,0>")
+
+
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
-          "C2B": make_c2b, "C2FB": make_c2fb, "C5P": make_c5p, "C5M": make_c5m}
+          "C2B": make_c2b, "C2FB": make_c2fb, "C5P": make_c5p, "C5M": make_c5m,
+          "C5A": make_c5a, "C5AB": make_c5ab, "C2W": make_c2w}
 
 
 def _settle(fn, seconds):
