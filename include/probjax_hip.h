@@ -7,8 +7,9 @@
  * duration of the call; nothing is cached across calls.  `stream` is a
  * hipStream_t passed as void* (NULL = the default stream).  Every entry point
  * only enqueues work on `stream`: no device synchronisation, no host<->device
- * copies, no allocation.  Entry points are reentrant; the only global state is
- * a thread-local error string.
+ * copies, no allocation.  Entry points are reentrant; the global state is a
+ * thread-local error string, plus, for pjx_splitkv_decode_static only, one
+ * library-held device array per GPU and its looked-up address.
  *
  * Layout conventions are probjax's: q [B, Lq, Hq, D], k/v [B, Lk, Hkv, D]
  * row-major (D fastest), query head h uses KV head h / (Hq / Hkv)
@@ -197,6 +198,29 @@ int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
                        size_t workspace_bytes, int64_t batch, int64_t q_len,
                        int64_t kv_len, int64_t q_heads, int64_t kv_heads,
                        int64_t head_dim, float sm_scale, int64_t chunk, void* stream);
+
+/*
+ * Size of the library-held device array behind pjx_splitkv_decode_static:
+ * 32 MiB on each GPU the library runs on, held until the process ends.
+ */
+#define PJX_DECODE_STATIC_SCRATCH_BYTES (32u << 20)
+
+/*
+ * pjx_splitkv_decode without a workspace argument: the partials go to the
+ * library's own device array of PJX_DECODE_STATIC_SCRATCH_BYTES per GPU, and
+ * nothing is allocated.  No counterpart in the reference: an extra entry for
+ * callers that cannot allocate (code under HIP graph capture, serving loops,
+ * harnesses that forbid hipMalloc).  Arguments, results and errors as
+ * pjx_splitkv_decode; sizes whose partials
+ * (pjx_decode_workspace_size(batch, kv_heads, rows, kv_len, head_dim, chunk))
+ * exceed the array are rejected with PJX_ERR_WORKSPACE.  Every call on one GPU
+ * shares that GPU's array: calls that overlap on one GPU (concurrent streams
+ * or threads) race and must be serialised by the caller.
+ */
+int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const void* v,
+                              const int32_t* kv_lengths, void* o, float* lse, int64_t batch,
+                              int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
+                              int64_t head_dim, float sm_scale, int64_t chunk, void* stream);
 
 /*
  * Latent (MLA) attention decode, absorbed form K = V = cache.  Replaces the

@@ -21,6 +21,10 @@
 //     softmax redundantly, and multiplies its own share of the output dims:
 //     O^T[d][row] += V^T P^T, with V^T read as one 16-byte LDS load per step;
 //   * the merge kernel combines the chunks of one (batch, group) exactly.
+#include <stdio.h>
+
+#include <atomic>
+
 #include "pjx_common.h"
 #include "pjx_internal.h"
 
@@ -807,6 +811,69 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 128) return run_decode(gqa_decode_kernel<128>, a, workspace, workspace_bytes, s, "pjx_splitkv_decode");
   return run_decode(gqa_decode_kernel<64>, a, workspace, workspace_bytes, s, "pjx_splitkv_decode");
+}
+
+// ---------------------------------------------------------------------------
+// Split-KV decode without allocation: the partials live in `scratch`, a
+// library-held device array (one copy per GPU, kept until the process ends),
+// for callers that cannot allocate (graph capture, serving loops).  Every call
+// on a GPU shares that GPU's array: calls that overlap on one GPU race.  No
+// part of it needs clearing: the chunk kernel writes every partial the merge
+// reads in the same call.
+// ---------------------------------------------------------------------------
+constexpr size_t kScratchBytes = (size_t)PJX_DECODE_STATIC_SCRATCH_BYTES;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kMaxDevices = 64;
+static std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's `scratch` (the name itself is only a
+// host-side stand-in), looked up on the first call on each device.
+static int scratch_ptr(void** out, const char* who) {
+  char buf[256];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    snprintf(buf, sizeof(buf), "%s: no usable current device (%s)", who, hipGetErrorString(e));
+    return fail(PJX_ERR_LAUNCH, buf);
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (!p) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p) {
+      snprintf(buf, sizeof(buf), "%s: hipGetSymbolAddress(scratch) failed: %s", who, hipGetErrorString(e));
+      return fail(PJX_ERR_LAUNCH, buf);
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return PJX_OK;
+}
+
+extern "C" int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const void* v,
+                                         const int32_t* kv_lengths, void* o, float* lse,
+                                         int64_t batch, int64_t q_len, int64_t kv_len,
+                                         int64_t q_heads, int64_t kv_heads, int64_t head_dim,
+                                         float sm_scale, int64_t chunk, void* stream) {
+  clear_error();
+  const char* who = "pjx_splitkv_decode_static";
+  if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
+    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode_static: bad sizes");
+  if (batch == 0) return PJX_OK;
+  const int64_t c = chunk == 0 ? auto_chunk(batch, kv_heads, kv_len, kGqaItems) : chunk;
+  if (c <= 0) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode_static: chunk must be a positive multiple of 128");
+  const size_t need = ws_size(batch, kv_heads, (q_heads / kv_heads) * q_len, kv_len, head_dim, c);
+  if (need > kScratchBytes) {
+    char buf[256];
+    snprintf(buf, sizeof(buf), "%s: these sizes need %zu bytes of partials, more than the %zu-byte "
+             "scratch the library holds; call pjx_splitkv_decode with a workspace", who, need, kScratchBytes);
+    return fail(PJX_ERR_WORKSPACE, buf);
+  }
+  void* ws = nullptr;
+  const int rc = scratch_ptr(&ws, who);
+  if (rc != PJX_OK) return rc;
+  return pjx_splitkv_decode(dtype, q, k, v, kv_lengths, o, lse, ws, kScratchBytes, batch, q_len, kv_len,
+                            q_heads, kv_heads, head_dim, sm_scale, c, stream);
 }
 
 extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,

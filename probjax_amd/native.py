@@ -16,6 +16,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libprobjax_hip.so"
 PJX_DTYPE_F32 = 0
 PJX_DTYPE_BF16 = 1
 PJX_OK = 0
+PJX_DECODE_STATIC_SCRATCH_BYTES = 32 << 20  # include/probjax_hip.h
 
 
 
@@ -63,6 +64,11 @@ _SIGNATURES = {
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64, _I64, _I64,
          _I64, _I64, ctypes.c_float, _I64, _P],
+    ),
+    "pjx_splitkv_decode_static": (
+        ctypes.c_int,
+        [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
+         _I64, _P],
     ),
     "pjx_mla_decode": (
         ctypes.c_int,
