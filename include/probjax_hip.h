@@ -183,11 +183,13 @@ size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
  * 43-250) and extends it with the per-sequence KVLenMask that the reference
  * routes to the regular forward (kernels/attention.py:2672-2675).
  *
- * q [B, Lq, Hq, D] bf16; k, v [B, Lk, Hkv, D] bf16 (Lk = KV capacity);
- * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, D] bf16;
+ * dtype PJX_DTYPE_BF16 or PJX_DTYPE_F32 (full fp32 products) for q, k, v, o:
+ * q [B, Lq, Hq, D]; k, v [B, Lk, Hkv, D] (Lk = KV capacity);
+ * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, D];
  * lse optional fp32 [B, Hq, Lq], natural log (attention_splitkv.py:248-250).
  * The (Hq/Hkv)*Lq query rows of a KV head are packed row = g*Lq + t
- * (attention_splitkv.py:121-126); at most 16 rows per KV head.
+ * (attention_splitkv.py:121-126); at most 64 rows per KV head in bf16 (the
+ * reference packs up to 64, :155-170), 32 in fp32.
  * Only keys < kv_lengths[b] are read.  head_dim == 128.
  * chunk: keys per work item (0 = automatic: a power of two in [128, 2048]
  *   leaving about 2048 items at full capacity; else a multiple of 128).

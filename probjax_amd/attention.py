@@ -51,7 +51,9 @@ FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 only
 FLASH_HEAD_DIMS_F32 = (64, 128)
 DECODE_HEAD_DIMS = (64, 128)
 LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (bfloat16)
-DECODE_MAX_ROWS = 16
+DECODE_MAX_ROWS = 64       # (Hq/Hkv)*Lq rows per KV head of the bf16 split-KV decode
+DECODE_MAX_ROWS_F32 = 32   # ... of the fp32 split-KV decode
+MLA_DECODE_MAX_ROWS = 16   # Lq*H folded rows of the latent decode
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
 BACKWARD_DTYPES = (torch.bfloat16, torch.float32)  # dtypes pjx_flash_bwd takes
 
@@ -123,13 +125,18 @@ def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
     """Arguments of the split-KV decode for this call, or None."""
     if lb is not None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return None
-    if query.dtype != torch.bfloat16:
+    if query.dtype not in (torch.bfloat16, torch.float32):
         return None
     B, l_q, h_q, d = query.shape
     h_kv = key.shape[2]
-    if d not in DECODE_HEAD_DIMS or (h_q // h_kv) * l_q > DECODE_MAX_ROWS:
+    if d not in DECODE_HEAD_DIMS or (h_q // h_kv) * l_q > _decode_max_rows(query.dtype):
         return None
     return dict(kv_lengths=lm.kv_lengths)
+
+
+def _decode_max_rows(dtype) -> int:
+    """Packed query rows per KV head the split-KV decode takes in ``dtype``."""
+    return DECODE_MAX_ROWS if dtype == torch.bfloat16 else DECODE_MAX_ROWS_F32
 
 
 def _int_tensor(x, shape, device):
@@ -279,9 +286,10 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return False
-    if q.dtype != torch.bfloat16 or _decode_width(q.shape[-1]) is None:
+    if q.dtype not in (torch.bfloat16, torch.float32) or _decode_width(q.shape[-1]) is None:
         return False
-    if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or (q.shape[2] // k.shape[2]) * q.shape[1] > DECODE_MAX_ROWS:
+    if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or \
+            (q.shape[2] // k.shape[2]) * q.shape[1] > _decode_max_rows(q.dtype):
         return False
     if split_kv:
         return True
@@ -607,7 +615,7 @@ def _mla_absorbed_lengths(q, cache, wk, wv, mask, bias):
         return None
     if not (q.dtype == cache.dtype == wk.dtype == wv.dtype == torch.bfloat16):
         return None
-    if (R, R) not in MLA_SHAPES or l_q * H > DECODE_MAX_ROWS:
+    if (R, R) not in MLA_SHAPES or l_q * H > MLA_DECODE_MAX_ROWS:
         return None
     if not _absorbed_cheaper(l_q, cache.shape[1], R, dk, dv):
         return None
@@ -728,7 +736,7 @@ def _latent_decode_lengths(q, cache, mask, bias, dv):
         return None
     if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
         return None
-    if (R, dv) not in MLA_SHAPES or l_q * H > DECODE_MAX_ROWS:
+    if (R, dv) not in MLA_SHAPES or l_q * H > MLA_DECODE_MAX_ROWS:
         return None
     lm = lower_mask(mask)
     if lm is None:

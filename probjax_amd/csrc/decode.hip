@@ -35,11 +35,12 @@ constexpr int kTile = 64;       // keys per latent tile (16 per wave)
 constexpr int kRows = 16;       // query rows per MFMA column block
 
 struct DecodeArgs {
-  const uint16_t* q;
+  const uint16_t* q;   // bf16 (fp32 decode: the same pointers hold floats)
   const uint16_t* k;
   const uint16_t* v;
   const int32_t* lengths;
-  uint16_t* o;
+  uint16_t* o;         // bf16 output, or null with o32
+  float* o32;          // fp32 output of the fp32 decode, else null
   float* lse;
   float* ws_o;   // [B*G][nch][rows][dv] unnormalised partial outputs
   float* ws_ml;  // [B*G][nch][rows][2]  running max (log2 units), sum
@@ -86,7 +87,11 @@ __device__ __forceinline__ void emit_row_elem(const DecodeArgs& a, int b, int g,
     int t, h;
     row_to_head(a, g, r, t, h);
     const float out = Ls > 0.f ? O / Ls : 0.f;
-    a.o[((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + d] = __builtin_bit_cast(uint16_t, (__bf16)out);
+    const size_t oi = ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + d;
+    if (a.o32)
+      a.o32[oi] = out;
+    else
+      a.o[oi] = __builtin_bit_cast(uint16_t, (__bf16)out);
     if (a.lse && d == 0)
       a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : INFINITY;
   } else {
@@ -182,8 +187,13 @@ __device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g,
     int t, h;
     row_to_head(a, g, r, t, h);
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-    const u32x2 pk = {pack_bf16x2(O[0] * inv, O[1] * inv), pack_bf16x2(O[2] * inv, O[3] * inv)};
-    *(u32x2*)(a.o + ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + d) = pk;
+    const size_t oi = ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + d;
+    if (a.o32) {
+      *(f32x4*)(a.o32 + oi) = O * inv;
+    } else {
+      const u32x2 pk = {pack_bf16x2(O[0] * inv, O[1] * inv), pack_bf16x2(O[2] * inv, O[3] * inv)};
+      *(u32x2*)(a.o + oi) = pk;
+    }
     if (a.lse && d == 0)
       a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : INFINITY;
   } else {
@@ -199,19 +209,64 @@ __device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g,
 // GQA split-KV decode.  One workgroup = one (chunk, batch, kv group) work
 // item; its 4 waves split the chunk's keys into contiguous quarters and run
 // independent online softmaxes (no block barrier inside the key loop), then
-// combine their (max, sum, O) in LDS.  Per iteration a wave takes 32 keys:
+// combine their (max, sum, O) in LDS.  The rows = (Hq/Hkv)*Lq query rows of
+// the KV head are NRB blocks of 16 MFMA columns (up to 64 rows, the
+// reference's largest packed tile, attention_splitkv.py:155-170).  Per
+// iteration a wave takes 32 keys:
 //   * K rows are loaded straight into the A operand of
 //     v_mfma_f32_16x16x32_bf16 (lane: key l%16, 16 bytes of dims), S^T = K Q^T
-//     with the G*Lq query rows as the 16 MFMA columns;
+//     for each row block;
 //   * V rows are loaded 4 keys x 8 dims per lane, packed with v_perm into
 //     [dim][key] order and written to a wave-private LDS slab, from which the
-//     A operand of O^T += V^T P^T is two 8-byte reads;
+//     A operand of O^T += V^T P^T is two 8-byte reads, shared by the row
+//     blocks;
 //   * the next iteration's K and V loads are issued before this iteration's
 //     softmax and P.V, so HBM traffic overlaps the arithmetic.
 // Keys at or past the sequence length are never read.
 // ---------------------------------------------------------------------------
+
+// Combines the 4 waves' (max, sum, O^T) of row block rb through LDS scratch
+// red (>= 4 x 16 x D floats + 4 x 16 x 2) and emits rows 16rb .. of the item.
+// acc[i] holds O^T[dim 16i + 4*q4 + r][row 16rb + c16].
 template <int D>
-__global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
+__device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, const f32x4* acc,
+                                             float m_run, float l_run, int rb, int b, int g,
+                                             size_t part, bool final_out) {
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  float* red_o = red;                  // [4][16 rows][D]
+  float* red_ml = red_o + 4 * 16 * D;  // [4][16 rows][2]
+  __syncthreads();  // the scratch is free (every wave is done with it)
+#pragma unroll
+  for (int db = 0; db < D / 16; ++db)
+    *(f32x4*)(red_o + (w * 16 + c16) * D + 16 * db + 4 * q4) = acc[db];
+  if (q4 == 0) {
+    red_ml[(w * 16 + c16) * 2] = m_run;
+    red_ml[(w * 16 + c16) * 2 + 1] = l_run;
+  }
+  __syncthreads();
+  const int nr = min(16, a.rows - 16 * rb);
+  for (int e = tid; e < nr * D; e += 256) {
+    const int r = e / D, d = e % D;
+    float M = kMaxInit;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, red_ml[(ww * 16 + r) * 2]);
+    float Ls = 0.f, O = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < 4; ++ww) {
+      const float wt = fast_exp2(red_ml[(ww * 16 + r) * 2] - M);
+      Ls = fmaf(wt, red_ml[(ww * 16 + r) * 2 + 1], Ls);
+      O = fmaf(wt, red_o[(ww * 16 + r) * D + d], O);
+    }
+    emit_row_elem(a, b, g, 16 * rb + r, d, part, final_out, M, Ls, O);
+  }
+}
+
+template <int NRB>
+constexpr int decode_occupancy() { return NRB == 4 ? 1 : 2; }
+
+template <int D, int NRB>
+__global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int KSTEPS = D / 32;  // 32-dim MFMA k-steps of Q.K
   constexpr int NDB = D / 16;     // 16-dim output blocks
   constexpr int DC = D / 8;       // 16-byte chunks per row
@@ -235,17 +290,19 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
   const int w0 = c0 + w * per_wave;
   const int w1 = min(w0 + per_wave, L);
 
-  bf16x8 qf[KSTEPS];
-  {
-    const bool rv = c16 < a.rows;
+  bf16x8 qf[NRB][KSTEPS];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    const int row = 16 * rb + c16;
+    const bool rv = row < a.rows;
     int t = 0, h = 0;
-    if (rv) row_to_head(a, g, c16, t, h);
+    if (rv) row_to_head(a, g, row, t, h);
     const uint16_t* qrow = a.q + ((size_t)(b * a.Lq + t) * a.Hq + h) * D;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (rv) r = *(const u32x4*)(qrow + 32 * s + 8 * q4);
-      qf[s] = as_bf16x8(r);
+      qf[rb][s] = as_bf16x8(r);
     }
   }
   const size_t kv_tok = (size_t)a.G * D;
@@ -253,10 +310,17 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
   const uint16_t* Vb = a.v + ((size_t)b * a.Lk * a.G + g) * D;
   uint16_t* vl = vt_lds + w * D * VTS;
 
-  f32x4 acc[NDB];
+  f32x4 acc[NRB][NDB];
 #pragma unroll
-  for (int i = 0; i < NDB; ++i) acc[i] = f32x4{};
-  float m_run = kMaxInit, l_run = 0.f;
+  for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc[rb][i] = f32x4{};
+  float m_run[NRB], l_run[NRB];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    m_run[rb] = kMaxInit;
+    l_run[rb] = 0.f;
+  }
 
   u32x4 kr[2][KSTEPS];
   u32x4 vr[VU][4];
@@ -317,48 +381,57 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
     const int kn = k0 + 32;
     store_vt();
     if (kn < w1) load_v(kn);
-    // S^T for keys k0 + 16*kb + 4*q4 + r (register r), query row c16.
-    f32x4 s[2];
+    // S^T for keys k0 + 16*kb + 4*q4 + r (register r), query row 16rb + c16.
+    f32x4 s[NRB][2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      s[kb] = f32x4{};
+    for (int rb = 0; rb < NRB; ++rb)
 #pragma unroll
-      for (int st = 0; st < KSTEPS; ++st) s[kb] = mfma16x16x32(as_bf16x8(kr[kb][st]), qf[st], s[kb]);
-    }
+      for (int kb = 0; kb < 2; ++kb) {
+        s[rb][kb] = f32x4{};
+#pragma unroll
+        for (int st = 0; st < KSTEPS; ++st) s[rb][kb] = mfma16x16x32(as_bf16x8(kr[kb][st]), qf[rb][st], s[rb][kb]);
+      }
     if (kn < w1) load_k(kn);
     if (kn > w1) {
 #pragma unroll
+      for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k0 + 16 * kb + 4 * q4 + r >= w1) s[rb][kb][r] = -INFINITY;
+    }
+    float corr[NRB];
+    bf16x8 pf[NRB];
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      float mx = -INFINITY;
+#pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
-          if (k0 + 16 * kb + 4 * q4 + r >= w1) s[kb][r] = -INFINITY;
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[rb][kb][r]);
+      mx = xor32_max(xor16_max(mx));
+      const float m_new = fmaxf(m_run[rb], mx * a.cx);
+      corr[rb] = fast_exp2(m_run[rb] - m_new);
+      m_run[rb] = m_new;
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(fmaf(s[rb][kb][r], a.cx, -m_new));
+          rs += p;
+          s[rb][kb][r] = p;
+        }
+      l_run[rb] = fmaf(l_run[rb], corr[rb], rs);
+      // P^T as the B operand: slot j < 4 <-> key 4*q4 + j, slot j >= 4 <-> key 16 + 4*q4 + j - 4.
+      u32x4 pk;
+      pk[0] = pack_bf16x2(s[rb][0][0], s[rb][0][1]);
+      pk[1] = pack_bf16x2(s[rb][0][2], s[rb][0][3]);
+      pk[2] = pack_bf16x2(s[rb][1][0], s[rb][1][1]);
+      pk[3] = pack_bf16x2(s[rb][1][2], s[rb][1][3]);
+      pf[rb] = as_bf16x8(pk);
     }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[kb][r]);
-    mx = xor32_max(xor16_max(mx));
-    const float m_new = fmaxf(m_run, mx * a.cx);
-    const float corr = fast_exp2(m_run - m_new);
-    m_run = m_new;
-    float rs = 0.f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float p = fast_exp2(fmaf(s[kb][r], a.cx, -m_new));
-        rs += p;
-        s[kb][r] = p;
-      }
-    l_run = fmaf(l_run, corr, rs);
-    // P^T as the B operand: slot j < 4 <-> key 4*q4 + j, slot j >= 4 <-> key 16 + 4*q4 + j - 4.
-    u32x4 pk;
-    pk[0] = pack_bf16x2(s[0][0], s[0][1]);
-    pk[1] = pack_bf16x2(s[0][2], s[0][3]);
-    pk[2] = pack_bf16x2(s[1][0], s[1][1]);
-    pk[3] = pack_bf16x2(s[1][2], s[1][3]);
-    const bf16x8 pf = as_bf16x8(pk);
     wave_lds_sync();
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
@@ -366,41 +439,162 @@ __global__ __launch_bounds__(256, 2) void gqa_decode_kernel(DecodeArgs a) {
       const u32x2 lo = *(const u32x2*)vp;
       const u32x2 hi = *(const u32x2*)(vp + 16);
       const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-      acc[db] *= corr;
-      acc[db] = mfma16x16x32(as_bf16x8(av), pf, acc[db]);
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) {
+        acc[rb][db] *= corr[rb];
+        acc[rb][db] = mfma16x16x32(as_bf16x8(av), pf[rb], acc[rb][db]);
+      }
     }
     wave_lds_sync();
   }
 
-  // ---- combine the 4 waves of this work item ----
-  l_run = xor32_sum(xor16_sum(l_run));
-  __syncthreads();  // every wave is done with its V^T slab
-  float* red_o = (float*)vt_lds;           // [4][16 rows][D]
-  float* red_ml = red_o + 4 * 16 * D;      // [4][16 rows][2]
-#pragma unroll
-  for (int db = 0; db < NDB; ++db)
-    *(f32x4*)(red_o + (w * 16 + c16) * D + 16 * db + 4 * q4) = acc[db];
-  if (q4 == 0) {
-    red_ml[(w * 16 + c16) * 2] = m_run;
-    red_ml[(w * 16 + c16) * 2 + 1] = l_run;
-  }
-  __syncthreads();
+  // ---- combine the 4 waves of this work item, one row block at a time ----
   const bool final_out = c0 == 0 && L <= a.chunk;
   const size_t part = (size_t)bg * a.nch + chunk_id;
-  for (int e = tid; e < a.rows * D; e += 256) {
-    const int r = e / D, d = e % D;
-    float M = kMaxInit;
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, red_ml[(ww * 16 + r) * 2]);
-    float Ls = 0.f, O = 0.f;
+  for (int rb = 0; rb < NRB; ++rb)
+    combine_rows<D>(a, (float*)vt_lds, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), rb, b, g,
+                    part, final_out);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 GQA split-KV decode: the work items and wave split of
+// gqa_decode_kernel with full fp32 products on v_mfma_f32_16x16x4f32
+// (A lane l holds A[l%16][l/16], B lane l holds B[l/16][l%16], C as
+// 16x16x32).  Q.K contracts dims d = 16j + 4*q4 + e in step (j, e) with k
+// index q4, so each lane's K and Q^T operands are float4 loads of dims
+// 16j + 4*q4 .. +3.  P.V's B operand for step e is the score register e
+// itself (keys 4*q4 + e of a 16-key block), and its A operand V[key][dim] is
+// loaded per lane (16 lanes read 16 consecutive dims of one key row).  Up to
+// 32 rows (2 row blocks).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <int D, int NRB>
+__global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
+  constexpr int NJ = D / 16;   // float4 groups of Q.K per lane
+  constexpr int NDB = D / 16;  // 16-dim output blocks
+  static_assert(D % 64 == 0 && NRB <= 2, "fp32 decode shape");
+  __shared__ __attribute__((aligned(16))) float red[4 * 16 * D + 4 * 16 * 2];
+
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int c16 = lane & 15, q4 = lane >> 4;
+  __shared__ int sched[4 + 2 * kSchedMaxBatch];
+  int b, g, chunk_id, L;
+  if (!decode_item(a, sched, b, g, chunk_id, L)) return;
+  const int bg = b * a.G + g;
+  const int c0 = chunk_id * a.chunk;
+  const int per_wave = ((min(L - c0, a.chunk) + 127) >> 7) << 5;
+  const int w0 = c0 + w * per_wave;
+  const int w1 = min(w0 + per_wave, L);
+  const float* Q = (const float*)a.q;
+  const size_t kv_tok = (size_t)a.G * D;
+  const float* Kb = (const float*)a.k + ((size_t)b * a.Lk * a.G + g) * D;
+  const float* Vb = (const float*)a.v + ((size_t)b * a.Lk * a.G + g) * D;
+
+  f32x4 qf[NRB][NJ];
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const float wt = fast_exp2(red_ml[(ww * 16 + r) * 2] - M);
-      Ls = fmaf(wt, red_ml[(ww * 16 + r) * 2 + 1], Ls);
-      O = fmaf(wt, red_o[(ww * 16 + r) * D + d], O);
-    }
-    emit_row_elem(a, b, g, r, d, part, final_out, M, Ls, O);
+  for (int rb = 0; rb < NRB; ++rb) {
+    const int row = 16 * rb + c16;
+    const bool rv = row < a.rows;
+    int t = 0, h = 0;
+    if (rv) row_to_head(a, g, row, t, h);
+    const float* qrow = Q + ((size_t)(b * a.Lq + t) * a.Hq + h) * D;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) qf[rb][j] = rv ? *(const f32x4*)(qrow + 16 * j + 4 * q4) : f32x4{};
   }
+  f32x4 acc[NRB][NDB];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+    for (int i = 0; i < NDB; ++i) acc[rb][i] = f32x4{};
+  float m_run[NRB], l_run[NRB];
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb) {
+    m_run[rb] = kMaxInit;
+    l_run[rb] = 0.f;
+  }
+
+  for (int k0 = w0; k0 < w1; k0 += 32) {
+    // S^T for keys k0 + 16*kb + 4*q4 + r, query row 16rb + c16.
+    f32x4 s[NRB][2];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      const int key = k0 + 16 * kb + c16;
+      const bool ok = key < w1;
+      const float* kp = Kb + (size_t)(ok ? key : 0) * kv_tok + 4 * q4;
+      f32x4 kf[NJ];
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) kf[j] = ok ? *(const f32x4*)(kp + 16 * j) : f32x4{};
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb) {
+        s[rb][kb] = f32x4{};
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) s[rb][kb] = mfma16x16x4f32(kf[j][e], qf[rb][j][e], s[rb][kb]);
+      }
+    }
+    // V[key 16kb + 4*q4 + e][dim 16i + c16] for the A operands of P.V
+    float vv[2][4][NDB];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int key = k0 + 16 * kb + 4 * q4 + e;
+        const bool ok = key < w1;
+        const float* vp = Vb + (size_t)(ok ? key : 0) * kv_tok + c16;
+#pragma unroll
+        for (int i = 0; i < NDB; ++i) vv[kb][e][i] = ok ? vp[16 * i] : 0.f;
+      }
+    if (k0 + 32 > w1) {
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (k0 + 16 * kb + 4 * q4 + r >= w1) s[rb][kb][r] = -INFINITY;
+    }
+#pragma unroll
+    for (int rb = 0; rb < NRB; ++rb) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) mx = fmaxf(mx, s[rb][kb][r]);
+      mx = xor32_max(xor16_max(mx));
+      const float m_new = fmaxf(m_run[rb], mx * a.cx);
+      const float corr = fast_exp2(m_run[rb] - m_new);
+      m_run[rb] = m_new;
+      float rs = 0.f;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float p = fast_exp2(fmaf(s[rb][kb][r], a.cx, -m_new));
+          rs += p;
+          s[rb][kb][r] = p;
+        }
+      l_run[rb] = fmaf(l_run[rb], corr, rs);
+#pragma unroll
+      for (int i = 0; i < NDB; ++i) {
+        acc[rb][i] *= corr;
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[rb][i] = mfma16x16x4f32(vv[kb][e][i], s[rb][kb][e], acc[rb][i]);
+      }
+    }
+  }
+
+  const bool final_out = c0 == 0 && L <= a.chunk;
+  const size_t part = (size_t)bg * a.nch + chunk_id;
+#pragma unroll
+  for (int rb = 0; rb < NRB; ++rb)
+    combine_rows<D>(a, red, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), rb, b, g, part, final_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -715,8 +909,13 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
   int t, h;
   row_to_head(a, g, r, t, h);
   const float inv = den > 0.f ? 1.f / den : 0.f;
-  const u32x2 pk = {pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
-  *(u32x2*)(a.o + ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + 4 * u) = pk;
+  const size_t oi = ((size_t)(b * a.Lq + t) * a.Hq + h) * a.dv + 4 * u;
+  if (a.o32) {
+    *(f32x4*)(a.o32 + oi) = num * inv;
+  } else {
+    const u32x2 pk = {pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
+    *(u32x2*)(a.o + oi) = pk;
+  }
   if (a.lse && u == 0)
     a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = den > 0.f ? (M + __log2f(den)) * kLn2 : INFINITY;
 }
@@ -788,13 +987,17 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
                                   int64_t kv_heads, int64_t head_dim, float sm_scale,
                                   int64_t chunk, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: only bf16 is supported");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
+  const bool f32 = dtype == PJX_DTYPE_F32;
   if (!q || !k || !v || !o) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: null pointer");
   if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
     return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: bad sizes");
   if (head_dim != 128 && head_dim != 64) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: head_dim must be 64 or 128");
   const int64_t rows = (q_heads / kv_heads) * q_len;
-  if (rows > kRows) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: (Hq/Hkv)*Lq must be <= 16");
+  if (rows > (f32 ? 2 : 4) * kRows)
+    return fail(PJX_ERR_INVALID, f32 ? "pjx_splitkv_decode: (Hq/Hkv)*Lq must be <= 32 in fp32"
+                                     : "pjx_splitkv_decode: (Hq/Hkv)*Lq must be <= 64");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: sm_scale must be > 0");
   if (chunk == 0) chunk = auto_chunk(batch, kv_heads, kv_len, kGqaItems);
   if (chunk < 128 || chunk % 128) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: chunk must be a positive multiple of 128");
@@ -803,14 +1006,33 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   if (batch == 0) return PJX_OK;
   DecodeArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
-  a.lengths = kv_lengths; a.o = (uint16_t*)o; a.lse = lse;
+  a.lengths = kv_lengths; a.lse = lse;
+  if (f32)
+    a.o32 = (float*)o;
+  else
+    a.o = (uint16_t*)o;
   a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len; a.Hq = (int)q_heads; a.G = (int)kv_heads;
   a.rows = (int)rows; a.fold = 0; a.chunk = (int)chunk;
   a.nch = (int)std::max<int64_t>((kv_len + chunk - 1) / chunk, 1);
   a.dv = (int)head_dim; a.cx = sm_scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
-  if (head_dim == 128) return run_decode(gqa_decode_kernel<128>, a, workspace, workspace_bytes, s, "pjx_splitkv_decode");
-  return run_decode(gqa_decode_kernel<64>, a, workspace, workspace_bytes, s, "pjx_splitkv_decode");
+  const char* who = "pjx_splitkv_decode";
+  const int nrb = (int)((rows + kRows - 1) / kRows);
+  if (f32) {
+    if (head_dim == 128)
+      return nrb == 1 ? run_decode(gqa_decode_f32_kernel<128, 1>, a, workspace, workspace_bytes, s, who)
+                      : run_decode(gqa_decode_f32_kernel<128, 2>, a, workspace, workspace_bytes, s, who);
+    return nrb == 1 ? run_decode(gqa_decode_f32_kernel<64, 1>, a, workspace, workspace_bytes, s, who)
+                    : run_decode(gqa_decode_f32_kernel<64, 2>, a, workspace, workspace_bytes, s, who);
+  }
+  if (head_dim == 128) {
+    if (nrb == 1) return run_decode(gqa_decode_kernel<128, 1>, a, workspace, workspace_bytes, s, who);
+    if (nrb == 2) return run_decode(gqa_decode_kernel<128, 2>, a, workspace, workspace_bytes, s, who);
+    return run_decode(gqa_decode_kernel<128, 4>, a, workspace, workspace_bytes, s, who);
+  }
+  if (nrb == 1) return run_decode(gqa_decode_kernel<64, 1>, a, workspace, workspace_bytes, s, who);
+  if (nrb == 2) return run_decode(gqa_decode_kernel<64, 2>, a, workspace, workspace_bytes, s, who);
+  return run_decode(gqa_decode_kernel<64, 4>, a, workspace, workspace_bytes, s, who);
 }
 
 // ---------------------------------------------------------------------------

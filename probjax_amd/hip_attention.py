@@ -239,7 +239,8 @@ def splitkv_decode(
     q, k, v, *, sm_scale: float, kv_lengths=None, chunk: int = 0, return_lse: bool = False,
     workspace=None,
 ):
-    """``pjx_splitkv_decode``: bf16 ``q [B, Lq, Hq, D]``, ``k/v [B, S, Hkv, D]``."""
+    """``pjx_splitkv_decode``: bf16 or fp32 ``q [B, Lq, Hq, D]``,
+    ``k/v [B, S, Hkv, D]``; ``(Hq/Hkv)*Lq`` up to 64 (bf16) or 32 (fp32)."""
     dev = _on_device(q, k, v)
     if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
         raise ValueError("q must be [B, Lq, Hq, D] and k, v [B, S, Hkv, D]")
@@ -247,11 +248,12 @@ def splitkv_decode(
     _, S, Hkv, Dk = k.shape
     if Dk != D or k.shape[0] != B or Hq % Hkv:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}")
-    if q.dtype != torch.bfloat16 or k.dtype != torch.bfloat16 or v.dtype != torch.bfloat16:
-        raise ValueError("split-KV decode takes bfloat16 q, k, v")
+    if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("split-KV decode takes bfloat16 or float32 q, k, v of one dtype")
     rows = (Hq // Hkv) * Lq
-    if rows > 16 or D not in (64, 128):
-        raise ValueError("split-KV decode needs (Hq/Hkv)*Lq <= 16 and head_dim 64 or 128")
+    max_rows = 64 if q.dtype == torch.bfloat16 else 32
+    if rows > max_rows or D not in (64, 128):
+        raise ValueError(f"split-KV decode needs (Hq/Hkv)*Lq <= {max_rows} and head_dim 64 or 128")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     L = _lengths(kv_lengths, B, dev)
     nbytes = decode_workspace_bytes(B, Hkv, rows, S, D, chunk)
@@ -259,7 +261,7 @@ def splitkv_decode(
     o = torch.empty_like(q)
     lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=dev) if return_lse else None
     rc = native.load().pjx_splitkv_decode(
-        native.PJX_DTYPE_BF16, _ptr(q), _ptr(k), _ptr(v), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
+        _dtype_code(q), _ptr(q), _ptr(k), _ptr(v), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
         nbytes, B, Lq, S, Hq, Hkv, D, float(sm_scale), int(chunk), _stream(dev),
     )
     native.check(rc)

@@ -75,9 +75,13 @@ def test_use_splitkv_only_for_exact_cases():
     q3, k3, _ = _qkv(lq=100)
     assert not A.use_splitkv(q3, k3)
     q4, k4, _ = _qkv(hq=64, hkv=2)                              # 32 rows per KV head
-    assert not A.use_splitkv(q4, k4, split_kv=True)
+    assert A.use_splitkv(q4, k4, split_kv=True)
+    q4b, k4b, _ = _qkv(hq=64, hkv=2, lq=3)                      # 96 rows: past the reference's 64
+    assert not A.use_splitkv(q4b, k4b, split_kv=True)
     q5, k5, _ = _qkv(dtype=torch.float32)
-    assert not A.use_splitkv(q5, k5)
+    assert A.use_splitkv(q5, k5)                                # fp32 split-KV
+    q5b, k5b, _ = _qkv(dtype=torch.float32, hq=64, hkv=1)       # 64 rows: fp32 takes up to 32
+    assert not A.use_splitkv(q5b, k5b, split_kv=True)
     # head dims up to 128 are zero-padded to a kernel width; wider ones are not
     q6, k6 = torch.zeros(1, 1, 8, 96, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 96, dtype=torch.bfloat16)
     assert A.use_splitkv(q6, k6)

@@ -126,16 +126,21 @@ def test_decode_rejects_invalid_arguments(lib):
     ok = [native.PJX_DTYPE_BF16, P(1), P(1), P(1), None, P(1), None, P(1), 1 << 30,
           1, 1, 64, 32, 8, 128, 0.1, 0, None]
     bad_rows = list(ok)
-    bad_rows[12] = 256  # (Hq/Hkv)*Lq = 32 rows > 16
+    bad_rows[12] = 8 * 65  # (Hq/Hkv)*Lq = 65 rows > 64
     assert lib.pjx_splitkv_decode(*bad_rows) == 1
-    assert "<= 16" in lib.pjx_last_error().decode()
+    assert "<= 64" in lib.pjx_last_error().decode()
     bad_chunk = list(ok)
     bad_chunk[16] = 100
     assert lib.pjx_splitkv_decode(*bad_chunk) == 1
     assert "chunk" in lib.pjx_last_error().decode()
     f32 = list(ok)
     f32[0] = native.PJX_DTYPE_F32
+    f32[12] = 8 * 33  # 33 rows: fp32 takes up to 32
     assert lib.pjx_splitkv_decode(*f32) == 1
+    assert "<= 32 in fp32" in lib.pjx_last_error().decode()
+    bad_dtype = list(ok)
+    bad_dtype[0] = 7
+    assert lib.pjx_splitkv_decode(*bad_dtype) == 1
     mla = [native.PJX_DTYPE_BF16, P(1), P(1), None, P(1), None, P(1), 1 << 30,
            1, 1, 16, 64, 300, 512, 0.1, 0, None]
     assert lib.pjx_mla_decode(*mla) == 1
