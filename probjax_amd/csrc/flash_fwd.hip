@@ -371,6 +371,7 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
 #pragma unroll
   for (int i = 0; i < D / 32; ++i) acc[i] = f32x16{};
   float m_run = kMaxInit, l_run = 0.f;
+  float thr = -INFINITY;  // rescale when a raw row max exceeds (m_run + kRescaleLog2) / cx
 
   const int n_tiles = max((g.kv_stop + BK - 1) / BK, 0);
   const int q_last_w = g.qw + 31;
@@ -413,16 +414,20 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
         for (int r = 0; r < 16; ++r)
           if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
     }
-    float mx = -INFINITY;
+    // Row max as a chain of 3-input maxima, compared in raw score units with
+    // the rescale threshold (m_run + kRescaleLog2) / cx kept from the last
+    // rescale: no per-tile multiply.
+    float mx = fmaxf(s[0][0], s[0][1]);
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; r += 2) mx = fmaxf(mx, fmaxf(s[kb][r], s[kb][r + 1]));
-    const float mc = xor32_max(mx) * cx;
-    if (wave_any(mc > m_run + kRescaleLog2)) {
-      const float m_new = fmaxf(m_run, mc);
+      for (int r = (kb == 0 ? 2 : 0); r < 16; r += 2) mx = fmaxf(fmaxf(mx, s[kb][r]), s[kb][r + 1]);
+    mx = xor32_max(mx);
+    if (wave_any(mx > thr)) {
+      const float m_new = fmaxf(m_run, mx * cx);
       const float corr = fast_exp2(m_run - m_new);
       m_run = m_new;
+      thr = (m_run + kRescaleLog2) / cx;
       l_run *= corr;
 #pragma unroll
       for (int i = 0; i < D / 32; ++i)
@@ -431,16 +436,20 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
     }
     // one basic block from here: S_{t+1} on the MFMA pipe under the exponentials
     qk(ks_next, sn);
-    float rs = 0.f;
+    // two independent partial sums (the adds need not wait on each other)
+    float rs0 = 0.f, rs1 = 0.f;
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = fast_exp2(fmaf(s[kb][r], cx, -m_run));
-        rs += p;
-        s[kb][r] = p;
+      for (int r = 0; r < 16; r += 2) {
+        const float p0 = fast_exp2(fmaf(s[kb][r], cx, -m_run));
+        const float p1 = fast_exp2(fmaf(s[kb][r + 1], cx, -m_run));
+        rs0 += p0;
+        rs1 += p1;
+        s[kb][r] = p0;
+        s[kb][r + 1] = p1;
       }
-    l_run += rs;
+    l_run += rs0 + rs1;
     bf16x8 pf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) {
