@@ -27,8 +27,15 @@
 extern "C" {
 #endif
 
+/* Element types of q, k, v, o (and cache / weights).  The bf16 and fp16
+ * paths are the same kernels (v_mfma_f32_*_bf16 / _f16 operands, fp32
+ * accumulation); P and dS are rounded to the input's 16-bit type before their
+ * products, as the reference's casts to V's / Q's dtype do.  The reference's
+ * fused paths take all three (layers/attention.py:1187,
+ * kernels/attention.py:2678). */
 #define PJX_DTYPE_F32 0
 #define PJX_DTYPE_BF16 1
+#define PJX_DTYPE_F16 2
 
 #define PJX_OK 0
 #define PJX_ERR_INVALID 1  /* unsupported shape / dtype / argument */
@@ -98,8 +105,8 @@ const char* pjx_last_error(void);
  * the XLA reference (kernels/attention_xla.py:339-429):
  *
  *   s = sm_scale * q.k (fp32)  [+ bias[b|0, h|0, q, k]]  then masked -> -inf,
- *   o = softmax(s) . v with fp32 accumulation; P is rounded to bf16 before the
- *   P.V product in bf16 mode; rows without a valid key give 0.
+ *   o = softmax(s) . v with fp32 accumulation; P is rounded to bf16 / fp16
+ *   before the P.V product with 16-bit inputs; rows without a valid key give 0.
  *
  * Masks (ANDed), all optional:
  *   causal      -- CausalMask, q >= k (attention_mask_bias.py:615-646)
@@ -114,8 +121,8 @@ const char* pjx_last_error(void);
  *
  * mods: extended masks / score modifiers (pjx_score_mods) or NULL.
  *
- * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim in {64, 128},
- * or 256 in bf16 (k and v share it; the reference's fused path takes
+ * dtype: PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim
+ * in {64, 128}, or 256 in bf16 / fp16 (k and v share it; the reference's fused path takes
  * head_dim <= 256, layers/attention.py:1193-1195).  sm_scale must be > 0.
  */
 int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
@@ -138,7 +145,8 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * 909-1160, _mha_backward_raw 3505-3560 with the GQA group sums 2123-2128):
  *
  *   delta = sum_d o*do;  p = exp(s - lse);  ds = p * (do.v^T - delta) * sm_scale
- *   dv = sum_q bf16(p)^T do,  dk = sum_q bf16(ds)^T q,  dq = sum_k bf16(ds) k
+ *   dv = sum_q r(p)^T do,  dk = sum_q r(ds)^T q,  dq = sum_k r(ds) k
+ *   (r: rounding to the 16-bit input type; none in fp32)
  *
  * with s the forward's score (sm_scale * q.k + bias, masked keys excluded)
  * and fp32 accumulation; dk/dv sum the query heads of each KV head's group.
@@ -155,8 +163,8 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * (fully written, zeros where no valid score reaches).  workspace: at least
  * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.  mods: the
  * forward's (pjx_score_mods) or NULL.
- * dtype: PJX_DTYPE_BF16 or PJX_DTYPE_F32 (all fp32 products, no roundings).
- * head_dim in {64, 128}, or 256 in bf16.
+ * dtype: PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 (all fp32 products, no
+ * roundings).  head_dim in {64, 128}, or 256 in bf16 / fp16.
  */
 int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
@@ -183,12 +191,12 @@ size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
  * 43-250) and extends it with the per-sequence KVLenMask that the reference
  * routes to the regular forward (kernels/attention.py:2672-2675).
  *
- * dtype PJX_DTYPE_BF16 or PJX_DTYPE_F32 (full fp32 products) for q, k, v, o:
+ * dtype PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 (full fp32 products) for q, k, v, o:
  * q [B, Lq, Hq, D]; k, v [B, Lk, Hkv, D] (Lk = KV capacity);
  * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, D];
  * lse optional fp32 [B, Hq, Lq], natural log (attention_splitkv.py:248-250).
  * The (Hq/Hkv)*Lq query rows of a KV head are packed row = g*Lq + t
- * (attention_splitkv.py:121-126); at most 64 rows per KV head in bf16 (the
+ * (attention_splitkv.py:121-126); at most 64 rows per KV head in bf16 / fp16 (the
  * reference packs up to 64, :155-170), 32 in fp32.
  * Only keys < kv_lengths[b] are read.  head_dim == 128.
  * chunk: keys per work item (0 = automatic: a power of two in [128, 2048]
@@ -230,8 +238,9 @@ int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const voi
  * latent_attention.py:79-197, 247-377, 636-766) with heads folded onto the
  * query axis (layers/latent_attention.py:458-469, row = t*H + h).
  *
- * q [B, Lq, H, R] bf16; cache [B, S, R] bf16; kv_lengths int32 [B] or NULL;
- * o [B, Lq, H, v_dim] bf16 = the first v_dim columns of mla(q, cache, None,
+ * q [B, Lq, H, R] and cache [B, S, R] of dtype (PJX_DTYPE_BF16 or PJX_DTYPE_F16);
+ * kv_lengths int32 [B] or NULL;
+ * o [B, Lq, H, v_dim] of dtype = the first v_dim columns of mla(q, cache, None,
  * None) (v_dim == R gives the API-exact output); lse optional fp32 [B, H, Lq].
  * Lq*H <= 16.  R a multiple of 64, R <= 576; v_dim a multiple of 64, <= R.
  * chunk: keys per work item (0 = automatic, as for pjx_splitkv_decode; else a
@@ -253,16 +262,17 @@ int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* k
  * called from mla 636-766) with the masks and bias of pjx_flash_fwd:
  *
  *   s = sm_scale * q.c (fp32) [+ bias] then masked -> -inf;
- *   o = softmax(s) . c[:, :v_dim], P rounded to bf16 before the product.
+ *   o = softmax(s) . c[:, :v_dim], P rounded to the 16-bit dtype before the product.
  *
- * q [B, Lq, H, R] bf16 (all H heads share the one latent head; folded calls
- * pass [B, Lq*H, 1, R] with H = 1); cache [B, S, R] bf16; o [B, Lq, H, v_dim]
- * bf16 = the first v_dim columns of mla(q, cache, None, None) (v_dim == R
+ * q [B, Lq, H, R] (all H heads share the one latent head; folded calls
+ * pass [B, Lq*H, 1, R] with H = 1); cache [B, S, R]; o [B, Lq, H, v_dim]
+ * = the first v_dim columns of mla(q, cache, None, None) (v_dim == R
  * gives the API-exact output); lse optional fp32 [B, H, Lq] natural log.
  * kv_lengths, bias ([1|B, 1|H, Lq, S] fp32), q_valid / kv_valid, causal and
  * mods as for pjx_flash_fwd (with Lk = S, Hq = H).
  * (rank, v_dim) in {(576, 512), (576, 576), (512, 512)}, or rank in
  * {64, 128, 256} with v_dim == rank (the flash kernels with one K = V head).
+ * dtype PJX_DTYPE_BF16 or PJX_DTYPE_F16 for q, cache, o.
  */
 int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o, float* lse,
                 const int32_t* kv_lengths, const float* bias, int64_t bias_batch,
@@ -287,8 +297,9 @@ size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64_t q_len, i
  * _materialized_mla :413-468), so that
  *
  *   delta = sum_d o*do;  p = exp(s - lse);  ds = p * (do.c[:, :v_dim]^T - delta) * sm_scale
- *   dq = sum_k bf16(ds) c,
- *   dcache = sum over heads and queries of bf16(ds)^T q + bf16(p)^T do (first v_dim dims)
+ *   dq = sum_k r(ds) c,
+ *   dcache = sum over heads and queries of r(ds)^T q + r(p)^T do (first v_dim dims)
+ *   (r: rounding to the 16-bit dtype)
  *
  * with fp32 accumulation (the sum over heads in fp32 before one rounding).
  * The bias gets no gradient, as the reference's VJP returns none for mask
@@ -297,7 +308,7 @@ size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64_t q_len, i
  * [B, H, Lq] natural-log LSE); dq [B, Lq, H, rank] and dcache [B, S, rank] are
  * fully written.  workspace: at least pjx_mla_bwd_workspace_size(batch, heads,
  * q_len, kv_len, rank) bytes.  (rank, v_dim) in {(576, 512), (576, 576),
- * (512, 512)}; bf16.
+ * (512, 512)}; dtype PJX_DTYPE_BF16 or PJX_DTYPE_F16.
  */
 int pjx_mla_bwd(int dtype, const void* q, const void* cache, const void* o, const void* dout,
                 const float* lse, void* dq, void* dcache, void* workspace, size_t workspace_bytes,
@@ -316,7 +327,7 @@ int pjx_mla_bwd(int dtype, const void* q, const void* cache, const void* o, cons
  *   k[b, s, h, d] = sum_r cache[b, s, r] * wk[h, d, r]  (d < qk_dim; 0 up to width)
  *   v[b, s, h, d] = sum_r cache[b, s, r] * wv[h, d, r]  (d < v_dim;  0 up to width)
  *
- * fp32 accumulation, rounded to dtype (PJX_DTYPE_BF16 or PJX_DTYPE_F32; all
+ * fp32 accumulation, rounded to dtype (PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32; all
  * operands the same dtype).  cache [B, S, R]; wk [H, qk_dim, R];
  * wv [H, v_dim, R]; k, v [B, S, H, width] fully written.  The flash kernels
  * then attend q (zero-padded to width) over k / v: the padded channels carry

@@ -15,7 +15,7 @@ Pinning status of each function is recorded in the module docstrings
 (``parity pinned by ...``); nothing here is "parity unpinned".
 """
 
-from .bf16 import round_bf16  # noqa: F401
+from .bf16 import round_bf16, round_f16, round_to  # noqa: F401
 from .masks import (  # noqa: F401
     BlockDiagonalCausalMask,
     BlockDiagonalMask,

@@ -16,9 +16,9 @@ Follows ``probjax/nn/pallas_kernels/kernels/attention_xla.py``:
 * ``_tiled_forward``     -- ``:380-429`` (online softmax; statically empty tiles
   skipped ``:318-331,373-377``; empty rows -> output 0, LSE ``+inf``)
 
-bf16 inputs are float32 arrays holding bfloat16 values with ``dtype="bf16"``:
-products are exact in fp32, P and the output are rounded like the reference's
-``astype(bfloat16)`` casts.  Dropout is off the path (rate 0) and not restated.
+bf16 / fp16 inputs are float32 arrays holding bfloat16 / float16 values with
+``dtype="bf16"`` / ``"f16"``: products are exact in fp32, P and the output are
+rounded like the reference's ``astype(bfloat16)`` / ``astype(float16)`` casts.  Dropout is off the path (rate 0) and not restated.
 
 Parity pinned (``tests/test_oracle_attention.py``) by: float64 brute force on
 tiny inputs; torch ``scaled_dot_product_attention`` on CPU (an independent
@@ -35,7 +35,7 @@ import math
 
 import numpy as np
 
-from .bf16 import round_bf16
+from .bf16 import LOW_PRECISION, round_to
 
 DENSE_MAX_SCORES = 256 * 256
 SINGLE_TILE_MAX_SCORES = 512 * 512
@@ -107,16 +107,16 @@ def _scores(q5, kc, sm_scale, cdt):
     return s.reshape(b, hkv * g, q, k)
 
 
-def _pv(p, vc, hkv, bf16, cdt):
+def _pv(p, vc, hkv, dtype, cdt):
     """attention_xla.py:347-350: P cast to V's dtype, fp32 accumulation."""
     b, hq, q, k = p.shape
     p5 = p.reshape(b, hkv, hq // hkv, q, k)
-    if bf16:
-        p5 = round_bf16(p5)
+    if dtype in LOW_PRECISION:
+        p5 = round_to(p5, dtype)
     return np.matmul(p5.astype(cdt), vc.astype(cdt)[:, :, None])
 
 
-def _dense_forward(q5, k, v, mods, sm_scale, bf16, cdt):
+def _dense_forward(q5, k, v, mods, sm_scale, dtype, cdt):
     """attention_xla.py:353-366."""
     hkv = k.shape[1]
     q_len, kv_len = q5.shape[3], k.shape[2]
@@ -130,10 +130,10 @@ def _dense_forward(q5, k, v, mods, sm_scale, bf16, cdt):
     lse = np.where(nonempty, m + np.log(np.where(nonempty, l_, 1.0)), np.inf)
     l_ = np.where(l_ == 0.0, cdt(1.0), l_)
     p = p / l_[..., None]
-    return _pv(p, v, hkv, bf16, cdt), lse
+    return _pv(p, v, hkv, dtype, cdt), lse
 
 
-def _tiled_forward(q5, k, v, mods, sm_scale, bq, kc, bm, bf16, cdt):
+def _tiled_forward(q5, k, v, mods, sm_scale, bq, kc, bm, dtype, cdt):
     """attention_xla.py:380-429: online softmax over bq x kc tiles."""
     b, hkv, g, q_total, _ = q5.shape
     dv = v.shape[-1]
@@ -159,7 +159,7 @@ def _tiled_forward(q5, k, v, mods, sm_scale, bq, kc, bm, bf16, cdt):
             p = np.exp(s - m_safe[..., None])
             l_ = l_ * corr + np.sum(p, axis=-1)
             corr5 = corr.reshape(b, hkv, g, bq)[..., None]
-            o = o * corr5 + _pv(p, vj, hkv, bf16, cdt)
+            o = o * corr5 + _pv(p, vj, hkv, dtype, cdt)
             m = m_new
         nonempty = l_ > 0.0
         l_safe = np.where(nonempty, l_, cdt(1.0))
@@ -198,16 +198,14 @@ def xla_attention(
     """Oracle of ``xla_attention`` (attention_xla.py:601-721).
 
     ``q [B, Lq, Hq, D]``, ``k/v [B, Lk, Hkv, D|Dv]`` numpy arrays.  ``dtype``
-    is the input dtype being emulated (``"f32"`` or ``"bf16"``).  Returns the
-    output ``[B, Lq, Hq, Dv]`` (float32; bf16-rounded when ``dtype="bf16"``)
+    is the input dtype being emulated (``"f32"``, ``"bf16"`` or ``"f16"``).
+    Returns the output ``[B, Lq, Hq, Dv]`` (float32; rounded to the 16-bit
+    dtype for ``"bf16"`` / ``"f16"``)
     and, with ``return_lse``, the natural-log LSE ``[B, Hq, Lq]`` (``+inf``
     for rows with no valid key).
     """
-    bf16 = dtype == "bf16"
     cdt = np.dtype(compute_dtype).type
-    q, k, v = (np.asarray(x, np.float32) for x in (q, k, v))
-    if bf16:
-        q, k, v = (round_bf16(x) for x in (q, k, v))
+    q, k, v = (round_to(np.asarray(x, np.float32), dtype) for x in (q, k, v))
     batch, q_len, hq, _ = q.shape
     kv_len, hkv = k.shape[1], k.shape[2]
     if hq % hkv != 0:
@@ -240,15 +238,14 @@ def xla_attention(
     mods = _Mods(mask, bias, q_len, kv_len, kv_pad)
 
     if strategy == "dense":
-        o5, lse = _dense_forward(q5, kt, vt, mods, sm_scale, bf16, cdt)
+        o5, lse = _dense_forward(q5, kt, vt, mods, sm_scale, dtype, cdt)
     else:
         bm = _tile_block_mask(mask, q_pad, kv_pad, bq, kc)
-        o5, lse = _tiled_forward(q5, kt, vt, mods, sm_scale, bq, kc, bm, bf16, cdt)
+        o5, lse = _tiled_forward(q5, kt, vt, mods, sm_scale, bq, kc, bm, dtype, cdt)
 
     o = o5.reshape(batch, hq, q_pad, v.shape[-1])[:, :, :q_len]
     o = np.transpose(o, (0, 2, 1, 3)).astype(np.float32)
-    if bf16:
-        o = round_bf16(o)
+    o = round_to(o, dtype)
     if return_lse:
         return o, np.asarray(lse[:, :, :q_len], np.float32)
     return o

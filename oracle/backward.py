@@ -32,7 +32,9 @@ Rows without a valid key: the forward's natural-log LSE is ``+inf`` there
 rows contribute nothing -- the gradient of the constant 0 output those rows
 have in the XLA path.
 
-bf16 inputs are float32 arrays holding bfloat16 values with ``dtype="bf16"``.
+bf16 / fp16 inputs are float32 arrays holding bfloat16 / float16 values with
+``dtype="bf16"`` / ``"f16"`` (P and dS rounded to that dtype before their
+products, as the reference's casts do).
 
 Parity pinned (``tests/test_oracle_backward.py``) by: torch autograd in
 float64 through an explicit masked softmax and through
@@ -48,7 +50,7 @@ from __future__ import annotations
 
 import numpy as np
 
-from .bf16 import round_bf16
+from .bf16 import LOW_PRECISION, round_to
 
 
 def preprocess_delta(o, do, compute_dtype=np.float32):
@@ -80,11 +82,9 @@ def attention_backward(
     natural log (``+inf`` for rows without a valid key).  ``mask`` is an
     oracle mask object (``tile_keep``), ``bias`` a ``DenseBias`` (``tile_add``).
     """
-    bf16 = dtype == "bf16"
+    low = dtype in LOW_PRECISION
     cdt = np.dtype(compute_dtype).type
-    q, k, v, o, do = (np.asarray(x, np.float32) for x in (q, k, v, o, do))
-    if bf16:
-        q, k, v, o, do = (round_bf16(x) for x in (q, k, v, o, do))
+    q, k, v, o, do = (round_to(np.asarray(x, np.float32), dtype) for x in (q, k, v, o, do))
     B, Lq, Hq, D = q.shape
     Lk, Hkv = k.shape[1], k.shape[2]
     if Hq % Hkv:
@@ -122,15 +122,15 @@ def attention_backward(
                 ds = ds * cdt(sm_scale)
             if gf is not None:
                 ds = ds * np.asarray(gf, cdt)  # score-modifier derivative (:1051-1056)
-            pc = round_bf16(p).astype(cdt) if bf16 else p
-            dsc = round_bf16(ds).astype(cdt) if bf16 else ds
+            pc = round_to(p, dtype).astype(cdt) if low else p
+            dsc = round_to(ds, dtype).astype(cdt) if low else ds
             dv_h[b, :, h] = pc.T @ dob
             dk_h[b, :, h] = dsc.T @ qb
             dq[b, :, h] = dsc @ kb
 
     def finish(x):
         x = np.asarray(x, np.float32)
-        return round_bf16(x) if bf16 else x
+        return round_to(x, dtype)
 
     dk_h, dv_h = finish(dk_h), finish(dv_h)
     dk = np.sum(dk_h.reshape(B, Lk, Hkv, G, D).astype(cdt), axis=3)

@@ -38,7 +38,7 @@ import math
 import numpy as np
 
 from .attention_xla import xla_attention
-from .bf16 import round_bf16
+from .bf16 import round_to
 
 
 def materialize_kv(cache, wk, wv, num_heads):
@@ -98,7 +98,7 @@ def unfold_heads(o, num_q, num_heads):
 
 
 def _round(x, dtype):
-    return round_bf16(np.asarray(x, np.float32)) if dtype == "bf16" else x
+    return x if dtype == "f32" else round_to(np.asarray(x, np.float32), dtype)
 
 
 def _pad_last(x, width):
@@ -108,9 +108,7 @@ def _pad_last(x, width):
 
 def _materialized_operands(q, cache, wk, wv, dtype, compute_dtype):
     cdt = np.dtype(compute_dtype).type
-    q, cache, wk, wv = (np.asarray(x, np.float32) for x in (q, cache, wk, wv))
-    if dtype == "bf16":
-        q, cache, wk, wv = (round_bf16(x) for x in (q, cache, wk, wv))
+    q, cache, wk, wv = (round_to(np.asarray(x, np.float32), dtype) for x in (q, cache, wk, wv))
     q, cache, wk, wv = (x.astype(cdt) for x in (q, cache, wk, wv))
     key = _round(np.einsum("bsr,hdr->bshd", cache, wk, optimize=True), dtype).astype(cdt)
     value = _round(np.einsum("bsr,hdr->bshd", cache, wv, optimize=True), dtype).astype(cdt)

@@ -33,7 +33,7 @@ import numpy as np
 
 from .attention_xla import xla_attention
 from .backward import attention_backward
-from .bf16 import round_bf16
+from .bf16 import round_to
 from .masks import BatchedLowRankBias, LearnedAlibiBias, LowRankBias, SumBias
 
 _LOW_RANK = (LowRankBias, BatchedLowRankBias, LearnedAlibiBias)
@@ -54,7 +54,7 @@ def split_low_rank_bias(bias):
 
 
 def _cast(x, dtype):
-    return round_bf16(np.asarray(x, np.float32)) if dtype == "bf16" else np.asarray(x, np.float32)
+    return round_to(np.asarray(x, np.float32), dtype)
 
 
 def fold_low_rank(q, k, v, terms, sm_scale, dtype="f32"):

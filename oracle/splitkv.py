@@ -30,7 +30,7 @@ import math
 
 import numpy as np
 
-from .bf16 import round_bf16
+from .bf16 import LOW_PRECISION, round_to
 
 LOG2E = 1.4426950408889634
 NEG_INF = -1e15
@@ -67,7 +67,6 @@ def split_partials(q, k, v, *, sm_scale, split_len, kv_lengths=None, dtype="f32"
 
     Returns ``o_part [B, Hkv, S, R, Dv]`` and ``lse_part [B, Hkv, S, R]``.
     """
-    bf16 = dtype == "bf16"
     b, lq, hq, d = q.shape
     _, lkv, hkv, _ = k.shape
     qp = pack_queries(q, hkv).astype(np.float32)  # [B, Hkv, R, D]
@@ -92,7 +91,7 @@ def split_partials(q, k, v, *, sm_scale, split_len, kv_lengths=None, dtype="f32"
         # merged result and also holds for masked keys whose V is not zero.
         p = np.where(valid[:, None, None, :], np.exp2(qk - m[..., None]), np.float32(0.0))
         l_ = p.sum(axis=-1)
-        pv = round_bf16(p) if bf16 else p
+        pv = round_to(p, dtype) if dtype in LOW_PRECISION else p
         o = np.matmul(pv, vt[:, :, k0:k1])
         safe_l = np.where(l_ == 0.0, 1.0, l_)
         o_part[:, :, s] = o / safe_l[..., None]
@@ -122,9 +121,7 @@ def splitkv_forward(
     dtype="f32", return_lse=False,
 ):
     """``q [B, Lq, Hq, D]``, ``k/v [B, Lkv, Hkv, *]`` -> ``[B, Lq, Hq, Dv]``."""
-    q, k, v = (np.asarray(x, np.float32) for x in (q, k, v))
-    if dtype == "bf16":
-        q, k, v = (round_bf16(x) for x in (q, k, v))
+    q, k, v = (round_to(np.asarray(x, np.float32), dtype) for x in (q, k, v))
     b, lq, hq, _ = q.shape
     lkv, hkv = k.shape[1], k.shape[2]
     if hq % hkv:
@@ -140,8 +137,7 @@ def splitkv_forward(
     )
     out, lse = merge_partials(o_part, lse_part)
     out = unpack_rows(out, lq, hq).astype(np.float32)
-    if dtype == "bf16":
-        out = round_bf16(out)
+    out = round_to(out, dtype)
     if not return_lse:
         return out
     return out, lse.reshape(b, hkv, hq // hkv, lq).reshape(b, hq, lq).astype(np.float32)

@@ -47,15 +47,17 @@ from .masks import (LoweredBias, LoweredMask, dense_keep, dense_relpos, dense_su
                     lower_mask, split_low_rank_bias)
 
 HIP_ARCH = "gfx950"
-FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 only
+HALF_DTYPES = (torch.bfloat16, torch.float16)  # the 16-bit (MFMA bf16 / fp16) kernels
+KERNEL_DTYPES = HALF_DTYPES + (torch.float32,)  # dtypes the kernels take
+FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 / float16 only
 FLASH_HEAD_DIMS_F32 = (64, 128)
 DECODE_HEAD_DIMS = (64, 128)
-LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (bfloat16)
-DECODE_MAX_ROWS = 64       # (Hq/Hkv)*Lq rows per KV head of the bf16 split-KV decode
+LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (16-bit)
+DECODE_MAX_ROWS = 64       # (Hq/Hkv)*Lq rows per KV head of the 16-bit split-KV decode
 DECODE_MAX_ROWS_F32 = 32   # ... of the fp32 split-KV decode
 MLA_DECODE_MAX_ROWS = 16   # Lq*H folded rows of the latent decode
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
-BACKWARD_DTYPES = (torch.bfloat16, torch.float32)  # dtypes pjx_flash_bwd takes
+BACKWARD_DTYPES = KERNEL_DTYPES  # dtypes pjx_flash_bwd takes
 
 # Split-KV decode thresholds (probjax kernels/attention.py:2649-2650).
 _SPLITKV_MAX_Q_LEN = 64
@@ -125,7 +127,7 @@ def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
     """Arguments of the split-KV decode for this call, or None."""
     if lb is not None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return None
-    if query.dtype not in (torch.bfloat16, torch.float32):
+    if query.dtype not in KERNEL_DTYPES:
         return None
     B, l_q, h_q, d = query.shape
     h_kv = key.shape[2]
@@ -136,7 +138,7 @@ def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
 
 def _decode_max_rows(dtype) -> int:
     """Packed query rows per KV head the split-KV decode takes in ``dtype``."""
-    return DECODE_MAX_ROWS if dtype == torch.bfloat16 else DECODE_MAX_ROWS_F32
+    return DECODE_MAX_ROWS if dtype in HALF_DTYPES else DECODE_MAX_ROWS_F32
 
 
 def _int_tensor(x, shape, device):
@@ -199,7 +201,7 @@ def _score_mods(lm: LoweredMask, lb: LoweredBias | None, B, l_q, l_k, h_q, devic
 def _flash_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None, check_dim: bool = True):
     """Arguments of the flash forward for this call, or None (``check_dim``:
     the head dim must be a flash kernel width)."""
-    if query.dtype not in (torch.bfloat16, torch.float32):
+    if query.dtype not in KERNEL_DTYPES:
         return None
     B, l_q, h_q, d = query.shape
     l_k = key.shape[1]
@@ -286,7 +288,7 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if lm is None or lm.causal or lm.extended or lm.q_valid is not None or lm.kv_valid is not None:
         return False
-    if q.dtype not in (torch.bfloat16, torch.float32) or _decode_width(q.shape[-1]) is None:
+    if q.dtype not in KERNEL_DTYPES or _decode_width(q.shape[-1]) is None:
         return False
     if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or \
             (q.shape[2] // k.shape[2]) * q.shape[1] > _decode_max_rows(q.dtype):
@@ -349,8 +351,8 @@ def _needs_grad(*ts) -> bool:
 
 def _kernel_width(d: int, dtype=torch.bfloat16):
     """The flash kernels' head dim that carries head dim ``d`` in ``dtype``
-    (None: too wide): 64, 128, or 256 in bfloat16."""
-    widths = FLASH_HEAD_DIMS if dtype == torch.bfloat16 else FLASH_HEAD_DIMS_F32
+    (None: too wide): 64, 128, or 256 in bfloat16 / float16."""
+    widths = FLASH_HEAD_DIMS if dtype in HALF_DTYPES else FLASH_HEAD_DIMS_F32
     return next((w for w in widths if w >= d), None)
 
 
@@ -478,13 +480,13 @@ def _unsupported_message(q, k, mask, bias, dropout_rate) -> str:
         why.append(f"mask {type(mask).__name__} is not supported")
     if lower_bias(bias) is False:
         why.append(f"bias {type(bias).__name__} is not supported")
-    if getattr(q, "dtype", None) not in (torch.bfloat16, torch.float32):
-        why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp32)")
+    if getattr(q, "dtype", None) not in KERNEL_DTYPES:
+        why.append(f"dtype {getattr(q, 'dtype', None)} is not supported (bf16, fp16, fp32)")
     if _needs_grad(q, k) and getattr(q, "dtype", None) not in BACKWARD_DTYPES:
         why.append(f"gradients need {BACKWARD_DTYPES} inputs (got {getattr(q, 'dtype', None)})")
     if q.ndim == 4 and _kernel_width(q.shape[-1], getattr(q, "dtype", None)) is None:
-        why.append(f"head_dim {q.shape[-1]} is not supported (at most {FLASH_HEAD_DIMS[-1]} in bfloat16, "
-                   f"{FLASH_HEAD_DIMS_F32[-1]} in float32)")
+        why.append(f"head_dim {q.shape[-1]} is not supported (at most {FLASH_HEAD_DIMS[-1]} in bfloat16 / "
+                   f"float16, {FLASH_HEAD_DIMS_F32[-1]} in float32)")
     detail = "; ".join(why) or "unsupported shape combination"
     return f"the HIP attention kernels cannot compute this call exactly: {detail}"
 
@@ -576,11 +578,11 @@ def _mla_materialized(q, cache, wk, wv, *, mask, bias, sm_scale):
     dv_dim = wv.shape[1]
     width = _kernel_width(max(dk_dim, dv_dim), q.dtype)
     if width is None:
-        top = (FLASH_HEAD_DIMS if q.dtype == torch.bfloat16 else FLASH_HEAD_DIMS_F32)[-1]
+        top = (FLASH_HEAD_DIMS if q.dtype in HALF_DTYPES else FLASH_HEAD_DIMS_F32)[-1]
         raise ValueError(f"materialised mla supports head dims up to {top} in {q.dtype}, "
                          f"got qk {dk_dim}, v {dv_dim}")
     if not (q.dtype == cache.dtype == wk.dtype == wv.dtype) or q.dtype not in BACKWARD_DTYPES:
-        raise ValueError("materialised mla takes q, cache, wk and wv of one dtype (bfloat16 or float32)")
+        raise ValueError("materialised mla takes q, cache, wk and wv of one dtype (bfloat16, float16 or float32)")
     if not all(hip_device(t) and t.device == q.device for t in (cache, wk, wv)):
         raise ValueError(f"the HIP latent-attention kernels need tensors on a {HIP_ARCH} ROCm device")
     with torch.no_grad():
@@ -613,7 +615,7 @@ def _mla_absorbed_lengths(q, cache, wk, wv, mask, bias):
     R, dv = cache.shape[-1], wv.shape[1]
     if bias is not None or _needs_grad(q, cache, wk, wv):
         return None
-    if not (q.dtype == cache.dtype == wk.dtype == wv.dtype == torch.bfloat16):
+    if not (q.dtype == cache.dtype == wk.dtype == wv.dtype) or q.dtype not in HALF_DTYPES:
         return None
     if (R, R) not in MLA_SHAPES or l_q * H > MLA_DECODE_MAX_ROWS:
         return None
@@ -663,7 +665,7 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     which is all a caller that multiplies by ``W_UV`` of width ``v_dim``
     needs), any query length, every mask and bias of the flash route,
     differentiable in ``q`` and ``cache`` (bias data gets no gradient, as in
-    the reference's VJP); latent widths up to 576 in bfloat16 (up to 128 in
+    the reference's VJP); latent widths up to 576 in bfloat16 / float16 (up to 128 in
     float32).  Decode steps (``Q * H <= 16``, no gradient, no bias,
     ``None`` / ``KVLenMask``) run the split-KV latent kernel; the rest the
     latent flash kernels, whose heads share one K = V head (the folded
@@ -729,12 +731,12 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
 def _latent_decode_lengths(q, cache, mask, bias, dv):
     """Per-batch KV lengths ("all" for none) when an absorbed call is a decode
     step the split-KV latent kernel computes exactly (no gradient, no bias,
-    ``None`` / ``KVLenMask`` / one-row ``KeyPaddingMask``, bf16, a rank and
+    ``None`` / ``KVLenMask`` / one-row ``KeyPaddingMask``, bf16 / fp16, a rank and
     output width it carries, ``Lq * H <= 16``); else None."""
     B, l_q, H, R = q.shape
     if bias is not None or _needs_grad(q, cache):
         return None
-    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
+    if q.dtype != cache.dtype or q.dtype not in HALF_DTYPES:
         return None
     if (R, dv) not in MLA_SHAPES or l_q * H > MLA_DECODE_MAX_ROWS:
         return None
@@ -755,11 +757,11 @@ def _latent_decode_lengths(q, cache, mask, bias, dv):
 
 def _latent_width(r: int, dtype):
     """The kernel rank that carries latent width ``r`` (zero-padded): a flash
-    head width up to 256, else 512 or 576 (bfloat16); None when too wide."""
+    head width up to 256, else 512 or 576 (bfloat16 / float16); None when too wide."""
     w = _kernel_width(r, dtype)
     if w is not None:
         return w
-    if dtype != torch.bfloat16:
+    if dtype not in HALF_DTYPES:
         return None
     return next((x for x in LATENT_WIDTHS if x >= r), None)
 
@@ -790,7 +792,7 @@ def _mla_latent(q, cache, *, mask, bias, sm_scale, v_dim):
     """Absorbed ``mla`` for any query length, mask and bias (latent_attention.py:
     79-197, 636-766), with the reference's gradient.  Latent widths up to 256
     run the flash kernels with the latent as one shared K = V head (torch
-    autograd adds the dK and dV of that one tensor); 512 and 576 (bfloat16)
+    autograd adds the dK and dV of that one tensor); 512 and 576 (bfloat16 / float16)
     run the wide latent kernels.  A width between kernel ranks is zero-padded
     (zero features change no score and add zero output columns)."""
     B, l_q, H, R = q.shape
@@ -799,7 +801,7 @@ def _mla_latent(q, cache, *, mask, bias, sm_scale, v_dim):
     width = _latent_width(R, q.dtype)
     if width is None:
         raise ValueError(f"absorbed mla supports latent widths up to {FLASH_HEAD_DIMS_F32[-1]} in float32 and "
-                         f"{LATENT_WIDTHS[-1]} in bfloat16, got {R} ({q.dtype})")
+                         f"{LATENT_WIDTHS[-1]} in bfloat16 / float16, got {R} ({q.dtype})")
     if width <= FLASH_HEAD_DIMS[-1]:
         c4 = cache[:, :, None, :]
         e = _eligible(q, c4, c4, mask=mask, bias=bias, dropout_rate=0.0)

@@ -21,6 +21,8 @@
 //     softmax redundantly, and multiplies its own share of the output dims:
 //     O^T[d][row] += V^T P^T, with V^T read as one 16-byte LDS load per step;
 //   * the merge kernel combines the chunks of one (batch, group) exactly.
+// Inputs are bf16 or fp16 (the kernels are templated on the 16-bit format;
+// the v_mfma_*_bf16 named here are v_mfma_*_f16 for fp16) or fp32 (GQA only).
 #include <stdio.h>
 
 #include <atomic>
@@ -35,12 +37,13 @@ constexpr int kTile = 64;       // keys per latent tile (16 per wave)
 constexpr int kRows = 16;       // query rows per MFMA column block
 
 struct DecodeArgs {
-  const uint16_t* q;   // bf16 (fp32 decode: the same pointers hold floats)
+  const uint16_t* q;   // bf16 / fp16 (fp32 decode: the same pointers hold floats)
   const uint16_t* k;
   const uint16_t* v;
   const int32_t* lengths;
-  uint16_t* o;         // bf16 output, or null with o32
+  uint16_t* o;         // 16-bit output (bf16, or fp16 when f16), or null with o32
   float* o32;          // fp32 output of the fp32 decode, else null
+  int f16;             // 16-bit inputs and output are fp16 (else bf16)
   float* lse;
   float* ws_o;   // [B*G][nch][rows][dv] unnormalised partial outputs
   float* ws_ml;  // [B*G][nch][rows][2]  running max (log2 units), sum
@@ -77,7 +80,7 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-// Writes the combined result of one work item: the final bf16 output and LSE
+// Writes the combined result of one work item: the final 16-bit output and LSE
 // when the item covers the whole sequence, else the unnormalised partial
 // (O relative to max M, plus M and the sum) for the merge kernel.
 __device__ __forceinline__ void emit_row_elem(const DecodeArgs& a, int b, int g, int r, int d,
@@ -91,7 +94,7 @@ __device__ __forceinline__ void emit_row_elem(const DecodeArgs& a, int b, int g,
     if (a.o32)
       a.o32[oi] = out;
     else
-      a.o[oi] = __builtin_bit_cast(uint16_t, (__bf16)out);
+      a.o[oi] = a.f16 ? F16Fmt::bits(out) : Bf16Fmt::bits(out);
     if (a.lse && d == 0)
       a.lse[((size_t)b * a.Hq + h) * a.Lq + t] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : INFINITY;
   } else {
@@ -191,7 +194,8 @@ __device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g,
     if (a.o32) {
       *(f32x4*)(a.o32 + oi) = O * inv;
     } else {
-      const u32x2 pk = {pack_bf16x2(O[0] * inv, O[1] * inv), pack_bf16x2(O[2] * inv, O[3] * inv)};
+      const u32x2 pk = a.f16 ? u32x2{F16Fmt::pack2(O[0] * inv, O[1] * inv), F16Fmt::pack2(O[2] * inv, O[3] * inv)}
+                             : u32x2{Bf16Fmt::pack2(O[0] * inv, O[1] * inv), Bf16Fmt::pack2(O[2] * inv, O[3] * inv)};
       *(u32x2*)(a.o + oi) = pk;
     }
     if (a.lse && d == 0)
@@ -265,13 +269,13 @@ __device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, co
 template <int NRB>
 constexpr int decode_occupancy() { return NRB == 4 ? 1 : 2; }
 
-template <int D, int NRB>
+template <typename E, int D, int NRB>
 __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int KSTEPS = D / 32;  // 32-dim MFMA k-steps of Q.K
   constexpr int NDB = D / 16;     // 16-dim output blocks
   constexpr int DC = D / 8;       // 16-byte chunks per row
   constexpr int VU = D / 64;      // (4 keys x 8 dims) V units per lane per 32 keys
-  constexpr int VTS = 36;         // V^T row stride (bf16): 32 keys + 4 pad
+  constexpr int VTS = 36;         // V^T row stride (16-bit elements): 32 keys + 4 pad
   static_assert(D % 64 == 0, "head dim");
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[4 * D * VTS];
   static_assert(4 * D * VTS * 2 >= 4 * 16 * D * 4 + 4 * 16 * 2 * 4, "combine scratch fits");
@@ -290,7 +294,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
   const int w0 = c0 + w * per_wave;
   const int w1 = min(w0 + per_wave, L);
 
-  bf16x8 qf[NRB][KSTEPS];
+  typename E::v8 qf[NRB][KSTEPS];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
     const int row = 16 * rb + c16;
@@ -302,7 +306,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
     for (int s = 0; s < KSTEPS; ++s) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (rv) r = *(const u32x4*)(qrow + 32 * s + 8 * q4);
-      qf[rb][s] = as_bf16x8(r);
+      qf[rb][s] = E::as8(r);
     }
   }
   const size_t kv_tok = (size_t)a.G * D;
@@ -389,7 +393,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
       for (int kb = 0; kb < 2; ++kb) {
         s[rb][kb] = f32x4{};
 #pragma unroll
-        for (int st = 0; st < KSTEPS; ++st) s[rb][kb] = mfma16x16x32(as_bf16x8(kr[kb][st]), qf[rb][st], s[rb][kb]);
+        for (int st = 0; st < KSTEPS; ++st) s[rb][kb] = E::mma16(E::as8(kr[kb][st]), qf[rb][st], s[rb][kb]);
       }
     if (kn < w1) load_k(kn);
     if (kn > w1) {
@@ -402,7 +406,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
             if (k0 + 16 * kb + 4 * q4 + r >= w1) s[rb][kb][r] = -INFINITY;
     }
     float corr[NRB];
-    bf16x8 pf[NRB];
+    typename E::v8 pf[NRB];
 #pragma unroll
     for (int rb = 0; rb < NRB; ++rb) {
       float mx = -INFINITY;
@@ -426,11 +430,11 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
       l_run[rb] = fmaf(l_run[rb], corr[rb], rs);
       // P^T as the B operand: slot j < 4 <-> key 4*q4 + j, slot j >= 4 <-> key 16 + 4*q4 + j - 4.
       u32x4 pk;
-      pk[0] = pack_bf16x2(s[rb][0][0], s[rb][0][1]);
-      pk[1] = pack_bf16x2(s[rb][0][2], s[rb][0][3]);
-      pk[2] = pack_bf16x2(s[rb][1][0], s[rb][1][1]);
-      pk[3] = pack_bf16x2(s[rb][1][2], s[rb][1][3]);
-      pf[rb] = as_bf16x8(pk);
+      pk[0] = E::pack2(s[rb][0][0], s[rb][0][1]);
+      pk[1] = E::pack2(s[rb][0][2], s[rb][0][3]);
+      pk[2] = E::pack2(s[rb][1][0], s[rb][1][1]);
+      pk[3] = E::pack2(s[rb][1][2], s[rb][1][3]);
+      pf[rb] = E::as8(pk);
     }
     wave_lds_sync();
 #pragma unroll
@@ -442,7 +446,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb) {
         acc[rb][db] *= corr[rb];
-        acc[rb][db] = mfma16x16x32(as_bf16x8(av), pf[rb], acc[rb][db]);
+        acc[rb][db] = E::mma16(E::as8(av), pf[rb], acc[rb][db]);
       }
     }
     wave_lds_sync();
@@ -635,7 +639,7 @@ struct LatentTile {
   }
 };
 
-template <int D, int DV>
+template <typename E, int D, int DV>
 __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a) {
   using T = LatentTile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, NLD = T::NLD, GRP = T::GRP;
@@ -662,7 +666,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
   const int n_tiles = (c1 - c0 + BK - 1) / BK;
 
   // Q^T as the B operand: lane holds query row c16, dims 32*s + 8*q4 + [0,8).
-  bf16x8 qf[KSTEPS];
+  typename E::v8 qf[KSTEPS];
   {
     const bool rv = c16 < a.rows;
     int t = 0, h = 0;
@@ -672,7 +676,7 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
     for (int s = 0; s < KSTEPS; ++s) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (rv) r = *(const u32x4*)(qrow + 32 * s + 8 * q4);
-      qf[s] = as_bf16x8(r);
+      qf[s] = E::as8(r);
     }
   }
   const unsigned char* Kb = (const unsigned char*)a.k + (size_t)b * a.Lk * ROWB;
@@ -726,8 +730,8 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
     f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int st = 0; st < KSTEPS; ++st) {
-      const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + offK[st % SPG] + 16 * GRP * (st / SPG)));
-      s = mfma16x16x32(kf, qf[st], s);
+      const typename E::v8 kf = E::as8(*(const u32x4*)(ks + offK[st % SPG] + 16 * GRP * (st / SPG)));
+      s = E::mma16(kf, qf[st], s);
     }
     if (k0 + BK > c1) {
       const int lim = c1 - (k0 + 16 * w + 4 * q4);
@@ -750,12 +754,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
 #pragma unroll
     for (int r = 0; r < 4; ++r) p[r] = fast_exp2(fmaf(s[r], a.cx, -m_run));
     l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    const u32x2 pk = {pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+    const u32x2 pk = {E::pack2(p[0], p[1]), E::pack2(p[2], p[3])};
     const s16x4 pb = __builtin_bit_cast(s16x4, pk);
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
       const u32x2 av = lds_read_tr16(ks + offV[dt % DPG] + 16 * GRP * (dt / DPG));
-      acc[dt] = mfma16x16x16(__builtin_bit_cast(s16x4, av), pb, acc[dt]);
+      acc[dt] = E::mma16k16(__builtin_bit_cast(s16x4, av), pb, acc[dt]);
     }
   };
 
@@ -913,7 +917,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
   if (a.o32) {
     *(f32x4*)(a.o32 + oi) = num * inv;
   } else {
-    const u32x2 pk = {pack_bf16x2(num[0] * inv, num[1] * inv), pack_bf16x2(num[2] * inv, num[3] * inv)};
+    const u32x2 pk = a.f16 ? u32x2{F16Fmt::pack2(num[0] * inv, num[1] * inv), F16Fmt::pack2(num[2] * inv, num[3] * inv)}
+                           : u32x2{Bf16Fmt::pack2(num[0] * inv, num[1] * inv), Bf16Fmt::pack2(num[2] * inv, num[3] * inv)};
     *(u32x2*)(a.o + oi) = pk;
   }
   if (a.lse && u == 0)
@@ -971,6 +976,31 @@ static int run_decode(K kernel, DecodeArgs& a, void* workspace, size_t ws_bytes,
   return check_launch(name);
 }
 
+// The 16-bit GQA decode (format E) with nrb 16-row blocks.
+template <typename E>
+static int run_gqa_h16(DecodeArgs& a, int head_dim, int nrb, void* ws, size_t ws_bytes, hipStream_t s,
+                       const char* who) {
+  if (head_dim == 128) {
+    if (nrb == 1) return run_decode(gqa_decode_kernel<E, 128, 1>, a, ws, ws_bytes, s, who);
+    if (nrb == 2) return run_decode(gqa_decode_kernel<E, 128, 2>, a, ws, ws_bytes, s, who);
+    return run_decode(gqa_decode_kernel<E, 128, 4>, a, ws, ws_bytes, s, who);
+  }
+  if (nrb == 1) return run_decode(gqa_decode_kernel<E, 64, 1>, a, ws, ws_bytes, s, who);
+  if (nrb == 2) return run_decode(gqa_decode_kernel<E, 64, 2>, a, ws, ws_bytes, s, who);
+  return run_decode(gqa_decode_kernel<E, 64, 4>, a, ws, ws_bytes, s, who);
+}
+
+// The latent decode (format E) at one (rank, v_dim).
+template <typename E>
+static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, size_t ws_bytes, hipStream_t s) {
+  const char* who = "pjx_mla_decode";
+  if (rank == 576 && v_dim == 512) return run_decode(mla_decode_kernel<E, 576, 512>, a, ws, ws_bytes, s, who);
+  if (rank == 576 && v_dim == 576) return run_decode(mla_decode_kernel<E, 576, 576>, a, ws, ws_bytes, s, who);
+  if (rank == 512 && v_dim == 512) return run_decode(mla_decode_kernel<E, 512, 512>, a, ws, ws_bytes, s, who);
+  if (rank == 128 && v_dim == 128) return run_decode(mla_decode_kernel<E, 128, 128>, a, ws, ws_bytes, s, who);
+  return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
+}
+
 }  // namespace pjx
 
 using namespace pjx;
@@ -987,8 +1017,8 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
                                   int64_t kv_heads, int64_t head_dim, float sm_scale,
                                   int64_t chunk, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
   const bool f32 = dtype == PJX_DTYPE_F32;
   if (!q || !k || !v || !o) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: null pointer");
   if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
@@ -1011,6 +1041,7 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
     a.o32 = (float*)o;
   else
     a.o = (uint16_t*)o;
+  a.f16 = dtype == PJX_DTYPE_F16;
   a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len; a.Hq = (int)q_heads; a.G = (int)kv_heads;
   a.rows = (int)rows; a.fold = 0; a.chunk = (int)chunk;
   a.nch = (int)std::max<int64_t>((kv_len + chunk - 1) / chunk, 1);
@@ -1025,14 +1056,8 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
     return nrb == 1 ? run_decode(gqa_decode_f32_kernel<64, 1>, a, workspace, workspace_bytes, s, who)
                     : run_decode(gqa_decode_f32_kernel<64, 2>, a, workspace, workspace_bytes, s, who);
   }
-  if (head_dim == 128) {
-    if (nrb == 1) return run_decode(gqa_decode_kernel<128, 1>, a, workspace, workspace_bytes, s, who);
-    if (nrb == 2) return run_decode(gqa_decode_kernel<128, 2>, a, workspace, workspace_bytes, s, who);
-    return run_decode(gqa_decode_kernel<128, 4>, a, workspace, workspace_bytes, s, who);
-  }
-  if (nrb == 1) return run_decode(gqa_decode_kernel<64, 1>, a, workspace, workspace_bytes, s, who);
-  if (nrb == 2) return run_decode(gqa_decode_kernel<64, 2>, a, workspace, workspace_bytes, s, who);
-  return run_decode(gqa_decode_kernel<64, 4>, a, workspace, workspace_bytes, s, who);
+  return a.f16 ? run_gqa_h16<F16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who)
+               : run_gqa_h16<Bf16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who);
 }
 
 // ---------------------------------------------------------------------------
@@ -1104,7 +1129,8 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
                               int64_t heads, int64_t kv_len, int64_t rank, int64_t v_dim,
                               float sm_scale, int64_t chunk, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_mla_decode: only bf16 is supported");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16)
+    return fail(PJX_ERR_INVALID, "pjx_mla_decode: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F16");
   if (!q || !cache || !o) return fail(PJX_ERR_INVALID, "pjx_mla_decode: null pointer");
   if (batch < 0 || q_len <= 0 || heads <= 0 || kv_len < 0) return fail(PJX_ERR_INVALID, "pjx_mla_decode: bad sizes");
   if (q_len * heads > kRows) return fail(PJX_ERR_INVALID, "pjx_mla_decode: Lq*H must be <= 16");
@@ -1122,9 +1148,7 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   a.dv = (int)v_dim; a.cx = sm_scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (batch == 0) return PJX_OK;
-  if (rank == 576 && v_dim == 512) return run_decode(mla_decode_kernel<576, 512>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 576 && v_dim == 576) return run_decode(mla_decode_kernel<576, 576>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 512 && v_dim == 512) return run_decode(mla_decode_kernel<512, 512>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  if (rank == 128 && v_dim == 128) return run_decode(mla_decode_kernel<128, 128>, a, workspace, workspace_bytes, s, "pjx_mla_decode");
-  return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
+  a.f16 = dtype == PJX_DTYPE_F16;
+  return a.f16 ? run_mla_h16<F16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s)
+               : run_mla_h16<Bf16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s);
 }

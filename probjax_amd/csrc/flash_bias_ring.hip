@@ -1,4 +1,4 @@
-// Flash-attention forward for gfx950, bf16 with a dense fp32 bias: the LDS
+// Flash-attention forward for gfx950, bf16 / fp16 with a dense fp32 bias: the LDS
 // ring kernel (semantics as flash_fwd.hip's kernels: scores sm_scale * q.k in
 // fp32, then the bias, then the mask; probjax's XLA attention reference,
 // probjax/nn/pallas_kernels/kernels/attention_xla.py:339-429, with DenseBias
@@ -52,7 +52,7 @@ struct BiasRing {
   static_assert(NP >= 2, "ring depth");
 };
 
-template <int D>
+template <typename E, int D>
 __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kernel(FlashArgs a) {
   using T = Bf16Tile<D, 32>;
   using R = BiasRing<D>;
@@ -78,7 +78,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   const bool row_in = g.qi < a.Lq;
   const bool row_ok = g.qi < g.q_hi;
 
-  bf16x8 qf[D / 16];
+  typename E::v8 qf[D / 16];
   {
     const uint16_t* qrow =
         (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
     for (int s = 0; s < D / 16; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_in) raw = *(const u32x4*)(qrow + 16 * s + 8 * half);
-      qf[s] = as_bf16x8(raw);
+      qf[s] = E::as8(raw);
     }
   }
 
@@ -164,8 +164,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
     f32x16 s = f32x16{};
 #pragma unroll
     for (int st = 0; st < D / 16; ++st) {
-      const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + offK[st]));
-      s = mfma32x32x16(kf, qf[st], s);
+      const typename E::v8 kf = E::as8(*(const u32x4*)(ks + offK[st]));
+      s = E::mma32(kf, qf[st], s);
     }
     // Register r holds key k0 + 8*(r/4) + 4*half + r%4: bias chunk
     // 2*(r/4) + half of this lane's row.
@@ -208,13 +208,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
       s[r] = pv;
     }
     l_run += rs;
-    bf16x8 pf[2];
+    typename E::v8 pf[2];
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
       u32x4 pk;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(s[8 * c + 2 * j], s[8 * c + 2 * j + 1]);
-      pf[c] = as_bf16x8(pk);
+      for (int j = 0; j < 4; ++j) pk[j] = E::pack2(s[8 * c + 2 * j], s[8 * c + 2 * j + 1]);
+      pf[c] = E::as8(pk);
     }
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
@@ -223,7 +223,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
         const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + offV[db]);
         const u32x2 hi = lds_read_tr16(vs + (16 * c + 8) * ROWB + offV[db]);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+        acc[db] = E::mma32(E::as8(av), pf[c], acc[db]);
       }
     }
   };
@@ -293,8 +293,8 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
-        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        pk[0] = E::pack2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = E::pack2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
       }
     if (a.lse && half == 0)
@@ -302,12 +302,20 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   }
 }
 
-int launch_flash_bias_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {
+template <typename E>
+static void launch_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   if (head_dim == 128)
-    hipLaunchKernelGGL(flash_fwd_bf16_bias_ring_kernel<128>, dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
+    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 128>), dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
   else
-    hipLaunchKernelGGL(flash_fwd_bf16_bias_ring_kernel<64>, dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
+    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64>), dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
+}
+
+int launch_flash_bias_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {
+  if (a.f16)
+    launch_ring<F16Fmt>(head_dim, a, stream);
+  else
+    launch_ring<Bf16Fmt>(head_dim, a, stream);
   return check_launch("pjx_flash_fwd");
 }
 

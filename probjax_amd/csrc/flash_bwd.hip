@@ -1,4 +1,4 @@
-// Flash-attention backward for gfx950 (bf16 or fp32 inputs, fp32 accumulation).
+// Flash-attention backward for gfx950 (bf16, fp16 or fp32 inputs, fp32 accumulation).
 //
 // Replaces the Pallas backward of probjax's `mha`:
 //   _preprocess_backward_kernel (probjax/nn/pallas_kernels/kernels/attention.py:853-867)
@@ -7,7 +7,8 @@
 // with the math of those kernels:
 //   delta = sum_d o * do;  p = exp2(s * log2e - lse * log2e);  dp = do . v^T
 //   ds = p * (dp - delta) * sm_scale
-//   dv = sum_q bf16(p)^T do,  dk = sum_q bf16(ds)^T q,  dq = sum_k bf16(ds) k.
+//   dv = sum_q r(p)^T do,  dk = sum_q r(ds)^T q,  dq = sum_k r(ds) k,
+// r() rounding to the input's 16-bit format (bf16 or fp16; none in fp32).
 // s is the forward's score: sm_scale * q.k [+ bias], masked keys excluded.
 // lse is the forward's natural-log residual (+inf for rows without a valid
 // key: p = 0 there, so those rows contribute nothing).
@@ -26,7 +27,7 @@
 //     LDS.  S = Q K^T and dP = dO V^T put queries on the MFMA rows, so P and
 //     dS in registers are directly the B operands of dV^T += dO^T P and
 //     dK^T += Q^T dS (dO^T and Q^T by transposing LDS reads).  The group's
-//     query heads accumulate in fp32 before the single rounding to bf16.
+//     query heads accumulate in fp32 before the single rounding to 16 bits.
 //
 // LDS tiles (both kernels) are row-major [row][dim] with 16-byte chunks
 // XOR-swizzled so that both reads of a tile are free of bank conflicts: the
@@ -91,26 +92,24 @@ struct BwdOffsets {
 
 // A operand X^T (dims 32*db.., 16 rows starting at row0 in slot order
 // 8*(j/4) + 4*half + j%4) from a row-major tile.
-template <int D>
-__device__ __forceinline__ bf16x8 read_t(const unsigned char* tile, int row0, uint32_t lo, uint32_t hi) {
+template <typename E, int D>
+__device__ __forceinline__ typename E::v8 read_t(const unsigned char* tile, int row0, uint32_t lo, uint32_t hi) {
   const unsigned char* p = tile + row0 * BwdTile<D>::ROWB;
   const u32x2 a = lds_read_tr16(p + lo);
   const u32x2 b = lds_read_tr16(p + hi);
   const u32x4 v = {a[0], a[1], b[0], b[1]};
-  return as_bf16x8(v);
+  return E::as8(v);
 }
 
 // Registers of a 32x32 C block as the B operand of the next product:
-// k-step c (16 rows) holds registers 8c .. 8c+7, rounded to bf16.
-__device__ __forceinline__ bf16x8 pack_step(const f32x16& x, int c) {
+// k-step c (16 rows) holds registers 8c .. 8c+7, rounded to the 16-bit format.
+template <typename E>
+__device__ __forceinline__ typename E::v8 pack_step(const f32x16& x, int c) {
   u32x4 pk;
 #pragma unroll
-  for (int j = 0; j < 4; ++j) pk[j] = pack_bf16x2(x[8 * c + 2 * j], x[8 * c + 2 * j + 1]);
-  return as_bf16x8(pk);
+  for (int j = 0; j < 4; ++j) pk[j] = E::pack2(x[8 * c + 2 * j], x[8 * c + 2 * j + 1]);
+  return E::as8(pk);
 }
-
-__device__ __forceinline__ float bf16_lo(uint32_t x) { return __uint_as_float(x << 16); }
-__device__ __forceinline__ float bf16_hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
 // dL/d(bias) of one key tile in the S^T layout (lane = query g.qi, register
 // r of block kb = key k0 + kb*32 + 8*(r/4) + 4*half + r%4): 4 consecutive
@@ -142,7 +141,7 @@ __device__ __forceinline__ void store_dbias(const FlashBwdArgs& ba, const BlockG
 // ---------------------------------------------------------------------------
 // dQ (and delta): one workgroup per (128-query tile, batch, head).
 // ---------------------------------------------------------------------------
-template <int D, int BIAS, int EXT>
+template <typename E, int D, int BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
   // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
   constexpr bool HB = BIAS != 0, DB = BIAS == 2;
@@ -166,7 +165,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 
   // Q^T and dO^T as B operands (lane: query `col`, dims 16*s + 8*half + [0,8)),
   // and delta = sum_d o*do of this query over both halves.
-  bf16x8 qf[D / 16], dof[D / 16];
+  typename E::v8 qf[D / 16], dof[D / 16];
   float dsum = 0.f;
   {
     const size_t roff = ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
@@ -181,11 +180,11 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         rd = *(const u32x4*)(drow + 16 * s + 8 * half);
         ro = *(const u32x4*)(orow + 16 * s + 8 * half);
       }
-      qf[s] = as_bf16x8(rq);
-      dof[s] = as_bf16x8(rd);
+      qf[s] = E::as8(rq);
+      dof[s] = E::as8(rd);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        dsum = fmaf(bf16_lo(ro[j]), bf16_lo(rd[j]), fmaf(bf16_hi(ro[j]), bf16_hi(rd[j]), dsum));
+        dsum = fmaf(E::lo(ro[j]), E::lo(rd[j]), fmaf(E::hi(ro[j]), E::hi(rd[j]), dsum));
     }
   }
   const float delta = xor32_sum(dsum);
@@ -257,13 +256,13 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
       dp[kb] = f32x16{};
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + off.row[st]));
-        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+        const typename E::v8 kf = E::as8(*(const u32x4*)(ks + kb * 32 * ROWB + off.row[st]));
+        s[kb] = E::mma32(kf, qf[st], s[kb]);
       }
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 vf = as_bf16x8(*(const u32x4*)(vs + kb * 32 * ROWB + off.row[st]));
-        dp[kb] = mfma32x32x16(vf, dof[st], dp[kb]);
+        const typename E::v8 vf = E::as8(*(const u32x4*)(vs + kb * 32 * ROWB + off.row[st]));
+        dp[kb] = E::mma32(vf, dof[st], dp[kb]);
       }
     }
     f32x16 dbv[DB ? BK / 32 : 1];  // dL/d(bias) = P (dP - delta), kept for the store
@@ -303,7 +302,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
         for (int r = 0; r < 16; ++r)
           if (kb * 32 + 8 * (r >> 2) + (r & 3) > lim) s[kb][r] = -INFINITY;
     }
-    // dS^T = P^T (dP^T - delta) * scale, rounded to bf16 as the B operand.
+    // dS^T = P^T (dP^T - delta) * scale, rounded to 16 bits as the B operand.
 #pragma unroll
     for (int kb = 0; kb < BK / 32; ++kb)
 #pragma unroll
@@ -315,15 +314,15 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
       }
     }
     if constexpr (DB) store_dbias<BK / 32>(ba, g, dbv, k0, half, row_in);
-    bf16x8 dsf[BK / 16];
+    typename E::v8 dsf[BK / 16];
 #pragma unroll
-    for (int c = 0; c < BK / 16; ++c) dsf[c] = pack_step(s[c >> 1], c & 1);
+    for (int c = 0; c < BK / 16; ++c) dsf[c] = pack_step<E>(s[c >> 1], c & 1);
     // dQ^T[d][query] += K^T dS^T
 #pragma unroll
     for (int db = 0; db < D / 32; ++db)
 #pragma unroll
       for (int c = 0; c < BK / 16; ++c)
-        acc[db] = mfma32x32x16(read_t<D>(ks, 16 * c, off.tlo[db], off.thi[db]), dsf[c], acc[db]);
+        acc[db] = E::mma32(read_t<E, D>(ks, 16 * c, off.tlo[db], off.thi[db]), dsf[c], acc[db]);
   };
 
   if (n_tiles > 0) issue(0, smem0);
@@ -346,8 +345,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[db][4 * gq], acc[db][4 * gq + 1]);
-        pk[1] = pack_bf16x2(acc[db][4 * gq + 2], acc[db][4 * gq + 3]);
+        pk[0] = E::pack2(acc[db][4 * gq], acc[db][4 * gq + 1]);
+        pk[1] = E::pack2(acc[db][4 * gq + 2], acc[db][4 * gq + 3]);
         *(u32x2*)(drow + db * 32 + 8 * gq + 4 * half) = pk;
       }
   }
@@ -356,7 +355,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 // ---------------------------------------------------------------------------
 // dK, dV: one workgroup per (128-key tile, batch, KV head).
 // ---------------------------------------------------------------------------
-template <int D, bool BIAS, int EXT>
+template <typename E, int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
@@ -408,7 +407,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
   const int n_tiles = G * n_qt;
 
   // K^T and V^T as B operands: lane holds key `key`, dims 16*s + 8*half + [0,8).
-  bf16x8 kf[D / 16], vf[D / 16];
+  typename E::v8 kf[D / 16], vf[D / 16];
   {
     const bool kin = key < a.Lk;
     const size_t koff = ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * D;
@@ -421,8 +420,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
         rk = *(const u32x4*)(krow + 16 * s + 8 * half);
         rv = *(const u32x4*)(vrow + 16 * s + 8 * half);
       }
-      kf[s] = as_bf16x8(rk);
-      vf[s] = as_bf16x8(rv);
+      kf[s] = E::as8(rk);
+      vf[s] = E::as8(rv);
     }
   }
   const float cx = (BIAS || EXT == 2) ? kLog2e : a.scale * kLog2e;
@@ -489,13 +488,13 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
         f32x16 sx = f32x16{}, dpx = f32x16{};
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8 qf = as_bf16x8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[kk]));
-          sx = mfma32x32x16(qf, kf[kk], sx);
+          const typename E::v8 qf = E::as8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[kk]));
+          sx = E::mma32(qf, kf[kk], sx);
         }
 #pragma unroll
         for (int kk = 0; kk < D / 16; ++kk) {
-          const bf16x8 df = as_bf16x8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[kk]));
-          dpx = mfma32x32x16(df, vf[kk], dpx);
+          const typename E::v8 df = E::as8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[kk]));
+          dpx = E::mma32(df, vf[kk], dpx);
         }
         const HeadMods hm = head_mods(a.m, h);
         ext_scores_S<BIAS>(a, b, hm, key, qlo, qhi, segk, sx, qs0, half, bbase,
@@ -507,12 +506,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
                            });
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
-          const bf16x8 pf = pack_step(sx, c);
-          const bf16x8 dsf = pack_step(dpx, c);
+          const typename E::v8 pf = pack_step<E>(sx, c);
+          const typename E::v8 dsf = pack_step<E>(dpx, c);
 #pragma unroll
           for (int db = 0; db < D / 32; ++db) {
-            accv[db] = mfma32x32x16(read_t<D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
-            acck[db] = mfma32x32x16(read_t<D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
+            accv[db] = E::mma32(read_t<E, D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
+            acck[db] = E::mma32(read_t<E, D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
           }
         }
         continue;
@@ -524,8 +523,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
       f32x16 s = f32x16{};
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
-        const bf16x8 qf = as_bf16x8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[k]));
-        s = mfma32x32x16(qf, kf[k], s);
+        const typename E::v8 qf = E::as8(*(const u32x4*)(qs + qb * 32 * ROWB + off.row[k]));
+        s = E::mma32(qf, kf[k], s);
       }
       if constexpr (BIAS) {
 #pragma unroll
@@ -555,17 +554,17 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const bf16x8 pf = pack_step(s, c);
+        const typename E::v8 pf = pack_step<E>(s, c);
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
-          accv[db] = mfma32x32x16(read_t<D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
+          accv[db] = E::mma32(read_t<E, D>(dos, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), pf, accv[db]);
       }
       // dP = dO V^T; dS = P (dP - delta) * scale; dK^T[d][key] += Q^T dS
       f32x16 dp = f32x16{};
 #pragma unroll
       for (int k = 0; k < D / 16; ++k) {
-        const bf16x8 df = as_bf16x8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[k]));
-        dp = mfma32x32x16(df, vf[k], dp);
+        const typename E::v8 df = E::as8(*(const u32x4*)(dos + qb * 32 * ROWB + off.row[k]));
+        dp = E::mma32(df, vf[k], dp);
       }
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
@@ -575,10 +574,10 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        const bf16x8 dsf = pack_step(s, c);
+        const typename E::v8 dsf = pack_step<E>(s, c);
 #pragma unroll
         for (int db = 0; db < D / 32; ++db)
-          acck[db] = mfma32x32x16(read_t<D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
+          acck[db] = E::mma32(read_t<E, D>(qs, 32 * qb + 16 * c, off.tlo[db], off.thi[db]), dsf, acck[db]);
       }
     }
   };
@@ -606,10 +605,10 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk, pv;
-        pk[0] = pack_bf16x2(acck[db][4 * gq], acck[db][4 * gq + 1]);
-        pk[1] = pack_bf16x2(acck[db][4 * gq + 2], acck[db][4 * gq + 3]);
-        pv[0] = pack_bf16x2(accv[db][4 * gq], accv[db][4 * gq + 1]);
-        pv[1] = pack_bf16x2(accv[db][4 * gq + 2], accv[db][4 * gq + 3]);
+        pk[0] = E::pack2(acck[db][4 * gq], acck[db][4 * gq + 1]);
+        pk[1] = E::pack2(acck[db][4 * gq + 2], acck[db][4 * gq + 3]);
+        pv[0] = E::pack2(accv[db][4 * gq], accv[db][4 * gq + 1]);
+        pv[1] = E::pack2(accv[db][4 * gq + 2], accv[db][4 * gq + 3]);
         *(u32x2*)(dkrow + db * 32 + 8 * gq + 4 * half) = pk;
         *(u32x2*)(dvrow + db * 32 + 8 * gq + 4 * half) = pv;
       }
@@ -1079,32 +1078,44 @@ static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
 // dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
 // dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
 template <int D, int EXT>
-static int run_bwd_t(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
+static int run_bwd_f32(const FlashBwdArgs& a, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
-    int rc;
     const bool db = a.dbias != nullptr;
-    if (f32)
-      rc = db ? launch_dq(flash_bwd_dq_f32_kernel<D, 2, EXT>, a, s)
-         : hb ? launch_dq(flash_bwd_dq_f32_kernel<D, 1, EXT>, a, s)
-              : launch_dq(flash_bwd_dq_f32_kernel<D, 0, EXT>, a, s);
-    else
-      rc = db ? launch_dq(flash_bwd_dq_kernel<D, 2, EXT>, a, s)
-         : hb ? launch_dq(flash_bwd_dq_kernel<D, 1, EXT>, a, s)
-              : launch_dq(flash_bwd_dq_kernel<D, 0, EXT>, a, s);
+    const int rc = db ? launch_dq(flash_bwd_dq_f32_kernel<D, 2, EXT>, a, s)
+                 : hb ? launch_dq(flash_bwd_dq_f32_kernel<D, 1, EXT>, a, s)
+                      : launch_dq(flash_bwd_dq_f32_kernel<D, 0, EXT>, a, s);
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
-  if (f32)
-    return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true, EXT>, a, s)
-              : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false, EXT>, a, s);
-  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<D, true, EXT>, a, s)
-            : launch_dkdv(flash_bwd_dkdv_kernel<D, false, EXT>, a, s);
+  return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true, EXT>, a, s)
+            : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false, EXT>, a, s);
+}
+
+template <typename E, int D, int EXT>
+static int run_bwd_h16(const FlashBwdArgs& a, bool hb, hipStream_t s) {
+  if (a.f.Lq > 0) {
+    const bool db = a.dbias != nullptr;
+    const int rc = db ? launch_dq(flash_bwd_dq_kernel<E, D, 2, EXT>, a, s)
+                 : hb ? launch_dq(flash_bwd_dq_kernel<E, D, 1, EXT>, a, s)
+                      : launch_dq(flash_bwd_dq_kernel<E, D, 0, EXT>, a, s);
+    if (rc != PJX_OK) return rc;
+  }
+  if (a.f.Lk == 0) return PJX_OK;
+  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, D, true, EXT>, a, s)
+            : launch_dkdv(flash_bwd_dkdv_kernel<E, D, false, EXT>, a, s);
+}
+
+template <int D, int EXT>
+static int run_bwd_t(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
+  if (dtype == PJX_DTYPE_F32) return run_bwd_f32<D, EXT>(a, hb, s);
+  if (dtype == PJX_DTYPE_F16) return run_bwd_h16<F16Fmt, D, EXT>(a, hb, s);
+  return run_bwd_h16<Bf16Fmt, D, EXT>(a, hb, s);
 }
 
 template <int D>
-static int run_bwd(const FlashBwdArgs& a, bool f32, bool hb, hipStream_t s) {
-  if (a.f.ext == 2) return run_bwd_t<D, 2>(a, f32, hb, s);
-  return a.f.ext == 1 ? run_bwd_t<D, 1>(a, f32, hb, s) : run_bwd_t<D, 0>(a, f32, hb, s);
+static int run_bwd(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
+  if (a.f.ext == 2) return run_bwd_t<D, 2>(a, dtype, hb, s);
+  return a.f.ext == 1 ? run_bwd_t<D, 1>(a, dtype, hb, s) : run_bwd_t<D, 0>(a, dtype, hb, s);
 }
 
 }  // namespace pjx
@@ -1124,16 +1135,16 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
                              int64_t kv_heads, int64_t head_dim, int64_t q_valid, int64_t kv_valid,
                              int causal, float sm_scale, const pjx_score_mods* mods, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
   if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q, k, v, o, dout, lse, dq, dk, dv must be non-null");
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: negative or zero size");
   if (q_heads % kv_heads != 0)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q_heads must be a multiple of kv_heads");
-  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype == PJX_DTYPE_BF16))
-    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128 (or 256 in bf16)");
+  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PJX_DTYPE_F32))
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128 (or 256 in bf16 / fp16)");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sm_scale must be > 0");
   if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
@@ -1159,6 +1170,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
   a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
   a.causal = causal ? 1 : 0;
+  a.f16 = dtype == PJX_DTYPE_F16;
   a.scale = sm_scale;
   a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
   if ((long)a.n_qtiles * batch * q_heads > 0x7fffffffL ||
@@ -1187,6 +1199,5 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
   }
   const bool hb = bias != nullptr;
-  const bool f32 = dtype == PJX_DTYPE_F32;
-  return head_dim == 128 ? run_bwd<128>(ba, f32, hb, s) : run_bwd<64>(ba, f32, hb, s);
+  return head_dim == 128 ? run_bwd<128>(ba, dtype, hb, s) : run_bwd<64>(ba, dtype, hb, s);
 }

@@ -25,6 +25,7 @@ struct FlashArgs {
   int n_qtiles;
   int dv;       // output row width (elements per head); the wide kernels' V width
   int ext;      // 0: none; 1: interval masks in `m`; 2: also segment ids / score modifiers
+  int f16;      // 16-bit inputs are fp16 (else bf16); read by the host-side launchers only
   ScoreMods m;
 };
 

@@ -61,7 +61,7 @@ namespace pjx {
 // ---------------------------------------------------------------------------
 
 
-template <int D, bool BIAS, int EXT>
+template <typename E, int D, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a) {
   using T = Bf16Tile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
@@ -86,7 +86,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
   const bool row_ok = g.qi < g.q_hi;
 
   // Q^T as the B operand: lane holds query `col`, dims 16*s + 8*half + [0,8).
-  bf16x8 qf[D / 16];
+  typename E::v8 qf[D / 16];
   {
     const uint16_t* qrow =
         (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
@@ -94,7 +94,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
     for (int s = 0; s < D / 16; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_in) raw = *(const u32x4*)(qrow + 16 * s + 8 * half);
-      qf[s] = as_bf16x8(raw);
+      qf[s] = E::as8(raw);
     }
   }
   const float* brow = nullptr;
@@ -171,8 +171,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
       s[kb] = f32x16{};
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
-        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+        const typename E::v8 kf = E::as8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
+        s[kb] = E::mma32(kf, qf[st], s[kb]);
       }
     }
 
@@ -238,14 +238,14 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 
     // P^T as the B operand, 16 keys per MFMA step c:
     // slot j <-> key 16c + 8*(j/4) + 4*half + j%4 (registers 8*(c%2)+j of block c/2).
-    bf16x8 pf[BK / 16];
+    typename E::v8 pf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) {
       u32x4 pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
-      pf[c] = as_bf16x8(pk);
+        pk[j] = E::pack2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
+      pf[c] = E::as8(pk);
     }
     // O^T[d][query] += V^T P^T; A operand = V^T rows 32*db.., keys in P's slot order,
     // from two transposing reads (keys 16c + 4*half + [0,4) and 16c + 8 + 4*half + [0,4)).
@@ -256,7 +256,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
         const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + offV[db]);
         const u32x2 hi = lds_read_tr16(vs + (16 * c + 8) * ROWB + offV[db]);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+        acc[db] = E::mma32(E::as8(av), pf[c], acc[db]);
       }
     }
   };
@@ -287,8 +287,8 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
-        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        pk[0] = E::pack2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = E::pack2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
       }
     if (a.lse && half == 0)
@@ -313,7 +313,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 // it reads whatever the slot holds and is discarded, so the block stays
 // branch-free.
 // ---------------------------------------------------------------------------
-template <int D, int BKT, int WPC>
+template <typename E, int D, int BKT, int WPC>
 __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(FlashArgs a) {
   using T = Bf16Tile<D, BKT>;
   constexpr int RPW = BKT / 4;  // tile rows each wave loads
@@ -333,7 +333,7 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
   const bool row_in = g.qi < a.Lq;
   const bool row_ok = g.qi < g.q_hi;
 
-  bf16x8 qf[D / 16];
+  typename E::v8 qf[D / 16];
   {
     const uint16_t* qrow =
         (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
@@ -341,7 +341,7 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
     for (int s = 0; s < D / 16; ++s) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_in) raw = *(const u32x4*)(qrow + 16 * s + 8 * half);
-      qf[s] = as_bf16x8(raw);
+      qf[s] = E::as8(raw);
     }
   }
   const float cx = a.scale * kLog2e;
@@ -393,8 +393,8 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
       s[kb] = f32x16{};
 #pragma unroll
       for (int st = 0; st < D / 16; ++st) {
-        const bf16x8 kf = as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
-        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+        const typename E::v8 kf = E::as8(*(const u32x4*)(ks + kb * 32 * ROWB + offK[st]));
+        s[kb] = E::mma32(kf, qf[st], s[kb]);
       }
     }
   };
@@ -450,14 +450,14 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
         s[kb][r + 1] = p1;
       }
     l_run += rs0 + rs1;
-    bf16x8 pf[BK / 16];
+    typename E::v8 pf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) {
       u32x4 pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
-      pf[c] = as_bf16x8(pk);
+        pk[j] = E::pack2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
+      pf[c] = E::as8(pk);
     }
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
@@ -466,7 +466,7 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
         const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + offV[db]);
         const u32x2 hi = lds_read_tr16(vs + (16 * c + 8) * ROWB + offV[db]);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+        acc[db] = E::mma32(E::as8(av), pf[c], acc[db]);
       }
     }
   };
@@ -504,8 +504,8 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
-        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        pk[0] = E::pack2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = E::pack2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
       }
     if (a.lse && half == 0)
@@ -917,11 +917,38 @@ static int launch(K kernel, const FlashArgs& a, hipStream_t stream) {
 // steps between barriers hide latency better at that occupancy (measured:
 // 87 us against 113 us at B=1, H=16, L=4096 causal; 1-1.5% slower than
 // 32-key tiles from 1024 workgroups up).
+template <typename E>
 static int launch_pipe128(const FlashArgs& a, hipStream_t stream) {
   const int cus = device_cu_count();
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
-  if (blocks < 3L * cus) return launch(flash_fwd_bf16_pipe_kernel<128, 64, 2>, a, stream);
-  return launch(flash_fwd_bf16_pipe_kernel<128, 32, 3>, a, stream);
+  if (blocks < 3L * cus) return launch(flash_fwd_bf16_pipe_kernel<E, 128, 64, 2>, a, stream);
+  return launch(flash_fwd_bf16_pipe_kernel<E, 128, 32, 3>, a, stream);
+}
+
+// The 16-bit kernels (bf16 or fp16 operands, format E) for head_dim 64 / 128.
+template <typename E>
+static int launch_h16(const FlashArgs& a, int head_dim, hipStream_t s) {
+  const bool hb = a.bias != nullptr;
+  if (a.ext) {
+    // Extended masks / score modifiers: the one-pass kernel's EXT variants
+    // (1: interval masks, 2: segment ids / score modifiers as well).
+    const bool full = a.ext == 2;
+    if (head_dim == 128) {
+      if (full) return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<E, 128, false, 2>, a, s);
+      return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<E, 128, false, 1>, a, s);
+    }
+    if (full) return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<E, 64, false, 2>, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<E, 64, false, 1>, a, s);
+  }
+  // Dense bias with 16-byte aligned rows and 32-bit slice offsets: the LDS
+  // ring that streams the bias; otherwise bias loads into registers.
+  const bool ring = hb && a.Lk % 4 == 0 && (int64_t)a.Lq * a.Lk * 4 < ((int64_t)1 << 31);
+  if (head_dim == 128) {
+    if (ring) return launch_flash_bias_ring(128, a, s);
+    return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 0>, a, s) : launch_pipe128<E>(a, s);
+  }
+  if (ring) return launch_flash_bias_ring(64, a, s);
+  return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 0>, a, s) : launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2>, a, s);
 }
 
 // The fp32 split kernel: one workgroup per 32-row query block.
@@ -988,6 +1015,7 @@ static int make_flash_args(FlashArgs& a, const char* who, const void* q, const v
   a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
   a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
   a.causal = causal ? 1 : 0;
+  a.f16 = 0;
   a.scale = sm_scale;
   a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
   a.dv = (int)v_dim;
@@ -1005,10 +1033,10 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
                              int64_t head_dim, int64_t q_valid, int64_t kv_valid, int causal,
                              float sm_scale, const pjx_score_mods* mods, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F32");
-  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype == PJX_DTYPE_BF16))
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128 (or 256 in bf16)");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
+  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PJX_DTYPE_F32))
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128 (or 256 in bf16 / fp16)");
   FlashArgs a;
   bool empty;
   int rc = make_flash_args(a, "pjx_flash_fwd", q, k, v, o, lse, kv_lengths, bias, bias_batch,
@@ -1017,36 +1045,18 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   if (rc != PJX_OK || empty) return rc;
   hipStream_t s = (hipStream_t)stream;
   const bool hb = bias != nullptr;
+  a.f16 = dtype == PJX_DTYPE_F16;
   if (head_dim == 256) return launch_flash_wide256(a, s);
+  if (dtype == PJX_DTYPE_BF16) return launch_h16<Bf16Fmt>(a, (int)head_dim, s);
+  if (dtype == PJX_DTYPE_F16) return launch_h16<F16Fmt>(a, (int)head_dim, s);
   if (a.ext) {
-    // Extended masks / score modifiers: the one-pass kernels' EXT variants
-    // (1: interval masks, 2: segment ids / score modifiers as well).
     const bool full = a.ext == 2;
-    if (dtype == PJX_DTYPE_BF16) {
-      if (head_dim == 128) {
-        if (full) return hb ? launch(flash_fwd_bf16_kernel<128, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 2>, a, s);
-        return hb ? launch(flash_fwd_bf16_kernel<128, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<128, false, 1>, a, s);
-      }
-      if (full) return hb ? launch(flash_fwd_bf16_kernel<64, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 2>, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<64, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<64, false, 1>, a, s);
-    }
     if (head_dim == 128) {
       if (full) return hb ? launch(flash_fwd_f32_kernel<128, true, 2>, a, s) : launch(flash_fwd_f32_kernel<128, false, 2>, a, s);
       return hb ? launch(flash_fwd_f32_kernel<128, true, 1>, a, s) : launch(flash_fwd_f32_kernel<128, false, 1>, a, s);
     }
     if (full) return hb ? launch(flash_fwd_f32_kernel<64, true, 2>, a, s) : launch(flash_fwd_f32_kernel<64, false, 2>, a, s);
     return hb ? launch(flash_fwd_f32_kernel<64, true, 1>, a, s) : launch(flash_fwd_f32_kernel<64, false, 1>, a, s);
-  }
-  if (dtype == PJX_DTYPE_BF16) {
-    // Dense bias with 16-byte aligned rows and 32-bit slice offsets: the LDS
-    // ring that streams the bias; otherwise bias loads into registers.
-    const bool ring = hb && kv_len % 4 == 0 && q_len * kv_len * 4 < ((int64_t)1 << 31);
-    if (head_dim == 128) {
-      if (ring) return launch_flash_bias_ring(128, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<128, true, 0>, a, s) : launch_pipe128(a, s);
-    }
-    if (ring) return launch_flash_bias_ring(64, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<64, true, 0>, a, s) : launch(flash_fwd_bf16_pipe_kernel<64, 64, 2>, a, s);
   }
   // fp32 with fewer 128-row workgroups than CUs: split each query block's
   // keys over several waves (latency-bound sizes, like the reference's CPU
@@ -1069,7 +1079,8 @@ extern "C" int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o,
                            int64_t kv_valid, int causal, float sm_scale,
                            const pjx_score_mods* mods, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_mla_fwd: dtype must be PJX_DTYPE_BF16");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16)
+    return fail(PJX_ERR_INVALID, "pjx_mla_fwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F16");
   const bool wide = (rank == 576 && (v_dim == 512 || v_dim == 576)) || (rank == 512 && v_dim == 512);
   const bool narrow = (rank == 64 || rank == 128 || rank == 256) && v_dim == rank;
   if (!wide && !narrow)
@@ -1086,5 +1097,6 @@ extern "C" int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o,
                            bias_heads, batch, q_len, kv_len, heads, 1, rank, v_dim, q_valid,
                            kv_valid, causal, sm_scale, mods, &empty);
   if (rc != PJX_OK || empty) return rc;
+  a.f16 = dtype == PJX_DTYPE_F16;
   return launch_mla_wide(a, (int)rank, (hipStream_t)stream);
 }

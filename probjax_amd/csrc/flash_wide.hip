@@ -1,4 +1,4 @@
-// Flash-attention forward for wide heads on gfx950 (MI355X), bf16: head dims
+// Flash-attention forward for wide heads on gfx950 (MI355X), bf16 or fp16: head dims
 // above 128 (D = 256) and the absorbed latent attention of probjax's `mla`
 // (K = V = one shared latent row of R = 512 or 576 values per key, Hkv = 1;
 // probjax/nn/pallas_kernels/kernels/latent_attention.py:79-197, 636-766).
@@ -6,7 +6,7 @@
 // Semantics are those of flash_fwd.hip (the XLA reference,
 // kernels/attention_xla.py:339-429): s = sm_scale * q.k in fp32, then the
 // bias, then the mask (-inf), online softmax in the exp2 domain, P rounded to
-// bf16 before P.V, fp32 accumulation, rows without a valid key give 0.
+// the input's 16-bit format before P.V, fp32 accumulation, rows without a valid key give 0.
 //
 // Decomposition: one workgroup = 4 waves = 128 query rows of one (batch,
 // head), 32 rows per wave, as in flash_fwd.hip.  S^T = K Q^T puts the keys on
@@ -58,7 +58,7 @@ struct WideRow {
   }
 };
 
-template <int D, int DVP, int BK, bool SHARED, bool BIAS, int EXT>
+template <typename E, int D, int DVP, int BK, bool SHARED, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a) {
   using R = WideRow<D>;
   constexpr int ROWB = R::ROWB, NC = R::NC, G = R::G;
@@ -92,7 +92,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
   const bool row_ok = g.qi < g.q_hi;
 
   // Q^T as the B operand: lane holds query `col`, dims 16*st + 8*half + [0,8).
-  bf16x8 qf[KS];
+  typename E::v8 qf[KS];
   {
     const uint16_t* qrow =
         (const uint16_t*)a.q + ((size_t)(g.b * a.Lq + (row_in ? g.qi : 0)) * a.Hq + g.h) * D;
@@ -100,7 +100,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
     for (int st = 0; st < KS; ++st) {
       u32x4 raw = {0u, 0u, 0u, 0u};
       if (row_in) raw = *(const u32x4*)(qrow + 16 * st + 8 * half);
-      qf[st] = as_bf16x8(raw);
+      qf[st] = E::as8(raw);
     }
   }
   const float* brow = nullptr;
@@ -186,9 +186,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
       s[kb] = f32x16{};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
-        const bf16x8 kf =
-            as_bf16x8(*(const u32x4*)(ks + kb * 32 * ROWB + 16 * G * (st / KE) + offK[st % KE]));
-        s[kb] = mfma32x32x16(kf, qf[st], s[kb]);
+        const typename E::v8 kf =
+            E::as8(*(const u32x4*)(ks + kb * 32 * ROWB + 16 * G * (st / KE) + offK[st % KE]));
+        s[kb] = E::mma32(kf, qf[st], s[kb]);
       }
     }
 
@@ -252,14 +252,14 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
 
     // P^T as the B operand, 16 keys per MFMA step c:
     // slot j <-> key 16c + 8*(j/4) + 4*half + j%4 (registers 8*(c%2)+j of block c/2).
-    bf16x8 pf[BK / 16];
+    typename E::v8 pf[BK / 16];
 #pragma unroll
     for (int c = 0; c < BK / 16; ++c) {
       u32x4 pk;
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        pk[j] = pack_bf16x2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
-      pf[c] = as_bf16x8(pk);
+        pk[j] = E::pack2(s[c >> 1][8 * (c & 1) + 2 * j], s[c >> 1][8 * (c & 1) + 2 * j + 1]);
+      pf[c] = E::as8(pk);
     }
     // O^T[d][query] += V^T P^T: output block db covers chunks dv_off/8 + 4*db + [0,4).
 #pragma unroll
@@ -271,7 +271,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
         const u32x2 lo = lds_read_tr16(vs + 16 * c * ROWB + gofs + offVlo[e]);
         const u32x2 hi = lds_read_tr16(vs + 16 * c * ROWB + gofs + offVhi[e]);
         const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
-        acc[db] = mfma32x32x16(as_bf16x8(av), pf[c], acc[db]);
+        acc[db] = E::mma32(E::as8(av), pf[c], acc[db]);
       }
     }
   };
@@ -302,8 +302,8 @@ __global__ __launch_bounds__(kThreads, 1) void flash_fwd_wide_kernel(FlashArgs a
 #pragma unroll
       for (int gq = 0; gq < 4; ++gq) {
         u32x2 pk;
-        pk[0] = pack_bf16x2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
-        pk[1] = pack_bf16x2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
+        pk[0] = E::pack2(acc[db][4 * gq] * inv, acc[db][4 * gq + 1] * inv);
+        pk[1] = E::pack2(acc[db][4 * gq + 2] * inv, acc[db][4 * gq + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * gq + 4 * half) = pk;
       }
     if (part == 0 && a.lse && half == 0)
@@ -323,17 +323,23 @@ static int launch_wide(K kernel, const FlashArgs& a, int n_parts, hipStream_t st
 // One (D, DVP, BK, SHARED) shape over the bias / extended-mask variants.
 // Interval masks (EXT = 1) run the full extended kernel: at these head widths
 // the per-score mask work is a small share of the tile.
+template <typename E, int D, int DVP, int BK, bool SHARED>
+static int launch_wide_fmt(const FlashArgs& a, hipStream_t s, const char* who) {
+  const int np = a.dv / DVP;
+  const bool hb = a.bias != nullptr;
+  if (a.ext)
+    return hb ? launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 2>, a, np, s, who)
+              : launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 2>, a, np, s, who);
+  return hb ? launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 0>, a, np, s, who)
+            : launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 0>, a, np, s, who);
+}
+
 template <int D, int DVP, int BK, bool SHARED>
 static int launch_wide_variant(const FlashArgs& a, hipStream_t s, const char* who) {
   static_assert(DVP % 32 == 0, "parts of whole output blocks");
   if (a.dv % DVP != 0) return fail(PJX_ERR_INVALID, "wide flash forward: output width not a multiple of the part");
-  const int np = a.dv / DVP;
-  const bool hb = a.bias != nullptr;
-  if (a.ext)
-    return hb ? launch_wide(flash_fwd_wide_kernel<D, DVP, BK, SHARED, true, 2>, a, np, s, who)
-              : launch_wide(flash_fwd_wide_kernel<D, DVP, BK, SHARED, false, 2>, a, np, s, who);
-  return hb ? launch_wide(flash_fwd_wide_kernel<D, DVP, BK, SHARED, true, 0>, a, np, s, who)
-            : launch_wide(flash_fwd_wide_kernel<D, DVP, BK, SHARED, false, 0>, a, np, s, who);
+  return a.f16 ? launch_wide_fmt<F16Fmt, D, DVP, BK, SHARED>(a, s, who)
+               : launch_wide_fmt<Bf16Fmt, D, DVP, BK, SHARED>(a, s, who);
 }
 
 // D = 256 flash forward (separate K and V), called by pjx_flash_fwd.

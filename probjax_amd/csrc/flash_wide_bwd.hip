@@ -1,4 +1,4 @@
-// Flash-attention backward for wide heads on gfx950 (MI355X), bf16: D = 256,
+// Flash-attention backward for wide heads on gfx950 (MI355X), bf16 or fp16: D = 256,
 // and the absorbed latent of probjax's `mla` (K = V = one shared latent row of
 // R = 512 or 576 values per key, Hkv = 1, output width DV <= R).
 //
@@ -7,8 +7,9 @@
 // broadcast to every head, so the cache gradient is the sum over heads of
 // dK + dV.  The math is the flash backward's (flash_bwd.hip; probjax
 // attention.py:853-1160): delta = sum_d o*do, p = exp2(s*log2e - lse*log2e),
-// ds = p (do.v^T - delta) sm_scale, dq = sum_k bf16(ds) k,
-// dk = sum_q bf16(ds)^T q, dv = sum_q bf16(p)^T do, fp32 accumulation.
+// ds = p (do.v^T - delta) sm_scale, dq = sum_k r(ds) k,
+// dk = sum_q r(ds)^T q, dv = sum_q r(p)^T do, fp32 accumulation (r() rounds
+// to the input's 16-bit format).
 //
 // At these widths a wave cannot hold 32 rows of Q^T and dO^T and a 32-row dQ
 // accumulator (1.5 K registers at R = 576), so both kernels put 16 rows (or
@@ -66,7 +67,7 @@ struct Row16 {
 };
 
 // Per-lane LDS offsets of one tile layout's two read patterns.
-template <int D>
+template <typename E, int D>
 struct Offs16 {
   using R = Row16<D>;
   static constexpr int PR = R::G / 4;  // period (in 32-dim steps) of row reads
@@ -88,17 +89,17 @@ struct Offs16 {
     }
   }
   // Row fragment of 32-dim step st, rows 16*rb .. +15 of the tile.
-  __device__ bf16x8 rows(const unsigned char* tile, int rb, int st) const {
-    return as_bf16x8(*(const u32x4*)(tile + 16 * rb * R::ROWB + 16 * R::G * (st / PR) + row[st % PR]));
+  __device__ typename E::v8 rows(const unsigned char* tile, int rb, int st) const {
+    return E::as8(*(const u32x4*)(tile + 16 * rb * R::ROWB + 16 * R::G * (st / PR) + row[st % PR]));
   }
   // Transposed fragment of dims 16i .. +15 over the tile's 32 rows in k-slot
   // order (slot 8qd + j <-> row 16(j/4) + 4qd + j%4).
-  __device__ bf16x8 trans(const unsigned char* tile, int i) const {
+  __device__ typename E::v8 trans(const unsigned char* tile, int i) const {
     const unsigned char* p = tile + 16 * R::G * (i / PT) + tr[i % PT];
     const u32x2 lo = lds_read_tr16(p);
     const u32x2 hi = lds_read_tr16(p + 16 * R::ROWB);
     const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
-    return as_bf16x8(v);
+    return E::as8(v);
   }
   // Copies rows [r0, r0 + n) (n >= 1) of a global tensor with row stride
   // `rowstride` into a tile; rows past n read as zero.
@@ -110,26 +111,23 @@ struct Offs16 {
   }
 };
 
-// Two f32x4 C blocks (k slots j < 4 from a, j >= 4 from b) as a bf16 B operand.
-__device__ __forceinline__ bf16x8 pack_slots(const f32x4& a, const f32x4& b) {
-  const u32x4 pk = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(b[0], b[1]),
-                    pack_bf16x2(b[2], b[3])};
-  return as_bf16x8(pk);
+// Two f32x4 C blocks (k slots j < 4 from a, j >= 4 from b) as a 16-bit B operand.
+template <typename E>
+__device__ __forceinline__ typename E::v8 pack_slots(const f32x4& a, const f32x4& b) {
+  const u32x4 pk = {E::pack2(a[0], a[1]), E::pack2(a[2], a[3]), E::pack2(b[0], b[1]), E::pack2(b[2], b[3])};
+  return E::as8(pk);
 }
-
-__device__ __forceinline__ float bf16_lo16(uint32_t x) { return __uint_as_float(x << 16); }
-__device__ __forceinline__ float bf16_hi16(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
 
 // ---------------------------------------------------------------------------
 // dQ (and delta, lse*log2e): one workgroup per (64-query tile, batch, head).
 // ---------------------------------------------------------------------------
-template <int D, int DV, bool SHARED, int BIAS, int EXT>
+template <typename E, int D, int DV, bool SHARED, int BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba) {
   // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
   constexpr bool HB = BIAS != 0, DB = BIAS == 2;
   const FlashArgs& a = ba.f;
-  using OK = Offs16<D>;
-  using OV = Offs16<DV>;
+  using OK = Offs16<E, D>;
+  using OV = Offs16<E, DV>;
   constexpr int KT_B = Row16<D>::TILE_B;
   constexpr int STAGE_B = SHARED ? KT_B : KT_B + Row16<DV>::TILE_B;
   constexpr int KS = D / 32, VS = DV / 32, ND = D / 16;
@@ -180,7 +178,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
 
   // Q^T, dO^T as B operands (lane: row qi, dims 32*st + 8*qd + [0,8)) and
   // delta = sum_d o*do over the DV output dims.
-  bf16x8 qf[KS], dof[VS];
+  typename E::v8 qf[KS], dof[VS];
   float dsum = 0.f;
   {
     const uint16_t* qrow = (const uint16_t*)a.q + ((size_t)(b * a.Lq + (row_in ? qi : 0)) * a.Hq + h) * D;
@@ -191,7 +189,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
     for (int st = 0; st < KS; ++st) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (row_in) r = *(const u32x4*)(qrow + 32 * st + 8 * qd);
-      qf[st] = as_bf16x8(r);
+      qf[st] = E::as8(r);
     }
 #pragma unroll
     for (int st = 0; st < VS; ++st) {
@@ -200,10 +198,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
         rd = *(const u32x4*)(drow + 32 * st + 8 * qd);
         ro = *(const u32x4*)(orow + 32 * st + 8 * qd);
       }
-      dof[st] = as_bf16x8(rd);
+      dof[st] = E::as8(rd);
 #pragma unroll
       for (int j = 0; j < 4; ++j)
-        dsum = fmaf(bf16_lo16(ro[j]), bf16_lo16(rd[j]), fmaf(bf16_hi16(ro[j]), bf16_hi16(rd[j]), dsum));
+        dsum = fmaf(E::lo(ro[j]), E::lo(rd[j]), fmaf(E::hi(ro[j]), E::hi(rd[j]), dsum));
     }
   }
   const float delta = xor32_sum(xor16_sum(dsum));
@@ -260,15 +258,15 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
       dp[kb] = f32x4{};
 #pragma unroll
       for (int st = 0; st < KS; ++st) {
-        const bf16x8 kf = ok.rows(ks, kb, st);
-        s[kb] = mfma16x16x32(kf, qf[st], s[kb]);
+        const typename E::v8 kf = ok.rows(ks, kb, st);
+        s[kb] = E::mma16(kf, qf[st], s[kb]);
         if constexpr (SHARED) {
-          if (st < VS) dp[kb] = mfma16x16x32(kf, dof[st], dp[kb]);
+          if (st < VS) dp[kb] = E::mma16(kf, dof[st], dp[kb]);
         }
       }
       if constexpr (!SHARED) {
 #pragma unroll
-        for (int st = 0; st < VS; ++st) dp[kb] = mfma16x16x32(ov.rows(vs, kb, st), dof[st], dp[kb]);
+        for (int st = 0; st < VS; ++st) dp[kb] = E::mma16(ov.rows(vs, kb, st), dof[st], dp[kb]);
       }
     }
     f32x4 dbv[2];
@@ -349,9 +347,9 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
       }
     }
     // dQ^T[16i + 4qd + r][row] += K^T dS^T
-    const bf16x8 dsb = pack_slots(s[0], s[1]);
+    const typename E::v8 dsb = pack_slots<E>(s[0], s[1]);
 #pragma unroll
-    for (int i = 0; i < ND; ++i) acc[i] = mfma16x16x32(ok.trans(ks, i), dsb, acc[i]);
+    for (int i = 0; i < ND; ++i) acc[i] = E::mma16(ok.trans(ks, i), dsb, acc[i]);
   };
 
   if (n_tiles > 0) issue(0, smem0);
@@ -372,8 +370,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
       u32x2 pk;
-      pk[0] = pack_bf16x2(acc[i][0], acc[i][1]);
-      pk[1] = pack_bf16x2(acc[i][2], acc[i][3]);
+      pk[0] = E::pack2(acc[i][0], acc[i][1]);
+      pk[1] = E::pack2(acc[i][2], acc[i][3]);
       *(u32x2*)(drow + 16 * i + 4 * qd) = pk;
     }
   }
@@ -383,11 +381,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
 // dK, dV (or dC = dK + dV of the shared latent): one workgroup per (64-key
 // tile, batch, KV head, query-head group).
 // ---------------------------------------------------------------------------
-template <int D, int DV, bool SHARED, bool BIAS, int EXT>
+template <typename E, int D, int DV, bool SHARED, bool BIAS, int EXT>
 __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs ba) {
   const FlashArgs& a = ba.f;
-  using OQ = Offs16<D>;
-  using OD = Offs16<DV>;
+  using OQ = Offs16<E, D>;
+  using OD = Offs16<E, DV>;
   constexpr int QT_B = Row16<D>::TILE_B, DT_B = Row16<DV>::TILE_B;
   // lse*log2e and delta of the tile's rows, one 64-float slot each (the
   // 4-byte buffer->LDS load writes one float per lane; lanes 32..63 fill the
@@ -442,7 +440,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
   const int n_tiles = gs * n_qt;
 
   // K^T (and V^T) as B operands: lane holds key `key`, dims 32*st + 8*qd + [0,8).
-  bf16x8 kf[KS], vf[SHARED ? 1 : VS];
+  typename E::v8 kf[KS], vf[SHARED ? 1 : VS];
   {
     const bool kin = key < a.Lk;
     const uint16_t* krow = (const uint16_t*)a.k + ((size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv) * D;
@@ -451,14 +449,14 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
     for (int st = 0; st < KS; ++st) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (kin) r = *(const u32x4*)(krow + 32 * st + 8 * qd);
-      kf[st] = as_bf16x8(r);
+      kf[st] = E::as8(r);
     }
     if constexpr (!SHARED) {
 #pragma unroll
       for (int st = 0; st < VS; ++st) {
         u32x4 r = {0u, 0u, 0u, 0u};
         if (kin) r = *(const u32x4*)(vrow + 32 * st + 8 * qd);
-        vf[st] = as_bf16x8(r);
+        vf[st] = E::as8(r);
       }
     }
   }
@@ -513,10 +511,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
       sx[rb] = f32x4{};
       dpx[rb] = f32x4{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s) sx[rb] = mfma16x16x32(oq.rows(qs, rb, s), kf[s], sx[rb]);
+      for (int s = 0; s < KS; ++s) sx[rb] = E::mma16(oq.rows(qs, rb, s), kf[s], sx[rb]);
 #pragma unroll
       for (int s = 0; s < VS; ++s)
-        dpx[rb] = mfma16x16x32(od.rows(dos, rb, s), SHARED ? kf[s] : vf[s], dpx[rb]);
+        dpx[rb] = E::mma16(od.rows(dos, rb, s), SHARED ? kf[s] : vf[s], dpx[rb]);
     }
     const float* bbase = nullptr;
     if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
@@ -551,17 +549,17 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
         dpx[rb][r] = p * (dpx[rb][r] - d4[r]) * a.scale * gg;
       }
     }
-    const bf16x8 pb = pack_slots(sx[0], sx[1]);
-    const bf16x8 dsb = pack_slots(dpx[0], dpx[1]);
+    const typename E::v8 pb = pack_slots<E>(sx[0], sx[1]);
+    const typename E::v8 dsb = pack_slots<E>(dpx[0], dpx[1]);
     // dK^T[16i + 4qd + r][key] += Q^T dS;  dV^T += dO^T P (into dK^T with the latent)
 #pragma unroll
-    for (int i = 0; i < ND; ++i) acck[i] = mfma16x16x32(oq.trans(qs, i), dsb, acck[i]);
+    for (int i = 0; i < ND; ++i) acck[i] = E::mma16(oq.trans(qs, i), dsb, acck[i]);
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
       if constexpr (SHARED)
-        acck[i] = mfma16x16x32(od.trans(dos, i), pb, acck[i]);
+        acck[i] = E::mma16(od.trans(dos, i), pb, acck[i]);
       else
-        accv[i] = mfma16x16x32(od.trans(dos, i), pb, accv[i]);
+        accv[i] = E::mma16(od.trans(dos, i), pb, accv[i]);
     }
   };
 
@@ -584,14 +582,14 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
     uint16_t* dkrow = (uint16_t*)ba.dk + krow * D;
 #pragma unroll
     for (int i = 0; i < ND; ++i) {
-      const u32x2 pk = {pack_bf16x2(acck[i][0], acck[i][1]), pack_bf16x2(acck[i][2], acck[i][3])};
+      const u32x2 pk = {E::pack2(acck[i][0], acck[i][1]), E::pack2(acck[i][2], acck[i][3])};
       *(u32x2*)(dkrow + 16 * i + 4 * qd) = pk;
     }
     if constexpr (!SHARED) {
       uint16_t* dvrow = (uint16_t*)ba.dv + krow * DV;
 #pragma unroll
       for (int i = 0; i < NV; ++i) {
-        const u32x2 pv = {pack_bf16x2(accv[i][0], accv[i][1]), pack_bf16x2(accv[i][2], accv[i][3])};
+        const u32x2 pv = {E::pack2(accv[i][0], accv[i][1]), E::pack2(accv[i][2], accv[i][3])};
         *(u32x2*)(dvrow + 16 * i + 4 * qd) = pv;
       }
     }
@@ -610,15 +608,16 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
   }
 }
 
-// Sums the head-group partials in split order and rounds to bf16:
+// Sums the head-group partials in split order and rounds to the 16-bit format:
 // out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
+template <typename E>
 __global__ __launch_bounds__(256) void wide_bwd_reduce_kernel(const float* part, int nsplit, size_t n,
                                                                 uint16_t* out) {
   const size_t e = 4 * ((size_t)blockIdx.x * 256 + threadIdx.x);
   if (e >= n) return;
   f32x4 acc = *(const f32x4*)(part + e);
   for (int s = 1; s < nsplit; ++s) acc += *(const f32x4*)(part + (size_t)s * n + e);
-  const u32x2 pk = {pack_bf16x2(acc[0], acc[1]), pack_bf16x2(acc[2], acc[3])};
+  const u32x2 pk = {E::pack2(acc[0], acc[1]), E::pack2(acc[2], acc[3])};
   *(u32x2*)(out + e) = pk;
 }
 
@@ -650,7 +649,7 @@ int wide_bwd_nsplit(int64_t B, int64_t Lk, int64_t Hq, int64_t Hkv) {
   return ns;
 }
 
-template <int D, int DV, bool SHARED>
+template <typename E, int D, int DV, bool SHARED>
 static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   const FlashArgs& a = ba.f;
   const bool hb = a.bias != nullptr, db = ba.dbias != nullptr, ext = a.ext != 0;
@@ -658,7 +657,7 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   const long kv_blocks = (long)((a.Lk + kWK - 1) / kWK) * a.B * a.Hkv * ba.nsplit;
   if (dq_blocks > 0x7fffffffL || kv_blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "wide backward: grid too large");
   const dim3 blk(kThreads);
-#define PJX_DQ(BI, EX) hipLaunchKernelGGL((wide_bwd_dq_kernel<D, DV, SHARED, BI, EX>), dim3((unsigned)dq_blocks), blk, 0, s, ba)
+#define PJX_DQ(BI, EX) hipLaunchKernelGGL((wide_bwd_dq_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)dq_blocks), blk, 0, s, ba)
   if (ext) {
     if (db) PJX_DQ(2, 2); else if (hb) PJX_DQ(1, 2); else PJX_DQ(0, 2);
   } else {
@@ -668,7 +667,7 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   int rc = check_launch(who);
   if (rc != PJX_OK) return rc;
   if (kv_blocks > 0) {
-#define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
+#define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
     if (ext) {
       if (hb) PJX_KV(true, 2); else PJX_KV(false, 2);
     } else {
@@ -680,11 +679,11 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   }
   if (ba.nsplit > 1) {
     const size_t nk = (size_t)a.B * a.Lk * a.Hkv * D;
-    hipLaunchKernelGGL(wide_bwd_reduce_kernel, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
+    hipLaunchKernelGGL(wide_bwd_reduce_kernel<E>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
                        (const float*)ba.part, ba.nsplit, nk, (uint16_t*)ba.dk);
     if constexpr (!SHARED) {
       const size_t nv = (size_t)a.B * a.Lk * a.Hkv * DV;
-      hipLaunchKernelGGL(wide_bwd_reduce_kernel, dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
+      hipLaunchKernelGGL(wide_bwd_reduce_kernel<E>, dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
                          (const float*)(ba.part + (size_t)ba.nsplit * nk), ba.nsplit, nv, (uint16_t*)ba.dv);
     }
     rc = check_launch(who);
@@ -692,12 +691,18 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   return rc;
 }
 
-int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
-  if (!shared && D == 256 && DV == 256) return run_wide_bwd_t<256, 256, false>(ba, s, who);
-  if (shared && D == 576 && DV == 512) return run_wide_bwd_t<576, 512, true>(ba, s, who);
-  if (shared && D == 576 && DV == 576) return run_wide_bwd_t<576, 576, true>(ba, s, who);
-  if (shared && D == 512 && DV == 512) return run_wide_bwd_t<512, 512, true>(ba, s, who);
+template <typename E>
+static int run_wide_bwd_fmt(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
+  if (!shared && D == 256 && DV == 256) return run_wide_bwd_t<E, 256, 256, false>(ba, s, who);
+  if (shared && D == 576 && DV == 512) return run_wide_bwd_t<E, 576, 512, true>(ba, s, who);
+  if (shared && D == 576 && DV == 576) return run_wide_bwd_t<E, 576, 576, true>(ba, s, who);
+  if (shared && D == 512 && DV == 512) return run_wide_bwd_t<E, 512, 512, true>(ba, s, who);
   return fail(PJX_ERR_INVALID, "wide backward: unsupported head widths");
+}
+
+int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
+  return ba.f.f16 ? run_wide_bwd_fmt<F16Fmt>(ba, D, DV, shared, s, who)
+                  : run_wide_bwd_fmt<Bf16Fmt>(ba, D, DV, shared, s, who);
 }
 
 }  // namespace pjx
@@ -720,7 +725,8 @@ extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const vo
                            float sm_scale, const pjx_score_mods* mods, void* stream) {
   clear_error();
   const char* who = "pjx_mla_bwd";
-  if (dtype != PJX_DTYPE_BF16) return fail(PJX_ERR_INVALID, "pjx_mla_bwd: dtype must be PJX_DTYPE_BF16");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16)
+    return fail(PJX_ERR_INVALID, "pjx_mla_bwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F16");
   if (!((rank == 576 && (v_dim == 512 || v_dim == 576)) || (rank == 512 && v_dim == 512)))
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: (rank, v_dim) must be (576, 512), (576, 576) or (512, 512)");
   if (!q || !cache || !o || !dout || !lse || !dq || !dcache)
@@ -750,6 +756,7 @@ extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const vo
   a.q_valid = (int)std::min<int64_t>(std::max<int64_t>(q_valid, 0), q_len);
   a.kv_valid = (int)std::min<int64_t>(std::max<int64_t>(kv_valid, 0), kv_len);
   a.causal = causal ? 1 : 0;
+  a.f16 = dtype == PJX_DTYPE_F16;
   a.scale = sm_scale;
   a.n_qtiles = (int)((q_len + kBQ - 1) / kBQ);
   a.dv = (int)v_dim;

@@ -17,7 +17,7 @@
 // have the rank contiguous (the "NT" form of Q K^T).  One launch covers K
 // (grid.y < ny) and V (grid.y >= ny).
 //
-// bf16: 128 x 128 output tiles, 4 waves of 64 x 64 (2 x 2 MFMA 32x32x16
+// bf16 / fp16 (one kernel template over the 16-bit format): 128 x 128 output tiles, 4 waves of 64 x 64 (2 x 2 MFMA 32x32x16
 // blocks).  Ranks that are a multiple of 8 stream chunks of 32 rank entries
 // straight from HBM into a 2-stage LDS ring (buffer -> LDS loads, the next
 // chunk in flight while the current one is multiplied, one barrier per
@@ -67,6 +67,7 @@ __device__ __forceinline__ u32x4 load_chunk_bf16(const uint16_t* row, int r0, in
 }
 
 // Ranks that are not a multiple of 8: register-staged chunks, element loads.
+template <typename E>
 __global__ __launch_bounds__(256, 2) void mla_project_bf16_ragged_kernel(ProjArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[2 * kBM * kPitch];
   unsigned char* As = lds;
@@ -130,15 +131,15 @@ __global__ __launch_bounds__(256, 2) void mla_project_bf16_ragged_kernel(ProjArg
     if (t + 1 < nk) load((t + 1) * kBK);
 #pragma unroll
     for (int ks = 0; ks < kBK / 16; ++ks) {
-      bf16x8 af[2], bf[2];
+      typename E::v8 af[2], bf[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = as_bf16x8(*(const u32x4*)(As + (wr + 32 * i) * kPitch + frag + ks * 32));
+      for (int i = 0; i < 2; ++i) af[i] = E::as8(*(const u32x4*)(As + (wr + 32 * i) * kPitch + frag + ks * 32));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = as_bf16x8(*(const u32x4*)(Bs + (wc + 32 * j) * kPitch + frag + ks * 32));
+      for (int j = 0; j < 2; ++j) bf[j] = E::as8(*(const u32x4*)(Bs + (wc + 32 * j) * kPitch + frag + ks * 32));
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(af[i], bf[j], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = E::mma32(af[i], bf[j], acc[i][j]);
     }
   }
 
@@ -154,7 +155,7 @@ __global__ __launch_bounds__(256, 2) void mla_project_bf16_ragged_kernel(ProjArg
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int64_t m = m0 + wr + 32 * i + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        if (m < a.M) O[m * ncols + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.f) & 0xffffu);
+        if (m < a.M) O[m * ncols + n] = E::bits(acc[i][j][r]);
       }
     }
 }
@@ -172,6 +173,7 @@ constexpr uint32_t kOff = 0x80000000u;  // a buffer offset past every range: loa
 constexpr int kOutPitch = kBN * 2 + 16;  // LDS bytes per output row in the epilogue
 constexpr int kLdsB = 2 * kStageB > kBM * kOutPitch ? 2 * kStageB : kBM * kOutPitch;
 
+template <typename E>
 __global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
   __shared__ __attribute__((aligned(16))) unsigned char lds[kLdsB];
   const int which = blockIdx.y >= (unsigned)a.ny ? 1 : 0;
@@ -230,17 +232,17 @@ __global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
 #pragma unroll
     for (int ks = 0; ks < kRK / 16; ++ks) {
       const int slot = 16 * ((2 * ks + (lane >> 5)) ^ rsw);
-      bf16x8 af[2], bf[2];
+      typename E::v8 af[2], bf[2];
 #pragma unroll
-      for (int i = 0; i < 2; ++i) af[i] = as_bf16x8(*(const u32x4*)(As + (wr + 32 * i + rrow) * kRowB + slot));
+      for (int i = 0; i < 2; ++i) af[i] = E::as8(*(const u32x4*)(As + (wr + 32 * i + rrow) * kRowB + slot));
 #pragma unroll
-      for (int j = 0; j < 2; ++j) bf[j] = as_bf16x8(*(const u32x4*)(Bs + (wc + 32 * j + rrow) * kRowB + slot));
+      for (int j = 0; j < 2; ++j) bf[j] = E::as8(*(const u32x4*)(Bs + (wc + 32 * j + rrow) * kRowB + slot));
       // W as the MFMA's first operand: the result is out^T, so each lane ends
       // with 4 consecutive output columns of one row per register group
 #pragma unroll
       for (int i = 0; i < 2; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = mfma32x32x16(bf[j], af[i], acc[i][j]);
+        for (int j = 0; j < 2; ++j) acc[i][j] = E::mma32(bf[j], af[i], acc[i][j]);
     }
   }
 
@@ -257,7 +259,7 @@ __global__ __launch_bounds__(256, 2) void mla_project_bf16_kernel(ProjArgs a) {
         const f32x16& c = acc[i][j];
         const int row = wr + 32 * i + (lane & 31), col = wc + 32 * j + 8 * g + 4 * (lane >> 5);
         *(u32x2*)(lds + row * kOutPitch + col * 2) =
-            u32x2{pack_bf16x2(c[4 * g], c[4 * g + 1]), pack_bf16x2(c[4 * g + 2], c[4 * g + 3])};
+            u32x2{E::pack2(c[4 * g], c[4 * g + 1]), E::pack2(c[4 * g + 2], c[4 * g + 3])};
       }
   stage_barrier();
   uint16_t* O = (uint16_t*)a.out[which];
@@ -352,8 +354,8 @@ extern "C" int pjx_mla_project(int dtype, const void* cache, const void* wk, con
                                void* v, int64_t batch, int64_t kv_len, int64_t heads, int64_t rank,
                                int64_t qk_dim, int64_t v_dim, int64_t width, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_mla_project: dtype must be bf16 or f32");
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
+    return fail(PJX_ERR_INVALID, "pjx_mla_project: dtype must be bf16, f16 or f32");
   if (batch < 0 || kv_len < 0 || heads <= 0 || rank <= 0)
     return fail(PJX_ERR_INVALID, "pjx_mla_project: bad sizes");
   if (width <= 0 || qk_dim <= 0 || v_dim <= 0 || qk_dim > width || v_dim > width)
@@ -377,17 +379,24 @@ extern "C" int pjx_mla_project(int dtype, const void* cache, const void* wk, con
   a.dim[1] = (int)v_dim;
   const int ncols = a.H * a.width;
   hipStream_t s = (hipStream_t)stream;
-  if (dtype == PJX_DTYPE_BF16) {
+  if (dtype != PJX_DTYPE_F32) {
     a.ny = (ncols + kBN - 1) / kBN;
     const int64_t gx = (M + kBM - 1) / kBM;
     if (gx > 0x7fffffff) return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
     // the ring's buffer offsets are 32-bit: 128 latent rows and each weight tensor
     const bool ring = (rank & 7) == 0 && 128 * rank * 2 < ((int64_t)1 << 31) &&
                       heads * std::max(qk_dim, v_dim) * rank * 2 < ((int64_t)1 << 31);
-    if (ring)
-      hipLaunchKernelGGL(mla_project_bf16_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
-    else
-      hipLaunchKernelGGL(mla_project_bf16_ragged_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+    const dim3 grid((unsigned)gx, 2 * a.ny);
+    if (dtype == PJX_DTYPE_F16) {
+      if (ring)
+        hipLaunchKernelGGL(mla_project_bf16_kernel<F16Fmt>, grid, dim3(256), 0, s, a);
+      else
+        hipLaunchKernelGGL(mla_project_bf16_ragged_kernel<F16Fmt>, grid, dim3(256), 0, s, a);
+    } else if (ring) {
+      hipLaunchKernelGGL(mla_project_bf16_kernel<Bf16Fmt>, grid, dim3(256), 0, s, a);
+    } else {
+      hipLaunchKernelGGL(mla_project_bf16_ragged_kernel<Bf16Fmt>, grid, dim3(256), 0, s, a);
+    }
   } else {
     a.ny = (ncols + kFN - 1) / kFN;
     const int64_t gx = (M + kFM - 1) / kFM;

@@ -8,8 +8,11 @@
 //   v_mfma_f32_16x16x32_bf16 : A lane l holds A[l%16][8*(l/16)+j];
 //                              B lane l holds B[8*(l/16)+j][l%16];
 //                              C reg r of lane l is C[4*(l/16)+r][l%16].
+//   v_mfma_f32_16x16x16_bf16 : A lane l holds A[l%16][4*(l/16)+j], j<4;
+//                              B lane l holds B[4*(l/16)+j][l%16]; C as for 16x16x32.
 //   v_mfma_f32_32x32x2f32    : A lane l holds A[l%32][l/32]; B lane l holds
 //                              B[l/32][l%32]; C as for 32x32x16.
+// The fp16 forms (v_mfma_f32_32x32x16_f16 etc.) have the same layouts.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -29,18 +32,9 @@ constexpr float kLn2 = 0.6931471805599453f;
 // -inf, so exp2(-inf - kMaxInit) == 0 while exp2(kMaxInit - kMaxInit) == 1.
 constexpr float kMaxInit = -1e30f;
 
-__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
-__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
-}
 __device__ __forceinline__ f32x16 mfma32x32x2f32(float a, float b, f32x16 c) {
   return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
-__device__ __forceinline__ u32x4 as_u32x4(bf16x8 v) { return __builtin_bit_cast(u32x4, v); }
 
 // Value of lane l^32 combined with lane l, identical in both halves.
 __device__ __forceinline__ float xor32_max(float x) {
@@ -71,10 +65,6 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   p[0] = (__bf16)lo;
   p[1] = (__bf16)hi;
   return __builtin_bit_cast(uint32_t, p);
-}
-
-__device__ __forceinline__ float bf16_bits_to_float(uint32_t bits16) {
-  return __uint_as_float(bits16 << 16);
 }
 
 // Select 16-bit halves of two dwords: lo halves (sel 0) or hi halves (sel 1)
@@ -136,12 +126,6 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
 
 __device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
 
-// v_mfma_f32_16x16x16_bf16: A lane l holds A[l%16][4*(l/16)+j], j<4;
-// B lane l holds B[4*(l/16)+j][l%16]; C as for 16x16x32.
-__device__ __forceinline__ f32x4 mfma16x16x16(s16x4 a, s16x4 b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
-}
-
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
@@ -167,5 +151,62 @@ __device__ __forceinline__ void stage_barrier() {
 // only when a row's new max exceeds it by more than this (log2 units), so P
 // stays <= 2^kRescaleLog2 and the O rescale runs on few tiles.
 constexpr float kRescaleLog2 = 8.0f;
+
+// ---------------------------------------------------------------------------
+// The two 16-bit element formats of the MFMA kernels.  bf16 and fp16 operands
+// have the same lane layouts for every instruction used here and the same
+// byte layout in memory and LDS, so a kernel templated on the format differs
+// only in the MFMA opcodes and the float <-> 16-bit conversions (both round to
+// nearest even).  P <= 2^kRescaleLog2 keeps the unnormalised probabilities
+// well inside fp16's range.
+// ---------------------------------------------------------------------------
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+struct Bf16Fmt {
+  typedef bf16x8 v8;
+  static constexpr bool kF16 = false;
+  __device__ static v8 as8(u32x4 v) { return __builtin_bit_cast(v8, v); }
+  __device__ static f32x16 mma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static f32x4 mma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static f32x4 mma16k16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(a, b, c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float lo, float hi) { return pack_bf16x2(lo, hi); }
+  __device__ static uint16_t bits(float x) { return __builtin_bit_cast(uint16_t, (__bf16)x); }
+  // the element in the low / high 16 bits of a dword, as float
+  __device__ static float lo(uint32_t x) { return __uint_as_float(x << 16); }
+  __device__ static float hi(uint32_t x) { return __uint_as_float(x & 0xffff0000u); }
+};
+
+struct F16Fmt {
+  typedef f16x8 v8;
+  static constexpr bool kF16 = true;
+  __device__ static v8 as8(u32x4 v) { return __builtin_bit_cast(v8, v); }
+  __device__ static f32x16 mma32(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static f32x4 mma16(v8 a, v8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+  __device__ static f32x4 mma16k16(s16x4 a, s16x4 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(__builtin_bit_cast(f16x4, a), __builtin_bit_cast(f16x4, b),
+                                                 c, 0, 0, 0);
+  }
+  __device__ static uint32_t pack2(float lo, float hi) {
+    typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+    f16x2 p;
+    p[0] = (_Float16)lo;
+    p[1] = (_Float16)hi;
+    return __builtin_bit_cast(uint32_t, p);
+  }
+  __device__ static uint16_t bits(float x) { return __builtin_bit_cast(uint16_t, (_Float16)x); }
+  __device__ static float lo(uint32_t x) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(x & 0xffffu)); }
+  __device__ static float hi(uint32_t x) { return (float)__builtin_bit_cast(_Float16, (uint16_t)(x >> 16)); }
+};
 
 }  // namespace pjx

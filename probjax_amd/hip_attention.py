@@ -15,14 +15,27 @@ import torch
 
 from . import native
 
-_DTYPES = {torch.bfloat16: native.PJX_DTYPE_BF16, torch.float32: native.PJX_DTYPE_F32}
+_DTYPES = {
+    torch.bfloat16: native.PJX_DTYPE_BF16,
+    torch.float16: native.PJX_DTYPE_F16,
+    torch.float32: native.PJX_DTYPE_F32,
+}
+# the dtypes of the 16-bit (MFMA bf16 / fp16) kernels
+HALF_DTYPES = (torch.bfloat16, torch.float16)
 
 
 def _dtype_code(t: torch.Tensor) -> int:
     try:
         return _DTYPES[t.dtype]
     except KeyError:
-        raise ValueError(f"unsupported dtype {t.dtype}; expected bfloat16 or float32") from None
+        raise ValueError(f"unsupported dtype {t.dtype}; expected bfloat16, float16 or float32") from None
+
+
+def _half_code(who: str, *ts) -> int:
+    """Dtype code of tensors that must share one 16-bit dtype."""
+    if ts[0].dtype not in HALF_DTYPES or any(t.dtype != ts[0].dtype for t in ts):
+        raise ValueError(f"{who} takes bfloat16 or float16 tensors of one dtype")
+    return _DTYPES[ts[0].dtype]
 
 
 def _on_device(*ts):
@@ -131,8 +144,8 @@ def flash_attention_fwd(
         raise ValueError("q, k, v must share a dtype")
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128) and not (D == 256 and q.dtype == torch.bfloat16):
-        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16)")
+    if D not in (64, 128) and not (D == 256 and q.dtype in HALF_DTYPES):
+        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16 / fp16)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     code = _dtype_code(q)
@@ -170,7 +183,7 @@ def flash_attention_bwd(
     ``[1|B, 1|H, Lq, Lk]`` shape, fp32).
 
     ``o`` and ``lse`` are the forward's output and natural-log LSE; ``do`` the
-    output gradient.  Masks, bias and scale must be the forward's.  bf16 or fp32.
+    output gradient.  Masks, bias and scale must be the forward's.  bf16, fp16 or fp32.
     """
     dev = _on_device(q, k, v, o, do, lse, bias)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -186,8 +199,8 @@ def flash_attention_bwd(
     code = _dtype_code(q)
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128) and not (D == 256 and q.dtype == torch.bfloat16):
-        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16)")
+    if D not in (64, 128) and not (D == 256 and q.dtype in HALF_DTYPES):
+        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16 / fp16)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))
@@ -239,8 +252,8 @@ def splitkv_decode(
     q, k, v, *, sm_scale: float, kv_lengths=None, chunk: int = 0, return_lse: bool = False,
     workspace=None,
 ):
-    """``pjx_splitkv_decode``: bf16 or fp32 ``q [B, Lq, Hq, D]``,
-    ``k/v [B, S, Hkv, D]``; ``(Hq/Hkv)*Lq`` up to 64 (bf16) or 32 (fp32)."""
+    """``pjx_splitkv_decode``: bf16, fp16 or fp32 ``q [B, Lq, Hq, D]``,
+    ``k/v [B, S, Hkv, D]``; ``(Hq/Hkv)*Lq`` up to 64 (bf16 / fp16) or 32 (fp32)."""
     dev = _on_device(q, k, v)
     if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
         raise ValueError("q must be [B, Lq, Hq, D] and k, v [B, S, Hkv, D]")
@@ -248,10 +261,10 @@ def splitkv_decode(
     _, S, Hkv, Dk = k.shape
     if Dk != D or k.shape[0] != B or Hq % Hkv:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}")
-    if q.dtype not in (torch.bfloat16, torch.float32) or k.dtype != q.dtype or v.dtype != q.dtype:
-        raise ValueError("split-KV decode takes bfloat16 or float32 q, k, v of one dtype")
+    if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
+        raise ValueError("split-KV decode takes bfloat16, float16 or float32 q, k, v of one dtype")
     rows = (Hq // Hkv) * Lq
-    max_rows = 64 if q.dtype == torch.bfloat16 else 32
+    max_rows = 64 if q.dtype in HALF_DTYPES else 32
     if rows > max_rows or D not in (64, 128):
         raise ValueError(f"split-KV decode needs (Hq/Hkv)*Lq <= {max_rows} and head_dim 64 or 128")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
@@ -272,15 +285,14 @@ def mla_decode(
     q, cache, *, sm_scale: float, v_dim: int | None = None, kv_lengths=None, chunk: int = 0,
     return_lse: bool = False, workspace=None,
 ):
-    """``pjx_mla_decode``: bf16 ``q [B, Lq, H, R]`` over ``cache [B, S, R]`` (K = V)."""
+    """``pjx_mla_decode``: bf16 / fp16 ``q [B, Lq, H, R]`` over ``cache [B, S, R]`` (K = V)."""
     dev = _on_device(q, cache)
     if q.ndim != 4 or cache.ndim != 3:
         raise ValueError("q must be [B, Lq, H, R] and cache [B, S, R]")
     B, Lq, H, R = q.shape
     if cache.shape[0] != B or cache.shape[2] != R:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, cache {tuple(cache.shape)}")
-    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
-        raise ValueError("MLA decode takes bfloat16 q and cache")
+    code = _half_code("MLA decode", q, cache)
     dv = R if v_dim is None else int(v_dim)
     if (R, dv) not in ((576, 512), (576, 576), (512, 512), (128, 128)) or Lq * H > 16:
         raise ValueError(f"MLA decode supports (R, v_dim) in (576,512),(576,576),(512,512),(128,128) and Lq*H <= 16; got ({R}, {dv}), Lq*H={Lq * H}")
@@ -289,10 +301,10 @@ def mla_decode(
     L = _lengths(kv_lengths, B, dev)
     nbytes = decode_workspace_bytes(B, 1, Lq * H, S, dv, chunk)
     ws = _workspace(nbytes, dev, workspace)
-    o = torch.empty((B, Lq, H, dv), dtype=torch.bfloat16, device=dev)
+    o = torch.empty((B, Lq, H, dv), dtype=q.dtype, device=dev)
     lse = torch.empty((B, H, Lq), dtype=torch.float32, device=dev) if return_lse else None
     rc = native.load().pjx_mla_decode(
-        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
+        code, _ptr(q), _ptr(cache), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
         nbytes, B, Lq, H, S, R, dv, float(sm_scale), int(chunk), _stream(dev),
     )
     native.check(rc)
@@ -314,8 +326,7 @@ def mla_fwd(
     B, Lq, H, R = q.shape
     if cache.shape[0] != B or cache.shape[2] != R:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, cache {tuple(cache.shape)}")
-    if q.dtype != torch.bfloat16 or cache.dtype != torch.bfloat16:
-        raise ValueError("the latent flash kernel takes bfloat16 q and cache")
+    code = _half_code("the latent flash kernel", q, cache)
     dv = R if v_dim is None else int(v_dim)
     S = cache.shape[1]
     if not sm_scale > 0:
@@ -331,10 +342,10 @@ def mla_fwd(
         bias = bias.to(torch.float32).contiguous()
     L = _lengths(kv_lengths, B, dev)
     ms = _mods_struct(mods, B, Lq, S, H, dev)
-    o = torch.empty((B, Lq, H, dv), dtype=torch.bfloat16, device=dev)
+    o = torch.empty((B, Lq, H, dv), dtype=q.dtype, device=dev)
     lse = torch.empty((B, H, Lq), dtype=torch.float32, device=dev) if return_lse else None
     rc = native.load().pjx_mla_fwd(
-        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(o), _ptr(lse), _ptr(L), _ptr(bias), bb, bh,
+        code, _ptr(q), _ptr(cache), _ptr(o), _ptr(lse), _ptr(L), _ptr(bias), bb, bh,
         B, Lq, S, H, R, dv, Lq if q_valid is None else int(q_valid), S if kv_valid is None else int(kv_valid),
         int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
     )
@@ -347,8 +358,8 @@ def mla_bwd(
     q_valid: int | None = None, kv_valid: int | None = None, mods: ScoreModsArgs | None = None,
     workspace=None,
 ):
-    """``pjx_mla_bwd``: ``(dq, dcache)`` of ``mla_fwd`` (absorbed latent, bf16,
-    rank 512 / 576).  ``o`` / ``do`` are the forward output and its gradient
+    """``pjx_mla_bwd``: ``(dq, dcache)`` of ``mla_fwd`` (absorbed latent, bf16
+    or fp16, rank 512 / 576).  ``o`` / ``do`` are the forward output and its gradient
     ``[B, Lq, H, v_dim]``, ``lse`` the forward's natural-log LSE ``[B, H, Lq]``;
     masks, bias and scale must be the forward's."""
     dev = _on_device(q, cache, o, do, lse, bias)
@@ -361,8 +372,7 @@ def mla_bwd(
         raise ValueError("incompatible shapes for the latent backward")
     if tuple(lse.shape) != (B, H, Lq):
         raise ValueError(f"lse must be [B, H, Lq] = {(B, H, Lq)}")
-    if not all(t.dtype == torch.bfloat16 for t in (q, cache, o, do)):
-        raise ValueError("the latent backward takes bfloat16 q, cache, o, do")
+    code = _half_code("the latent backward", q, cache, o, do)
     q, cache, o, do = (t.contiguous() for t in (q, cache, o, do))
     lse = lse.to(torch.float32).contiguous()
     bb = bh = 1
@@ -378,7 +388,7 @@ def mla_bwd(
     dq = torch.empty_like(q)
     dc = torch.empty_like(cache)
     rc = lib.pjx_mla_bwd(
-        native.PJX_DTYPE_BF16, _ptr(q), _ptr(cache), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dc),
+        code, _ptr(q), _ptr(cache), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq), _ptr(dc),
         _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, S, H, R, dv,
         Lq if q_valid is None else int(q_valid), S if kv_valid is None else int(kv_valid),
         int(bool(causal)), float(sm_scale), None if ms is None else ctypes.byref(ms[0]), _stream(dev),
@@ -400,7 +410,7 @@ def mla_project(cache, wk, wv, *, width: int):
         raise ValueError(f"incompatible shapes cache {tuple(cache.shape)}, wk {tuple(wk.shape)}, wv {tuple(wv.shape)}")
     dv = wv.shape[1]
     if not (cache.dtype == wk.dtype == wv.dtype) or cache.dtype not in _DTYPES:
-        raise ValueError("cache, wk and wv must share one dtype (bfloat16 or float32)")
+        raise ValueError("cache, wk and wv must share one dtype (bfloat16, float16 or float32)")
     cache, wk, wv = cache.contiguous(), wk.contiguous(), wv.contiguous()
     k = torch.empty((B, S, H, width), dtype=cache.dtype, device=dev)
     v = torch.empty((B, S, H, width), dtype=cache.dtype, device=dev)

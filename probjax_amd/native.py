@@ -15,6 +15,7 @@ LIB_PATH = Path(__file__).resolve().parent / "_lib" / "libprobjax_hip.so"
 
 PJX_DTYPE_F32 = 0
 PJX_DTYPE_BF16 = 1
+PJX_DTYPE_F16 = 2
 PJX_OK = 0
 PJX_DECODE_STATIC_SCRATCH_BYTES = 32 << 20  # include/probjax_hip.h
 

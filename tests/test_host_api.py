@@ -139,8 +139,11 @@ def test_eligibility_rejects_without_touching_a_device(monkeypatch):
     assert A._eligible(q, k, v, mask=M.KVLenMask([1, 2]), bias=None, dropout_rate=0.0) is None  # B = 1
     lm, b = A._eligible(q, k, v, mask=M.KVLenMask([7]), bias=None, dropout_rate=0.0)
     assert lm.kv_lengths.dtype == torch.int32 and b is None
-    q16 = q.to(torch.float16)
-    assert A._flash_plan(q16, k, v, M.LoweredMask(), None) is None
+    q64 = q.to(torch.float64)
+    assert A._flash_plan(q64, k, v, M.LoweredMask(), None) is None
+    q16, k16, v16 = (t.to(torch.float16) for t in (q, k, v))
+    assert A._flash_plan(q16, k16, v16, M.LoweredMask(), None) is not None
+    assert A._decode_plan(q16, k16, v16, M.LoweredMask(), None) is not None
     q96 = torch.zeros(1, 4, 4, 96, dtype=torch.bfloat16)
     assert A._flash_plan(q96, q96, q96, M.LoweredMask(), None) is None
 

@@ -184,6 +184,37 @@ def test_bf16_rounds_p_before_pv():
     assert out[0, 0, 0, 0] == want
 
 
+def test_f16_close_to_f32_and_rounds_p():
+    """fp16 mode (the reference's fused paths take float16, layers/attention.py:
+    1187): fp16-valued output within 2e-3 of fp32 (11 significant bits against
+    bf16's 8), and P rounded to fp16 before P.V -- the planted case above,
+    where the fp16 rounding of P moves the output by more than its own
+    output rounding."""
+    q, k, v = rng_normal(10, (1, 64, 2, 32), (1, 64, 2, 32), (1, 64, 2, 32))
+    q, k, v = (oracle.round_f16(x) for x in (q, k, v))
+    ref = oracle.xla_attention(q, k, v, mask=oracle.CausalMask(), sm_scale=1 / math.sqrt(32))
+    for strategy in ("dense", "tiled"):
+        out = oracle.xla_attention(q, k, v, mask=oracle.CausalMask(), sm_scale=1 / math.sqrt(32),
+                                   dtype="f16", strategy=strategy, block_q=16, block_k=16)
+        np.testing.assert_array_equal(out, oracle.round_f16(out))
+        assert 0 < np.max(np.abs(out - ref)) / np.max(np.abs(ref)) < 2e-3
+    q = np.zeros((1, 1, 1, 4), np.float32)
+    k = np.zeros((1, 3, 1, 4), np.float32)
+    v = np.zeros((1, 3, 1, 4), np.float32)
+    q[0, 0, 0, 0] = 1.0
+    k[0, 1, 0, 0] = 0.7
+    v[0, :, 0, 0] = [1.0, -1.0, 1.0]
+    out = oracle.xla_attention(q, k, v, sm_scale=1.0, dtype="f16", compute_dtype=np.float64)
+    s1 = float(oracle.round_f16(np.array([0.7], np.float32))[0])
+    p = np.exp(np.array([0.0, s1, 0.0]) - s1)
+    p = p / p.sum()
+    rp = oracle.round_f16(p.astype(np.float32)).astype(np.float64)
+    want = oracle.round_f16(np.array([rp[0] - rp[1] + rp[2]], np.float32))[0]
+    unrounded = oracle.round_f16(np.array([p[0] - p[1] + p[2]], np.float32))[0]
+    assert want != unrounded
+    assert out[0, 0, 0, 0] == want
+
+
 def test_auto_strategy_table():
     assert oracle.auto_strategy(256, 256) == ("dense", None, None)
     assert oracle.auto_strategy(1, 8192)[0] == "dense"

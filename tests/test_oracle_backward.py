@@ -212,6 +212,26 @@ def test_bf16_within_reference_gradient_tolerance():
     assert all(np.array_equal(x, oracle.round_bf16(x)) for x in g16)
 
 
+def test_f16_within_tolerance_and_rounded():
+    """fp16 mode: gradients within 2e-3 of fp32 (closer than bf16 mode), fp16
+    valued, and really rounded (P and dS cast to fp16, not a relabelled fp32 run)."""
+    B, L, Hq, Hkv, D = 1, 64, 4, 2, 32
+    q, k, v, do = (oracle.round_f16(x) for x in rng_normal(6, (B, L, Hq, D), (B, L, Hkv, D),
+                                                          (B, L, Hkv, D), (B, L, Hq, D)))
+    scale = 1.0 / math.sqrt(D)
+    mask = oracle.CausalMask()
+    o32, lse32 = _forward(q, k, v, mask=mask, scale=scale, cdt=np.float32)
+    oh, lseh = _forward(q, k, v, mask=mask, scale=scale, dtype="f16", cdt=np.float32)
+    g32 = attention_backward(q, k, v, o32, do, lse32, mask=mask, sm_scale=scale)
+    gh = attention_backward(q, k, v, oh, do, lseh, mask=mask, sm_scale=scale, dtype="f16")
+    gb = attention_backward(q, k, v, o32, do, lse32, mask=mask, sm_scale=scale, dtype="bf16")
+    for a, b, c in zip(gh, g32, gb):
+        np.testing.assert_allclose(a, b, atol=2e-3, rtol=2e-3)
+        assert np.max(np.abs(a - b)) < np.max(np.abs(c - b))
+    assert any(np.max(np.abs(a - b)) > 0 for a, b in zip(gh, g32))
+    assert all(np.array_equal(x, oracle.round_f16(x)) for x in gh)
+
+
 @pytest.mark.parametrize("kind", ["softcap", "headscale", "alibi", "window", "segments", "prefix"])
 def test_backward_with_score_modifiers_and_masks_matches_torch(kind):
     """The oracle's modifier derivatives and extended masks against torch
