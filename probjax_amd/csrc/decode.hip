@@ -13,13 +13,13 @@
 // Work decomposition (HBM-bound; compute is a few % of the MFMA rate):
 //   * one workgroup per (batch, kv group, chunk of `chunk` keys); chunks past
 //     the sequence's length exit at once, so only valid K/V is ever read;
-//   * per 64-key tile, wave w loads keys [16w, 16w+16) directly from HBM as
-//     the A operand of v_mfma_f32_16x16x32_bf16 (16-byte loads, 256 B per
-//     row) and computes S^T (keys x 16 rows); the values are also scattered
-//     into V^T in LDS (the shared latent is read once for both products);
-//   * every wave reads the 64 x 16 score tile back from LDS, runs the online
-//     softmax redundantly, and multiplies its own share of the output dims:
-//     O^T[d][row] += V^T P^T, with V^T read as one 16-byte LDS load per step;
+//   * GQA (gqa_decode_kernel): the 4 waves split the chunk's keys, load K rows
+//     straight into MFMA operands and V through a per-wave LDS slab, and
+//     combine their (max, sum, O) in LDS at the end;
+//   * latent (mla_decode_kernel): 64-key tiles of the shared latent go
+//     HBM -> LDS; each wave forms S^T for 16 keys, the 64 x 16 score tile is
+//     shared through LDS, every wave runs the same online softmax over it and
+//     multiplies its own quarter of the output dims, so no combine is needed;
 //   * the merge kernel combines the chunks of one (batch, group) exactly.
 // Inputs are bf16 or fp16 (the kernels are templated on the 16-bit format;
 // the v_mfma_*_bf16 named here are v_mfma_*_f16 for fp16) or fp32 (GQA only).
@@ -609,13 +609,19 @@ __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
 //   * Each 64-key tile is contiguous in HBM (64 rows x 2D bytes) and is copied
 //     HBM -> LDS with buffer->LDS loads, 1 KiB per wave instruction; the next
 //     tile is in flight while the current one is computed.
-//   * Wave w owns keys [16w, 16w+16) of every tile and keeps its own online
-//     softmax: S^T = K Q^T with v_mfma_f32_16x16x32_bf16 (K rows from LDS,
-//     Q^T in registers), then O^T += V^T P^T with v_mfma_f32_16x16x16_bf16,
-//     whose B operand is the score accumulator as it stands and whose A
-//     operand (V^T) comes from the same LDS tile through ds_read_b64_tr_b16.
-//     The latent row is read from HBM once and from LDS twice.
-//   * The four waves' (max, sum, O) are combined in LDS at the end.
+//   * Wave w forms S^T = K Q^T for keys [16w, 16w+16) of every tile with
+//     v_mfma_f32_16x16x32_bf16 (K rows from LDS, Q^T in registers) and writes
+//     it to LDS (1 KiB); after a barrier every wave reads the whole 64 x 16
+//     score tile, runs the online softmax over it (the same values in every
+//     wave) and computes O^T += V^T P^T for its DV/4 output dims over all 64
+//     keys with v_mfma_f32_16x16x16_bf16, whose B operands are the shared
+//     score blocks as they stand (the C layout of S^T is the B layout of
+//     P^T) and whose A operands (V^T) come from the same LDS tile through
+//     ds_read_b64_tr_b16.  The latent row is read from HBM once and from LDS
+//     twice.
+//   * Each wave ends with the finished (max, sum, O) of its dims: nothing is
+//     combined across waves (a combine of four key-split partials through LDS
+//     took ~2.6 us of the C5 step).
 // LDS rows keep their 16-byte columns XOR-swizzled per row (within aligned
 // groups of 8 or 16 columns), so that 16 lanes reading one column of 16 rows
 // (K fragments) and 32 lanes reading two columns of 8 rows (transposing V
@@ -645,15 +651,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
   constexpr int BK = T::BK, ROWB = T::ROWB, NLD = T::NLD, GRP = T::GRP;
   constexpr int KSTEPS = D / 32;  // 32-dim k-steps of Q.K
   constexpr int SPG = GRP / 4;    // k-steps per swizzle group
-  constexpr int NDT = DV / 16;    // 16-dim output tiles, all held by every wave
+  constexpr int NDT = DV / 16;    // 16-dim output tiles
+  constexpr int NDW = NDT / 4;    // output tiles of one wave
   constexpr int DPG = GRP / 2;    // output tiles per swizzle group
   static_assert(DV % 64 == 0 && DV <= D, "value dims are a prefix of the latent row");
   static_assert(KSTEPS % SPG == 0 && NDT % DPG == 0, "swizzle groups");
-  // The combine at the end puts 2 waves' O (16 rows x DV floats each) in each stage.
-  static_assert(2 * kRows * DV * 4 <= T::STAGE_B, "combine scratch fits");
   __shared__ __attribute__((aligned(1024))) unsigned char smem0[T::STAGE_B];
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[T::STAGE_B];
-  __shared__ float red_ml[4 * kRows * 2];
+  __shared__ f32x4 sx[4 * 64];  // the tile's S^T blocks, one per wave, in MFMA C layout
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -697,20 +702,22 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
 #pragma unroll
     for (int e = 0; e < SPG; ++e) offK[e] = r * ROWB + 16 * ((4 * e + q4) ^ T::swz(r));
   }
-  // Transposing V^T read for output tile dt (dims 16*dt + [0,16), keys
-  // 16w + 4*q4 + [0,4)): lane s of each 16-lane group points at row
-  // 16w + 4*q4 + s/4, dims 16*dt + 4*(s%4) + [0,4).
+  // Transposing V^T read for output tile dt (dims 16*dt + [0,16)) and key
+  // block kb (keys 16kb + 4*q4 + [0,4)): lane s of each 16-lane group points
+  // at row 16kb + 4*q4 + s/4, dims 16*dt + 4*(s%4) + [0,4).  The swizzle of a
+  // row depends on it modulo 16 only, so key block kb is offV + 16*kb rows.
   uint32_t offV[DPG];
   {
-    const int r = 16 * w + 4 * q4 + (c16 >> 2);
+    const int r = 4 * q4 + (c16 >> 2);
 #pragma unroll
     for (int e = 0; e < DPG; ++e)
       offV[e] = r * ROWB + 16 * ((2 * e + ((c16 & 3) >> 1)) ^ T::swz(r)) + 8 * (c16 & 1);
   }
 
-  f32x4 acc[NDT];
+  // acc[i] = O^T[dims 16*(NDW*w + i) + 4*q4 + r][row c16]
+  f32x4 acc[NDW];
 #pragma unroll
-  for (int i = 0; i < NDT; ++i) acc[i] = f32x4{};
+  for (int i = 0; i < NDW; ++i) acc[i] = f32x4{};
   float m_run = kMaxInit, l_run = 0.f;
 
   auto issue = [&](int t, unsigned char* ks) {
@@ -724,6 +731,9 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
     for (int j = 0; j < NLD; ++j) buffer_load_lds16(rs, ks + (NLD * w + j) * 1024, voff[j]);
   };
 
+  // One tile: wave w forms S^T for its 16 keys and shares it; every wave runs
+  // the softmax over all 64 keys (the same values in every wave) and
+  // multiplies its own NDW output tiles over all 64 keys.
   auto compute = [&](int t, const unsigned char* ks) {
     const int k0 = c0 + t * BK;
     // s[r] = S^T[key k0 + 16w + 4*q4 + r][row c16]
@@ -739,7 +749,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
       for (int r = 0; r < 4; ++r)
         if (r >= lim) s[r] = -INFINITY;
     }
-    float mx = fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3]));
+    sx[w * 64 + lane] = s;
+    stage_barrier();
+    f32x4 sk[4];  // sk[kb][r] = S^T[key k0 + 16kb + 4*q4 + r][row c16]
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) sk[kb] = sx[kb * 64 + lane];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) mx = fmaxf(mx, fmaxf(fmaxf(sk[kb][0], sk[kb][1]), fmaxf(sk[kb][2], sk[kb][3])));
     mx = xor16_max(mx);
     const float mc = xor32_max(mx) * a.cx;
     if (wave_any(mc > m_run + kRescaleLog2)) {
@@ -748,25 +765,36 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
       m_run = m_new;
       l_run *= corr;
 #pragma unroll
-      for (int i = 0; i < NDT; ++i) acc[i] *= corr;
+      for (int i = 0; i < NDW; ++i) acc[i] *= corr;
     }
-    float p[4];
+    s16x4 pb[4];
+    float ls = 0.f;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) p[r] = fast_exp2(fmaf(s[r], a.cx, -m_run));
-    l_run += (p[0] + p[1]) + (p[2] + p[3]);
-    const u32x2 pk = {E::pack2(p[0], p[1]), E::pack2(p[2], p[3])};
-    const s16x4 pb = __builtin_bit_cast(s16x4, pk);
+    for (int kb = 0; kb < 4; ++kb) {
+      float p[4];
 #pragma unroll
-    for (int dt = 0; dt < NDT; ++dt) {
-      const u32x2 av = lds_read_tr16(ks + offV[dt % DPG] + 16 * GRP * (dt / DPG));
-      acc[dt] = E::mma16k16(__builtin_bit_cast(s16x4, av), pb, acc[dt]);
+      for (int r = 0; r < 4; ++r) p[r] = fast_exp2(fmaf(sk[kb][r], a.cx, -m_run));
+      ls += (p[0] + p[1]) + (p[2] + p[3]);
+      const u32x2 pk = {E::pack2(p[0], p[1]), E::pack2(p[2], p[3])};
+      pb[kb] = __builtin_bit_cast(s16x4, pk);
+    }
+    l_run += ls;
+#pragma unroll
+    for (int i = 0; i < NDW; ++i) {
+      const int dt = NDW * w + i;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const u32x2 av = lds_read_tr16(ks + 16 * kb * ROWB + offV[dt % DPG] + 16 * GRP * (dt / DPG));
+        acc[i] = E::mma16k16(__builtin_bit_cast(s16x4, av), pb[kb], acc[i]);
+      }
     }
   };
 
   // Tile t lives in stage t % 2.  Before computing tile t: this wave's loads
   // of it have landed (vmcnt counts loads in issue order and only tile t+1's
-  // may still be pending), then the barrier makes every wave's loads visible.
-  // After computing it, a barrier lets tile t+2 be loaded into the same stage.
+  // may still be pending), then the barrier makes every wave's loads visible
+  // (each wave reads V^T rows of all four waves).  After computing it, a
+  // barrier lets tile t+2 be loaded into the same stage.
   // Every path issues the same sequence of loads (tiles past the chunk are
   // empty) and the loop has no early exit, so the compiler can tell that at
   // each read of a stage the NLD most recent loads target the other stage,
@@ -790,50 +818,18 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
     stage_barrier();
     issue(t + 3, smem1);
   }
+  wait_vmcnt<0>();  // the trailing (empty) tile loads still write LDS
 
-  // ---- combine the four waves: O^T in LDS, float4 columns XOR-swizzled by row ----
+  // Every wave holds the same (max, sum) and the whole output of its dims:
+  // no combine across waves.
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
-  wait_vmcnt<0>();  // the trailing (empty) tile loads still write LDS
-  __syncthreads();  // every wave is done with both stages
-  {
-    // Waves 0, 1 write stage 0, waves 2, 3 stage 1 (a branch, not a pointer
-    // select, keeps every LDS access tied to one array for the compiler).
-    auto put = [&](unsigned char* st) {
-      float* ro = (float*)st + (w & 1) * kRows * DV;
+  if (c16 < a.rows) {
+    const size_t part = (size_t)b * a.nch + chunk_id;
+    const bool final_out = c0 == 0 && L <= a.chunk;
 #pragma unroll
-      for (int dt = 0; dt < NDT; ++dt)
-        *(f32x4*)(ro + c16 * DV + 4 * ((4 * dt + q4) ^ c16)) = acc[dt];  // O[row c16][16dt + 4q4 + r]
-    };
-    if (w < 2) put(smem0); else put(smem1);
-    if (q4 == 0) {
-      red_ml[(w * kRows + c16) * 2] = m_run;
-      red_ml[(w * kRows + c16) * 2 + 1] = l_run;
-    }
-  }
-  __syncthreads();
-  const size_t part = (size_t)b * a.nch + chunk_id;
-  const bool final_out = c0 == 0 && L <= a.chunk;
-  constexpr int NQ = DV / 4;  // float4 columns per row
-  for (int idx = tid; idx < kRows * NQ; idx += kDecThreads) {
-    const int r = idx / NQ, u = idx % NQ;
-    if (r >= a.rows) break;
-    float mw[4], M = kMaxInit;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      mw[ww] = red_ml[(ww * kRows + r) * 2];
-      M = fmaxf(M, mw[ww]);
-    }
-    float Ls = 0.f;
-    f32x4 O = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) {
-      const float wt = fast_exp2(mw[ww] - M);
-      Ls = fmaf(wt, red_ml[(ww * kRows + r) * 2 + 1], Ls);
-      const float* ro = (const float*)(ww < 2 ? smem0 : smem1) + (ww & 1) * kRows * DV;
-      O += wt * *(const f32x4*)(ro + r * DV + 4 * (u ^ (r & 15)));
-    }
-    emit_row_quad(a, b, 0, r, 4 * u, part, final_out, M, Ls, O);
+    for (int i = 0; i < NDW; ++i)
+      emit_row_quad(a, b, 0, c16, 16 * (NDW * w + i) + 4 * q4, part, final_out, m_run, l_run, acc[i]);
   }
 }
 
