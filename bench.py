@@ -135,7 +135,7 @@ def make_c2(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="C2 causal fwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<128,32,3>")
+                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3>")
 
 
 def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
@@ -160,7 +160,7 @@ def make_c3(dev, gen):
     fn = lambda: splitkv_decode(q, k, v, sm_scale=1 / math.sqrt(D), kv_lengths=L, workspace=ws)  # noqa: E731
     return dict(name="C3 GQA split-KV decode bf16 B=32 Hq=32 Hkv=8 D=128 S=8192 ragged",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="gqa_decode_kernel<128> + decode_merge_kernel", sum_len=tot)
+                kernel="gqa_decode_kernel<Bf16Fmt,128,1> + decode_merge_kernel", sum_len=tot)
 
 
 def c4_lengths(seed=0, batch=2, length=2048):
@@ -183,7 +183,7 @@ def make_c4(dev, gen):
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, kv_lengths=L_, bias=bias)  # noqa: E731
     return dict(name="C4 bias+kvlen fwd bf16 B=2 H=8 L=2048 D=64, bias f32 [8,2048,2048]",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="flash_fwd_bf16_bias_ring_kernel<64>")
+                kernel="flash_fwd_bf16_bias_ring_kernel<Bf16Fmt,64>")
 
 
 def make_c5(dev, gen):
@@ -199,7 +199,7 @@ def make_c5(dev, gen):
     fn = lambda: mla_decode(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, workspace=ws)  # noqa: E731
     return dict(name="C5 MLA absorbed decode bf16 B=16 H=16 S=4096 R=576 Dv=512",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="mla_decode_kernel<576,512> + decode_merge_kernel")
+                kernel="mla_decode_kernel<Bf16Fmt,576,512> + decode_merge_kernel")
 
 
 def _c2_train_inputs(dev, gen):
@@ -230,7 +230,7 @@ def make_c2b(dev, gen):
                                      workspace=ws)
     return dict(name="C2 causal bwd bf16 B=4 H=16 L=4096 D=128 (dq, dk, dv)", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_bwd_dq_kernel<128,0,0> + flash_bwd_dkdv_kernel<128,false,0>")
+                kernel="flash_bwd_dq_kernel<Bf16Fmt,128,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0>")
 
 
 def make_c2fb(dev, gen):
@@ -251,7 +251,7 @@ def make_c2fb(dev, gen):
     nbytes = 2 * B * L * H * D * 2 * 5 + B * H * L * 4
     return dict(name="C2 causal fwd+bwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_fwd_bf16_pipe_kernel<128,32,3> + flash_bwd_dq_kernel<128,0,0> + flash_bwd_dkdv_kernel<128,false,0>")
+                kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3> + flash_bwd_dq_kernel<Bf16Fmt,128,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0>")
 
 
 def _mla_prefill_inputs(dev, gen):
@@ -274,7 +274,7 @@ def make_c5p(dev, gen):
     nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
     fn = lambda: mla_project(cache, wk, wv, width=D)  # noqa: E731
     return dict(name="MLA up-projection bf16 B=1 S=4096 R=512 H=16 dk=dv=128 (K and V)", fn=fn,
-                flop=flop, bytes=nbytes, bound="mfma", dtype="bf16", kernel="mla_project_bf16_kernel")
+                flop=flop, bytes=nbytes, bound="mfma", dtype="bf16", kernel="mla_project_bf16_kernel<Bf16Fmt>")
 
 
 def make_c5m(dev, gen):
@@ -294,7 +294,7 @@ def make_c5m(dev, gen):
     nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
     return dict(name="MLA materialised causal prefill bf16 B=1 L=4096 R=512 H=16 dk=dv=128", fn=fn,
                 flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="mla_project_bf16_kernel + flash_fwd_bf16_pipe_kernel<128,64,2>")
+                kernel="mla_project_bf16_kernel<Bf16Fmt> + flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,64,2>")
 
 
 def _latent_prefill_inputs(dev, gen):
@@ -320,7 +320,7 @@ def make_c5a(dev, gen):
     nbytes = B * L * H * R * 2 + B * L * R * 2 + B * L * H * DV * 2
     fn = lambda: mla_fwd(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, causal=True)  # noqa: E731
     return dict(name="MLA absorbed causal prefill bf16 B=1 L=4096 H=16 R=576 Dv=512", fn=fn, flop=flop,
-                bytes=nbytes, bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<576,256,32,true,false,0>")
+                bytes=nbytes, bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<Bf16Fmt,576,256,32,true,false,0>")
 
 
 def make_c5ab(dev, gen):
@@ -339,7 +339,7 @@ def make_c5ab(dev, gen):
     fn = lambda: mla_bwd(q, cache, o, do, lse, sm_scale=sc, causal=True)  # noqa: E731
     return dict(name="MLA absorbed causal prefill backward bf16 B=1 L=4096 H=16 R=576 Dv=512 (dq, dcache)",
                 fn=fn, flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="wide_bwd_dq_kernel<576,512,true,0,0> + wide_bwd_dkdv_kernel<576,512,true,false,0> + wide_bwd_reduce_kernel")
+                kernel="wide_bwd_dq_kernel<Bf16Fmt,576,512,true,0,0> + wide_bwd_dkdv_kernel<Bf16Fmt,576,512,true,false,0> + wide_bwd_reduce_kernel<Bf16Fmt>")
 
 
 def make_c2w(dev, gen):
@@ -354,7 +354,7 @@ def make_c2w(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="causal fwd bf16 B=2 H=16 L=4096 D=256", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<256,256,32,false,false,0>")
+                bound="mfma", dtype="bf16", kernel="flash_fwd_wide_kernel<Bf16Fmt,256,256,32,false,false,0>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
@@ -412,7 +412,7 @@ def _rates(w, ms):
     return tflops, gbs, frac
 
 
-TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench_c1_c5.json")
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "hbm_traffic_bench.json")
 
 
 def measured_traffic(kernel_key):
@@ -524,7 +524,7 @@ def main():
                        "head_dim": 128, "mask": "causal", "flop_per_step": w["flop"]},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(frac, 4),
-                         "traffic": measured_traffic("pjx::flash_fwd_bf16_pipe_kernel<128, 32, 3>"),
+                         "traffic": measured_traffic("pjx::flash_fwd_bf16_pipe_kernel<pjx::Bf16Fmt, 128, 32, 3>"),
                          "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
                          "kernel": w["kernel"]},
         })
@@ -532,8 +532,8 @@ def main():
         r = results["C3"]
         out["decode_roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": PEAK_HBM_GBS,
                                   "unit": "GB/s", "frac": r["roofline_frac"],
-                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<128>"),
-                                  "kernel": "gqa_decode_kernel<128> + decode_merge_kernel"}
+                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<pjx::Bf16Fmt, 128, 1>"),
+                                  "kernel": "gqa_decode_kernel<Bf16Fmt,128,1> + decode_merge_kernel"}
     out["configs"] = results
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()
