@@ -443,8 +443,12 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArg
     accv[i] = f32x16{};
   }
 
-  auto tile_head = [&](int t) { return hkv * G + t / n_qt; };
-  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * kBQs; };
+  // Query tiles last to first, the group's heads innermost: the workgroups of
+  // one KV head's key blocks (same XCD, running together) then stream the same
+  // Q / dO tile at the same time, so all but the first read it from L2
+  // (causal: each starts at the sequence's end and stops at its own keys).
+  auto tile_head = [&](int t) { return hkv * G + t % G; };
+  auto tile_q0 = [&](int t) { return q_begin + (n_qt - 1 - t / G) * kBQs; };
 
   auto issue = [&](int t, unsigned char* st) {
     const int h = tile_head(t), q0 = tile_q0(t);
@@ -913,8 +917,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
 
   f32x4 qreg[PER_T], dreg[PER_T];
   float lreg = 0.f;
-  auto tile_head = [&](int t) { return hkv * G + t / n_qt; };
-  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * BQ; };
+  // last query tile first, heads innermost (as the bf16 kernel)
+  auto tile_head = [&](int t) { return hkv * G + t % G; };
+  auto tile_q0 = [&](int t) { return q_begin + (n_qt - 1 - t / G) * BQ; };
   auto load_tile = [&](int t) {
     const int h = tile_head(t), q0 = tile_q0(t);
     const float* Qb = (const float*)a.q + ((size_t)b * a.Lq * a.Hq + h) * D;

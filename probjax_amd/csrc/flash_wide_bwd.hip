@@ -476,8 +476,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
     for (int i = 0; i < NV; ++i) accv[i] = f32x4{};
   }
 
-  auto tile_head = [&](int t) { return h_first + t / n_qt; };
-  auto tile_q0 = [&](int t) { return q_begin + (t % n_qt) * kWT; };
+  // Query tiles last to first, the group's heads innermost: the workgroups of
+  // one head group's key tiles (same XCD, running together) then stream the
+  // same Q / dO tile at the same time, so all but the first read it from L2.
+  auto tile_head = [&](int t) { return h_first + t % gs; };
+  auto tile_q0 = [&](int t) { return q_begin + (n_qt - 1 - t / gs) * kWT; };
 
   auto issue = [&](int t, unsigned char* st) {
     const int h = tile_head(t), q0 = tile_q0(t);
