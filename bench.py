@@ -138,6 +138,20 @@ def make_c2(dev, gen):
                 bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3>")
 
 
+def make_c2h(dev, gen):
+    """C2 in float16 (the same kernel on v_mfma_f32_32x32x16_f16)."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_fwd
+
+    B, L, H, D = 4, 4096, 16, 128
+    q, k, v = (_randn((B, L, H, D), gen, dev, torch.float16) for _ in range(3))
+    flop = 4 * B * H * L * L * D / 2
+    nbytes = 4 * B * L * H * D * 2
+    fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
+    return dict(name="C2 causal fwd fp16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
+                bound="mfma", dtype="f16", kernel="flash_fwd_bf16_pipe_kernel<F16Fmt,128,32,3>")
+
+
 def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
     """Per-sequence valid lengths, uniform integers in [lo, hi] (seeded)."""
     return np.random.default_rng(seed).integers(lo, hi + 1, size=batch).astype(np.int32)
@@ -359,7 +373,7 @@ def make_c2w(dev, gen):
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
           "C2B": make_c2b, "C2FB": make_c2fb, "C5P": make_c5p, "C5M": make_c5m,
-          "C5A": make_c5a, "C5AB": make_c5ab, "C2W": make_c2w}
+          "C5A": make_c5a, "C5AB": make_c5ab, "C2W": make_c2w, "C2H": make_c2h}
 
 
 def _settle(fn, seconds):
