@@ -469,6 +469,24 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
         acc[db] = E::mma32(E::as8(av), pf[c], acc[db]);
       }
     }
+    // 32-key tiles: issue order of the block is each S_{t+1} MFMA followed by
+    // 5 VALU instructions (tile t's scaling, exponentials, sums and packing),
+    // then the P.V MFMAs each followed by one.  Left to itself the scheduler
+    // places every exponential ahead of the MFMAs: measured 1.3-1.9% slower on
+    // C2; the 64-key form is 5% faster left alone.
+    if constexpr (BK == 32) {
+      constexpr int NQK = D / 16, NPV = D / 16;
+#pragma unroll
+      for (int i = 0; i < NQK; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+        __builtin_amdgcn_sched_group_barrier(0x402, 5, 0);  // VALU incl. transcendental
+      }
+#pragma unroll
+      for (int i = 0; i < NPV; ++i) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x402, 1, 0);
+      }
+    }
   };
 
   f32x16 sa[BK / 32], sb[BK / 32];
