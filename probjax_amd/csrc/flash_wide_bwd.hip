@@ -611,6 +611,213 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
   }
 }
 
+// ---------------------------------------------------------------------------
+// dC of the shared latent without bias or extended masks: the workgroup of
+// wide_bwd_dkdv_kernel (64 keys, one query-head group, Q / dO tiles of 32
+// rows through LDS) with the dC update split by columns instead of keys.
+// Wave w forms S, dP, P and dS for keys k0 + 16w .. +15 as there, and posts P
+// and dS (its two 16-bit B operands, 1 KiB each) to LDS.  After a barrier it
+// accumulates dC^T for the 16-column blocks i = w + 4j over all 64 keys: blocks
+// below DV/16 take Q^T dS and dO^T P into one accumulator, the rest Q^T dS.
+// A wave then reads the transposed Q / dO fragments of its own blocks only (a
+// quarter of the tile) where the key split reads all of them in every wave.
+// ---------------------------------------------------------------------------
+template <typename E, int D, int DV>
+__global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  using RQ = Row16<D>;
+  using RD = Row16<DV>;
+  using OQ = Offs16<E, D>;
+  using OD = Offs16<E, DV>;
+  constexpr int QT_B = RQ::TILE_B, DT_B = RD::TILE_B;
+  constexpr int SMALL_B = 2 * 64 * 4;  // lse*log2e and delta of the tile's rows
+  constexpr int STAGE_B = QT_B + DT_B + SMALL_B;
+  constexpr int KS = D / 32, VS = DV / 32, ND = D / 16, NV = DV / 16;
+  constexpr int NJ = ND / 4, NJV = NV / 4;  // column blocks per wave, those with dV first
+  static_assert(ND % 4 == 0 && NV % 4 == 0 && DV <= D, "column blocks split evenly over the 4 waves");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) u32x4 xp[4 * 2 * 64];  // [wave][P, dS][lane]
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, qd = lane >> 4;
+  const int nsplit = ba.nsplit;
+  const int split = (int)blockIdx.x % nsplit;
+  const int rest = (int)blockIdx.x / nsplit;
+  const int b = rest % a.B;  // one latent (Hkv = 1)
+  const int k0 = (rest / a.B) * kWK;
+  const int gs = a.Hq / nsplit;  // query heads of this group
+  const int h_first = split * gs;
+  const int kw = __builtin_amdgcn_readfirstlane(k0 + 16 * w);
+  const int key = kw + c;
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  const int q_hi = min(a.Lq, a.q_valid);
+  const int q_begin = a.causal ? (k0 / kWT) * kWT : 0;
+  const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + kWT - 1) / kWT : 0;
+  const int n_tiles = gs * n_qt;
+
+  // K^T as the B operand of S and dP: lane holds key `key`, dims 32*st + 8*qd + [0,8).
+  typename E::v8 kf[KS];
+  {
+    const bool kin = key < a.Lk;
+    const uint16_t* krow = (const uint16_t*)a.k + (size_t)(b * a.Lk + (kin ? key : 0)) * D;
+#pragma unroll
+    for (int st = 0; st < KS; ++st) {
+      u32x4 r = {0u, 0u, 0u, 0u};
+      if (kin) r = *(const u32x4*)(krow + 32 * st + 8 * qd);
+      kf[st] = E::as8(r);
+    }
+  }
+  const float cx = a.scale * kLog2e;
+  const uint32_t qrowstride = (uint32_t)a.Hq * 2 * D;
+  const uint32_t drowstride = (uint32_t)a.Hq * 2 * DV;
+  OQ oq;
+  oq.init(lane, w, qrowstride);
+  OD od;
+  od.init(lane, w, drowstride);
+  // Transposed-read offsets (Offs16::trans) of this wave's column blocks w + 4j.
+  uint32_t offq[NJ], offd[NJV];
+  {
+    const int rl = 4 * qd + (c >> 2), bsel = (c & 3) >> 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = w + 4 * j;
+      offq[j] = 16 * RQ::G * (i / OQ::PT) + rl * RQ::ROWB + 16 * ((2 * (i % OQ::PT) + bsel) ^ RQ::swz(rl)) + 8 * (c & 1);
+    }
+#pragma unroll
+    for (int j = 0; j < NJV; ++j) {
+      const int i = w + 4 * j;
+      offd[j] = 16 * RD::G * (i / OD::PT) + rl * RD::ROWB + 16 * ((2 * (i % OD::PT) + bsel) ^ RD::swz(rl)) + 8 * (c & 1);
+    }
+  }
+  auto trans_at = [](const unsigned char* tile, uint32_t off, int rowb) {
+    const u32x2 lo = lds_read_tr16(tile + off);
+    const u32x2 hi = lds_read_tr16(tile + off + 16 * rowb);
+    const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+    return E::as8(v);
+  };
+
+  // acc[j][kb][r] = dC^T[16 (w + 4j) + 4qd + r][k0 + 16kb + c]
+  f32x4 acc[NJ][4];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) acc[j][kb] = f32x4{};
+
+  // Query tiles last to first, the group's heads innermost (as in wide_bwd_dkdv_kernel).
+  auto tile_head = [&](int t) { return h_first + t % gs; };
+  auto tile_q0 = [&](int t) { return q_begin + (n_qt - 1 - t / gs) * kWT; };
+
+  auto issue = [&](int t, unsigned char* st) {
+    const int h = tile_head(t), q0 = tile_q0(t);
+    const int n = max(min(kWT, a.Lq - q0), 1);
+    oq.load(st, (const unsigned char*)a.q + ((size_t)(b * a.Lq + q0) * a.Hq + h) * (2 * D), qrowstride, n, w);
+    od.load(st + QT_B, (const unsigned char*)ba.dout + ((size_t)(b * a.Lq + q0) * a.Hq + h) * (2 * DV),
+            drowstride, n, w);
+    if (w < 2) {
+      const size_t loff = ((size_t)b * a.Hq + h) * a.Lq + q0;
+      const rsrc_t rl = make_rsrc((w == 0 ? ba.lse2 : ba.delta) + loff, (uint32_t)n * 4);
+      buffer_load_lds4(rl, st + QT_B + DT_B + w * 256, 4 * (lane & 31));
+    }
+  };
+
+  auto compute = [&](int t, const unsigned char* st) {
+    const int q0 = tile_q0(t);
+    if (q0 >= q_hi) return;  // uniform over the workgroup
+    const unsigned char* qs = st;
+    const unsigned char* dos = st + QT_B;
+    // P and dS of this wave's keys (zero where no row of the tile sees them)
+    u32x4 pbv = {0u, 0u, 0u, 0u}, dsv = pbv;
+    if (kw < kv_end && !(a.causal && q0 + kWT - 1 < kw)) {
+      const float* lsm = (const float*)(st + QT_B + DT_B);
+      const float* dlm = lsm + 64;
+      f32x4 sx[2], dpx[2];
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        sx[rb] = f32x4{};
+        dpx[rb] = f32x4{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) sx[rb] = E::mma16(oq.rows(qs, rb, s), kf[s], sx[rb]);
+#pragma unroll
+        for (int s = 0; s < VS; ++s) dpx[rb] = E::mma16(od.rows(dos, rb, s), kf[s], dpx[rb]);
+      }
+#pragma unroll
+      for (int rb = 0; rb < 2; ++rb) {
+        const int q4 = q0 + 16 * rb + 4 * qd;
+        const f32x4 l4 = *(const f32x4*)(lsm + 16 * rb + 4 * qd);
+        const f32x4 d4 = *(const f32x4*)(dlm + 16 * rb + 4 * qd);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int qr = q4 + r;
+          const bool keep = key < kv_end && qr < q_hi && (!a.causal || qr >= key);
+          const float p = keep ? fast_exp2(fmaf(sx[rb][r], cx, -l4[r])) : 0.f;
+          sx[rb][r] = p;
+          dpx[rb][r] = p * (dpx[rb][r] - d4[r]) * a.scale;
+        }
+      }
+      pbv = __builtin_bit_cast(u32x4, pack_slots<E>(sx[0], sx[1]));
+      dsv = __builtin_bit_cast(u32x4, pack_slots<E>(dpx[0], dpx[1]));
+    }
+    xp[(2 * w) * 64 + lane] = pbv;
+    xp[(2 * w + 1) * 64 + lane] = dsv;
+    stage_barrier();
+    typename E::v8 pk[4], dk[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      pk[kb] = E::as8(xp[(2 * kb) * 64 + lane]);
+      dk[kb] = E::as8(xp[(2 * kb + 1) * 64 + lane]);
+    }
+    // dC^T[block w + 4j][keys] += Q^T dS (+ dO^T P below DV)
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const typename E::v8 fq = trans_at(qs, offq[j], RQ::ROWB);
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) acc[j][kb] = E::mma16(fq, dk[kb], acc[j][kb]);
+      if (j < NJV) {
+        const typename E::v8 fd = trans_at(dos, offd[j < NJV ? j : 0], RD::ROWB);
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) acc[j][kb] = E::mma16(fd, pk[kb], acc[j][kb]);
+      }
+    }
+  };
+
+  // The ring of wide_bwd_dkdv_kernel; each compute adds one barrier between
+  // the xp writes and reads, and the next xp writes follow the next ring
+  // barrier.
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(t, smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(t + 1, smem1);
+  }
+
+  const size_t nrows = (size_t)a.B * a.Lk;
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const int kk = k0 + 16 * kb + c;
+    if (kk >= a.Lk) continue;
+    const size_t krow = (size_t)b * a.Lk + kk;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int col = 16 * (w + 4 * j) + 4 * qd;
+      if (nsplit == 1) {
+        const u32x2 pkd = {E::pack2(acc[j][kb][0], acc[j][kb][1]), E::pack2(acc[j][kb][2], acc[j][kb][3])};
+        *(u32x2*)((uint16_t*)ba.dk + krow * D + col) = pkd;
+      } else {
+        *(f32x4*)(ba.part + ((size_t)split * nrows + krow) * D + col) = acc[j][kb];
+      }
+    }
+  }
+}
+
 // Sums the head-group partials in split order and rounds to the 16-bit format:
 // out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
 template <typename E>
@@ -673,8 +880,12 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
 #define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
     if (ext) {
       if (hb) PJX_KV(true, 2); else PJX_KV(false, 2);
+    } else if (hb) {
+      PJX_KV(true, 0);
+    } else if constexpr (SHARED) {
+      hipLaunchKernelGGL((wide_bwd_dc_kernel<E, D, DV>), dim3((unsigned)kv_blocks), blk, 0, s, ba);
     } else {
-      if (hb) PJX_KV(true, 0); else PJX_KV(false, 0);
+      PJX_KV(false, 0);
     }
 #undef PJX_KV
     rc = check_launch(who);

@@ -87,6 +87,10 @@ _CASES = [
     ("folded_kvlen_bias", "bf16", 2, 64, 640, 16, 576, 512, "kvlen", "dense_folded", True, True),
     ("folded_causal", "bf16", 1, 40, 300, 8, 576, 576, "causal", None, True, False),
     ("causal_r512", "bf16", 2, 512, 512, 8, 512, 512, "causal", None, False, True),
+    # the bench shape's widths without bias: 16 head groups of fp32 partials
+    ("causal_r576_v512", "bf16", 1, 640, 700, 16, 576, 512, "causal", None, False, True),
+    # one head: a single group writes dcache directly (no partials)
+    ("one_head_kvlen_r576", "bf16", 2, 200, 300, 1, 576, 512, "kvlen", None, False, True),
     ("window_alibi_r576", "bf16", 2, 200, 200, 4, 576, 512, "window", "alibi", False, True),
     ("kvlen_empty_r576", "bf16", 3, 96, 333, 4, 576, 576, "kvlen_empty", None, False, True),
     ("ragged_r400", "bf16", 1, 130, 170, 4, 400, 400, None, "dense", False, True),
