@@ -612,17 +612,18 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
 }
 
 // ---------------------------------------------------------------------------
-// dC of the shared latent without bias or extended masks: the workgroup of
-// wide_bwd_dkdv_kernel (64 keys, one query-head group, Q / dO tiles of 32
-// rows through LDS) with the dC update split by columns instead of keys.
-// Wave w forms S, dP, P and dS for keys k0 + 16w .. +15 as there, and posts P
-// and dS (its two 16-bit B operands, 1 KiB each) to LDS.  After a barrier it
-// accumulates dC^T for the 16-column blocks i = w + 4j over all 64 keys: blocks
-// below DV/16 take Q^T dS and dO^T P into one accumulator, the rest Q^T dS.
-// A wave then reads the transposed Q / dO fragments of its own blocks only (a
+// dK and dV (or dC = dK + dV of the shared latent) without bias or extended
+// masks: the workgroup of wide_bwd_dkdv_kernel (64 keys, one query-head group,
+// Q / dO tiles of 32 rows through LDS) with the gradient update split by
+// columns instead of keys.  Wave w forms S, dP, P and dS for keys
+// k0 + 16w .. +15 as there, and posts P and dS (its two 16-bit B operands,
+// 1 KiB each) to LDS.  After a barrier it accumulates, for the 16-column
+// blocks i = w + 4j over all 64 keys, dK^T += Q^T dS and (blocks below DV/16)
+// dV^T += dO^T P; with the shared latent both go into one accumulator.  A
+// wave then reads the transposed Q / dO fragments of its own blocks only (a
 // quarter of the tile) where the key split reads all of them in every wave.
 // ---------------------------------------------------------------------------
-template <typename E, int D, int DV>
+template <typename E, int D, int DV, bool SHARED>
 __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using RQ = Row16<D>;
@@ -635,6 +636,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
   constexpr int KS = D / 32, VS = DV / 32, ND = D / 16, NV = DV / 16;
   constexpr int NJ = ND / 4, NJV = NV / 4;  // column blocks per wave, those with dV first
   static_assert(ND % 4 == 0 && NV % 4 == 0 && DV <= D, "column blocks split evenly over the 4 waves");
+  static_assert(SHARED || DV == D, "separate K / V of one width");
   __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
   __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
   __shared__ __attribute__((aligned(1024))) u32x4 xp[4 * 2 * 64];  // [wave][P, dS][lane]
@@ -645,10 +647,13 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
   const int nsplit = ba.nsplit;
   const int split = (int)blockIdx.x % nsplit;
   const int rest = (int)blockIdx.x / nsplit;
-  const int b = rest % a.B;  // one latent (Hkv = 1)
-  const int k0 = (rest / a.B) * kWK;
-  const int gs = a.Hq / nsplit;  // query heads of this group
-  const int h_first = split * gs;
+  const int BH = a.B * a.Hkv;
+  const int bh = rest % BH;
+  const int k0 = (rest / BH) * kWK;
+  const int b = bh / a.Hkv, hkv = bh % a.Hkv;
+  const int G = a.Hq / a.Hkv;
+  const int gs = G / nsplit;  // query heads of this group
+  const int h_first = hkv * G + split * gs;
   const int kw = __builtin_amdgcn_readfirstlane(k0 + 16 * w);
   const int key = kw + c;
   int kv_end = min(a.Lk, a.kv_valid);
@@ -658,16 +663,27 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
   const int n_qt = (k0 < kv_end && q_hi > q_begin) ? (q_hi - q_begin + kWT - 1) / kWT : 0;
   const int n_tiles = gs * n_qt;
 
-  // K^T as the B operand of S and dP: lane holds key `key`, dims 32*st + 8*qd + [0,8).
-  typename E::v8 kf[KS];
+  // K^T (and V^T) as the B operands of S and dP: lane holds key `key`, dims
+  // 32*st + 8*qd + [0,8).
+  typename E::v8 kf[KS], vf[SHARED ? 1 : VS];
   {
     const bool kin = key < a.Lk;
-    const uint16_t* krow = (const uint16_t*)a.k + (size_t)(b * a.Lk + (kin ? key : 0)) * D;
+    const size_t kr = (size_t)(b * a.Lk + (kin ? key : 0)) * a.Hkv + hkv;
+    const uint16_t* krow = (const uint16_t*)a.k + kr * D;
+    const uint16_t* vrow = (const uint16_t*)a.v + kr * DV;
 #pragma unroll
     for (int st = 0; st < KS; ++st) {
       u32x4 r = {0u, 0u, 0u, 0u};
       if (kin) r = *(const u32x4*)(krow + 32 * st + 8 * qd);
       kf[st] = E::as8(r);
+    }
+    if constexpr (!SHARED) {
+#pragma unroll
+      for (int st = 0; st < VS; ++st) {
+        u32x4 r = {0u, 0u, 0u, 0u};
+        if (kin) r = *(const u32x4*)(vrow + 32 * st + 8 * qd);
+        vf[st] = E::as8(r);
+      }
     }
   }
   const float cx = a.scale * kLog2e;
@@ -699,12 +715,18 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
     return E::as8(v);
   };
 
-  // acc[j][kb][r] = dC^T[16 (w + 4j) + 4qd + r][k0 + 16kb + c]
-  f32x4 acc[NJ][4];
+  // acc[j][kb][r] = dK^T (dC^T) [16 (w + 4j) + 4qd + r][k0 + 16kb + c]; accv likewise dV^T
+  f32x4 acc[NJ][4], accv[SHARED ? 1 : NJV][4];
 #pragma unroll
   for (int j = 0; j < NJ; ++j)
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) acc[j][kb] = f32x4{};
+  if constexpr (!SHARED) {
+#pragma unroll
+    for (int j = 0; j < NJV; ++j)
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) accv[j][kb] = f32x4{};
+  }
 
   // Query tiles last to first, the group's heads innermost (as in wide_bwd_dkdv_kernel).
   auto tile_head = [&](int t) { return h_first + t % gs; };
@@ -741,7 +763,8 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
 #pragma unroll
         for (int s = 0; s < KS; ++s) sx[rb] = E::mma16(oq.rows(qs, rb, s), kf[s], sx[rb]);
 #pragma unroll
-        for (int s = 0; s < VS; ++s) dpx[rb] = E::mma16(od.rows(dos, rb, s), kf[s], dpx[rb]);
+        for (int s = 0; s < VS; ++s)
+          dpx[rb] = E::mma16(od.rows(dos, rb, s), SHARED ? kf[s] : vf[s], dpx[rb]);
       }
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
@@ -769,7 +792,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
       pk[kb] = E::as8(xp[(2 * kb) * 64 + lane]);
       dk[kb] = E::as8(xp[(2 * kb + 1) * 64 + lane]);
     }
-    // dC^T[block w + 4j][keys] += Q^T dS (+ dO^T P below DV)
+    // block w + 4j: dK^T += Q^T dS, dV^T += dO^T P (below DV; into dK^T with the latent)
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const typename E::v8 fq = trans_at(qs, offq[j], RQ::ROWB);
@@ -778,7 +801,12 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
       if (j < NJV) {
         const typename E::v8 fd = trans_at(dos, offd[j < NJV ? j : 0], RD::ROWB);
 #pragma unroll
-        for (int kb = 0; kb < 4; ++kb) acc[j][kb] = E::mma16(fd, pk[kb], acc[j][kb]);
+        for (int kb = 0; kb < 4; ++kb) {
+          if constexpr (SHARED)
+            acc[j][kb] = E::mma16(fd, pk[kb], acc[j][kb]);
+          else
+            accv[j < NJV ? j : 0][kb] = E::mma16(fd, pk[kb], accv[j < NJV ? j : 0][kb]);
+        }
       }
     }
   };
@@ -799,12 +827,14 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
     compute(t + 1, smem1);
   }
 
-  const size_t nrows = (size_t)a.B * a.Lk;
+  // Outputs as wide_bwd_dkdv_kernel's: 16-bit rows with one group, else fp32
+  // partials [split][B*Lk*Hkv][D] (then, separate K / V, [split][..][DV]).
+  const size_t nrows = (size_t)a.B * a.Lk * a.Hkv;
 #pragma unroll
   for (int kb = 0; kb < 4; ++kb) {
     const int kk = k0 + 16 * kb + c;
     if (kk >= a.Lk) continue;
-    const size_t krow = (size_t)b * a.Lk + kk;
+    const size_t krow = (size_t)(b * a.Lk + kk) * a.Hkv + hkv;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
       const int col = 16 * (w + 4 * j) + 4 * qd;
@@ -813,6 +843,18 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
         *(u32x2*)((uint16_t*)ba.dk + krow * D + col) = pkd;
       } else {
         *(f32x4*)(ba.part + ((size_t)split * nrows + krow) * D + col) = acc[j][kb];
+      }
+    }
+    if constexpr (!SHARED) {
+#pragma unroll
+      for (int j = 0; j < NJV; ++j) {
+        const int col = 16 * (w + 4 * j) + 4 * qd;
+        if (nsplit == 1) {
+          const u32x2 pv = {E::pack2(accv[j][kb][0], accv[j][kb][1]), E::pack2(accv[j][kb][2], accv[j][kb][3])};
+          *(u32x2*)((uint16_t*)ba.dv + krow * DV + col) = pv;
+        } else {
+          *(f32x4*)(ba.part + (size_t)nsplit * nrows * D + ((size_t)split * nrows + krow) * DV + col) = accv[j][kb];
+        }
       }
     }
   }
@@ -882,10 +924,8 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
       if (hb) PJX_KV(true, 2); else PJX_KV(false, 2);
     } else if (hb) {
       PJX_KV(true, 0);
-    } else if constexpr (SHARED) {
-      hipLaunchKernelGGL((wide_bwd_dc_kernel<E, D, DV>), dim3((unsigned)kv_blocks), blk, 0, s, ba);
     } else {
-      PJX_KV(false, 0);
+      hipLaunchKernelGGL((wide_bwd_dc_kernel<E, D, DV, SHARED>), dim3((unsigned)kv_blocks), blk, 0, s, ba);
     }
 #undef PJX_KV
     rc = check_launch(who);
