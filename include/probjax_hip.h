@@ -15,6 +15,12 @@
  * row-major (D fastest), query head h uses KV head h / (Hq / Hkv)
  * (probjax/nn/pallas_kernels/kernels/attention.py:2164-2165,2189-2196).
  *
+ * Zero sizes: a tensor with no elements may be passed as a null pointer.  A
+ * batch or query length of 0 computes nothing; a key / cache length of 0
+ * gives every row output 0 and LSE +inf (the reference's rule for rows with
+ * no valid key, attention_xla.py), and in the backward dq = 0 (no keys) or
+ * dk = dv = 0 / dcache = 0 (no queries).
+ *
  * Return value: PJX_OK, or an error code with a message in pjx_last_error().
  */
 #ifndef PROBJAX_HIP_H_

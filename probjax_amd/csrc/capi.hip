@@ -24,6 +24,35 @@ int check_launch(const char* where) {
   return PJX_ERR_LAUNCH;
 }
 
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* p, uint32_t value, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = value;
+}
+
+__global__ __launch_bounds__(256) void zero_u16_kernel(uint16_t* p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0;
+}
+
+int fill_u32(void* p, uint32_t value, size_t n, hipStream_t stream, const char* who) {
+  if (n == 0) return PJX_OK;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (uint32_t*)p, value, n);
+  return check_launch(who);
+}
+
+int zero_u16(void* p, size_t n, hipStream_t stream, const char* who) {
+  if (n == 0) return PJX_OK;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
+  hipLaunchKernelGGL(zero_u16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)p, n);
+  return check_launch(who);
+}
+
+int write_keyless(void* o, float* lse, size_t o_elems, bool f32, size_t rows, hipStream_t stream,
+                  const char* who) {
+  int rc = f32 ? fill_u32(o, 0u, o_elems, stream, who) : zero_u16(o, o_elems, stream, who);
+  if (rc == PJX_OK && lse) rc = fill_u32(lse, kPosInfBits, rows, stream, who);
+  return rc;
+}
+
 int device_cu_count() {
   int dev = 0, n = 0;
   if (hipGetDevice(&dev) == hipSuccess &&

@@ -1016,7 +1016,8 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
     return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
   const bool f32 = dtype == PJX_DTYPE_F32;
-  if (!q || !k || !v || !o) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: null pointer");
+  // an empty cache (kv_len == 0) may come as null pointers
+  if (!q || !o || (batch * kv_len > 0 && (!k || !v))) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: null pointer");
   if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
     return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: bad sizes");
   if (head_dim != 128 && head_dim != 64) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: head_dim must be 64 or 128");
@@ -1030,6 +1031,9 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   if (kv_len > (1 << 30) || batch * kv_len * kv_heads * head_dim > ((int64_t)1 << 40))
     return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: sizes out of range");
   if (batch == 0) return PJX_OK;
+  if (kv_len == 0)
+    return write_keyless(o, lse, (size_t)(batch * q_len * q_heads * head_dim), f32, (size_t)(batch * q_heads * q_len),
+                         (hipStream_t)stream, "pjx_splitkv_decode");
   DecodeArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.lengths = kv_lengths; a.lse = lse;
@@ -1127,7 +1131,8 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   clear_error();
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16)
     return fail(PJX_ERR_INVALID, "pjx_mla_decode: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F16");
-  if (!q || !cache || !o) return fail(PJX_ERR_INVALID, "pjx_mla_decode: null pointer");
+  // an empty cache (kv_len == 0) may come as a null pointer
+  if (!q || !o || (batch * kv_len > 0 && !cache)) return fail(PJX_ERR_INVALID, "pjx_mla_decode: null pointer");
   if (batch < 0 || q_len <= 0 || heads <= 0 || kv_len < 0) return fail(PJX_ERR_INVALID, "pjx_mla_decode: bad sizes");
   if (q_len * heads > kRows) return fail(PJX_ERR_INVALID, "pjx_mla_decode: Lq*H must be <= 16");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_mla_decode: sm_scale must be > 0");
@@ -1144,6 +1149,9 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   a.dv = (int)v_dim; a.cx = sm_scale * kLog2e;
   hipStream_t s = (hipStream_t)stream;
   if (batch == 0) return PJX_OK;
+  if (kv_len == 0)
+    return write_keyless(o, lse, (size_t)(batch * q_len * heads * v_dim), false, (size_t)(batch * heads * q_len), s,
+                         "pjx_mla_decode");
   a.f16 = dtype == PJX_DTYPE_F16;
   return a.f16 ? run_mla_h16<F16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s)
                : run_mla_h16<Bf16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s);

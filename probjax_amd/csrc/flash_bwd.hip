@@ -1142,7 +1142,9 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   clear_error();
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
-  if (!q || !k || !v || !o || !dout || !lse || !dq || !dk || !dv)
+  // zero-element tensors may come as null pointers
+  const bool q_none = batch == 0 || q_len == 0, k_none = batch == 0 || kv_len == 0;
+  if ((!q_none && (!q || !o || !dout || !lse || !dq)) || (!k_none && (!k || !v || !dk || !dv)))
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q, k, v, o, dout, lse, dq, dk, dv must be non-null");
   if (batch < 0 || q_len < 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: negative or zero size");
@@ -1159,6 +1161,16 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
       (int64_t)q_heads * head_dim * 4 * 64 > 0xffffffffLL)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sizes out of range");
   if (batch == 0 || (q_len == 0 && kv_len == 0)) return PJX_OK;
+  const bool f32 = dtype == PJX_DTYPE_F32;
+  if (q_len == 0 || kv_len == 0) {
+    // no query reaches a key: dK = dV = 0 (no queries) or dQ = 0 (no keys)
+    hipStream_t s0 = (hipStream_t)stream;
+    const char* who = "pjx_flash_bwd";
+    auto zero = [&](void* p, size_t n) { return f32 ? fill_u32(p, 0u, n, s0, who) : zero_u16(p, n, s0, who); };
+    if (kv_len == 0) return zero(dq, (size_t)(batch * q_len * q_heads * head_dim));
+    const int rc = zero(dk, (size_t)(batch * kv_len * kv_heads * head_dim));
+    return rc != PJX_OK ? rc : zero(dv, (size_t)(batch * kv_len * kv_heads * head_dim));
+  }
   const size_t need = pjx_flash_bwd_workspace_size(batch, q_heads, q_len);
   if (need > 0 && (!workspace || workspace_bytes < need))
     return fail(PJX_ERR_WORKSPACE, "pjx_flash_bwd: workspace missing or smaller than pjx_flash_bwd_workspace_size()");

@@ -993,7 +993,9 @@ static int make_flash_args(FlashArgs& a, const char* who, const void* q, const v
                            int causal, float sm_scale, const pjx_score_mods* mods, bool* empty) {
   char buf[256];
   *empty = false;
-  if (!q || !k || !v || !o) {
+  // zero-element tensors may come as null pointers
+  const bool q_none = batch == 0 || q_len == 0, k_none = batch == 0 || kv_len == 0;
+  if ((!q_none && (!q || !o)) || (!k_none && (!k || !v))) {
     snprintf(buf, sizeof(buf), "%s: input and output pointers must be non-null", who);
     return fail(PJX_ERR_INVALID, buf);
   }
@@ -1062,6 +1064,9 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
                            q_valid, kv_valid, causal, sm_scale, mods, &empty);
   if (rc != PJX_OK || empty) return rc;
   hipStream_t s = (hipStream_t)stream;
+  if (kv_len == 0)
+    return write_keyless(o, lse, (size_t)(batch * q_len * q_heads * head_dim), dtype == PJX_DTYPE_F32,
+                         (size_t)(batch * q_heads * q_len), s, "pjx_flash_fwd");
   const bool hb = bias != nullptr;
   a.f16 = dtype == PJX_DTYPE_F16;
   if (head_dim == 256) return launch_flash_wide256(a, s);
@@ -1115,6 +1120,9 @@ extern "C" int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o,
                            bias_heads, batch, q_len, kv_len, heads, 1, rank, v_dim, q_valid,
                            kv_valid, causal, sm_scale, mods, &empty);
   if (rc != PJX_OK || empty) return rc;
+  if (kv_len == 0)
+    return write_keyless(o, lse, (size_t)(batch * q_len * heads * v_dim), false, (size_t)(batch * heads * q_len),
+                         (hipStream_t)stream, "pjx_mla_fwd");
   a.f16 = dtype == PJX_DTYPE_F16;
   return launch_mla_wide(a, (int)rank, (hipStream_t)stream);
 }

@@ -983,7 +983,9 @@ extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const vo
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: dtype must be PJX_DTYPE_BF16 or PJX_DTYPE_F16");
   if (!((rank == 576 && (v_dim == 512 || v_dim == 576)) || (rank == 512 && v_dim == 512)))
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: (rank, v_dim) must be (576, 512), (576, 576) or (512, 512)");
-  if (!q || !cache || !o || !dout || !lse || !dq || !dcache)
+  // zero-element tensors may come as null pointers
+  const bool q_none = batch == 0 || q_len == 0, k_none = batch == 0 || kv_len == 0;
+  if ((!q_none && (!q || !o || !dout || !lse || !dq)) || (!k_none && (!cache || !dcache)))
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: q, cache, o, dout, lse, dq, dcache must be non-null");
   if (batch < 0 || q_len < 0 || kv_len < 0 || heads <= 0)
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: negative or zero size");
@@ -994,6 +996,8 @@ extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const vo
       batch * kv_len * rank * 4 * heads > ((int64_t)1 << 46))
     return fail(PJX_ERR_INVALID, "pjx_mla_bwd: sizes out of range");
   if (batch == 0 || (q_len == 0 && kv_len == 0)) return PJX_OK;
+  if (kv_len == 0) return zero_u16(dq, (size_t)(batch * q_len * heads * rank), (hipStream_t)stream, who);
+  if (q_len == 0) return zero_u16(dcache, (size_t)(batch * kv_len * rank), (hipStream_t)stream, who);
   const int nsplit = wide_bwd_nsplit(batch, kv_len, heads, 1);
   const size_t need = wide_bwd_workspace(batch, heads, q_len, kv_len, 1, rank, 0, nsplit, true);
   if (!workspace || workspace_bytes < need)

@@ -27,4 +27,20 @@ int check_launch(const char* where);
 // thread-local error string); 256 if the query fails.
 int device_cu_count();
 
+// Fills n 32-bit words at p with `value` on `stream` (a kernel, so that a
+// caller may capture it in a graph); for the results of zero-length inputs
+// (output 0, LSE +inf).  p may be null when n == 0.  Returns a PJX_* status.
+int fill_u32(void* p, uint32_t value, size_t n, hipStream_t stream, const char* who);
+// Fills n 16-bit elements with zero (n may be odd).
+int zero_u16(void* p, size_t n, hipStream_t stream, const char* who);
+
+constexpr uint32_t kPosInfBits = 0x7f800000u;  // float +inf
+
+// Attention with no keys: every one of the o_elems output elements (fp32 if
+// f32, else 16-bit) is 0 and each of the `rows` LSE entries +inf (lse may be
+// null), the reference's l == 0 rule (attention_xla.py, output 0 and LSE
+// +inf for rows without a valid key).
+int write_keyless(void* o, float* lse, size_t o_elems, bool f32, size_t rows, hipStream_t stream,
+                  const char* who);
+
 }  // namespace pjx
