@@ -61,10 +61,11 @@ struct BwdTile {
   static constexpr int NLD = (ROWS / 4) / RPI;  // loads per wave per tensor per tile
   // Bijective over any 16 consecutive rows (16-byte column reads), and the
   // 4 rows of an aligned group differ in the chunk bits above the 4-chunk
-  // block of a transposing read (D=128: bits 3:2; D=64 with two rows per bank
-  // line: bit 2 between rows of equal parity).
+  // block of a transposing read (D=128, 256: bits 3:2 of the chunk within its
+  // bank line; D=64 with two rows per bank line: bit 2 between rows of equal
+  // parity).
   __device__ static int swz(int r) {
-    return D == 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
+    return D >= 128 ? (((r & 3) << 2) | ((r >> 2) & 3)) : ((((r >> 1) & 1) << 2) | ((r >> 2) & 3));
   }
 };
 
@@ -142,7 +143,7 @@ __device__ __forceinline__ void store_dbias(const FlashBwdArgs& ba, const BlockG
 // dQ (and delta): one workgroup per (128-query tile, batch, head).
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BIAS, int EXT>
-__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
+__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
   // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
   constexpr bool HB = BIAS != 0, DB = BIAS == 2;
   const FlashArgs& a = ba.f;
@@ -356,7 +357,7 @@ __global__ __launch_bounds__(kThreads, 2) void flash_bwd_dq_kernel(FlashBwdArgs 
 // dK, dV: one workgroup per (128-key tile, batch, KV head).
 // ---------------------------------------------------------------------------
 template <typename E, int D, bool BIAS, int EXT>
-__global__ __launch_bounds__(kThreads, 2) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
+__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
   constexpr int ROWB = T::ROWB, TILE_B = T::TILE_B;
@@ -1123,6 +1124,16 @@ static int run_bwd(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
   return a.f.ext == 1 ? run_bwd_t<D, 1>(a, dtype, hb, s) : run_bwd_t<D, 0>(a, dtype, hb, s);
 }
 
+// D = 256 (16-bit only): the same kernels at one wave per SIMD.
+template <int EXT>
+static int run_bwd256_t(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
+  return dtype == PJX_DTYPE_F16 ? run_bwd_h16<F16Fmt, 256, EXT>(a, hb, s) : run_bwd_h16<Bf16Fmt, 256, EXT>(a, hb, s);
+}
+static int run_bwd256(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
+  if (a.f.ext == 2) return run_bwd256_t<2>(a, dtype, hb, s);
+  return a.f.ext == 1 ? run_bwd256_t<1>(a, dtype, hb, s) : run_bwd256_t<0>(a, dtype, hb, s);
+}
+
 }  // namespace pjx
 
 using namespace pjx;
@@ -1201,6 +1212,11 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
   ba.dbias = dbias;
   hipStream_t s = (hipStream_t)stream;
+  // D = 256 without extended masks: these kernels at one wave per SIMD
+  // (32x32x16 MFMAs, 32 keys / rows per wave; 449 and 501 registers, no
+  // spills).  With extended masks their dK/dV instance would spill, so those
+  // take the 16-key / 16-row wide kernels.
+  if (head_dim == 256 && a.ext == 0) return run_bwd256(ba, dtype, bias != nullptr, s);
   if (head_dim == 256) {
     // the 16-row / 16-key wide kernels, one head group per KV head (no partials)
     WideBwdArgs wa;
