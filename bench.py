@@ -373,8 +373,8 @@ def make_c2w(dev, gen):
 
 def make_c2wb(dev, gen):
     """Backward of the head-dim-256 forward (the C2W shape): one pjx_flash_bwd
-    call (the 32-row / 32-key backward kernels at D = 256).  FLOPs by the
-    2.5x-forward convention, as for C2B."""
+    call (the 16-row dQ kernel and the 32-key dK/dV kernel at D = 256).  FLOPs
+    by the 2.5x-forward convention, as for C2B."""
     import torch
     from probjax_amd.hip_attention import flash_attention_bwd, flash_attention_fwd
 
@@ -388,7 +388,7 @@ def make_c2wb(dev, gen):
     fn = lambda: flash_attention_bwd(q, k, v, o, do, lse, sm_scale=sc, causal=True, workspace=ws)  # noqa: E731
     return dict(name="causal bwd bf16 B=2 H=16 L=4096 D=256 (dq, dk, dv)", fn=fn, flop=flop, bytes=nbytes,
                 bound="mfma", dtype="bf16",
-                kernel="flash_bwd_dq_kernel<Bf16Fmt,256,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,256,false,0>")
+                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,256,false,0>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,

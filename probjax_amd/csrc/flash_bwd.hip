@@ -1124,14 +1124,12 @@ static int run_bwd(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
   return a.f.ext == 1 ? run_bwd_t<D, 1>(a, dtype, hb, s) : run_bwd_t<D, 0>(a, dtype, hb, s);
 }
 
-// D = 256 (16-bit only): the same kernels at one wave per SIMD.
-template <int EXT>
-static int run_bwd256_t(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
-  return dtype == PJX_DTYPE_F16 ? run_bwd_h16<F16Fmt, 256, EXT>(a, hb, s) : run_bwd_h16<Bf16Fmt, 256, EXT>(a, hb, s);
-}
-static int run_bwd256(const FlashBwdArgs& a, int dtype, bool hb, hipStream_t s) {
-  if (a.f.ext == 2) return run_bwd256_t<2>(a, dtype, hb, s);
-  return a.f.ext == 1 ? run_bwd256_t<1>(a, dtype, hb, s) : run_bwd256_t<0>(a, dtype, hb, s);
+// dK/dV at D = 256 without extended masks (16-bit): the kernel above at one
+// wave per SIMD.
+template <typename E>
+static int run_dkdv256(const FlashBwdArgs& a, bool hb, hipStream_t s) {
+  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, 256, true, 0>, a, s)
+            : launch_dkdv(flash_bwd_dkdv_kernel<E, 256, false, 0>, a, s);
 }
 
 }  // namespace pjx
@@ -1212,13 +1210,11 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
   ba.dbias = dbias;
   hipStream_t s = (hipStream_t)stream;
-  // D = 256 without extended masks: these kernels at one wave per SIMD
-  // (32x32x16 MFMAs, 32 keys / rows per wave; 449 and 501 registers, no
-  // spills).  With extended masks their dK/dV instance would spill, so those
-  // take the 16-key / 16-row wide kernels.
-  if (head_dim == 256 && a.ext == 0) return run_bwd256(ba, dtype, bias != nullptr, s);
   if (head_dim == 256) {
-    // the 16-row / 16-key wide kernels, one head group per KV head (no partials)
+    // dQ (and delta, lse*log2e): the 16-row wide kernel.  dK/dV: without
+    // extended masks the 32-key kernel above at one wave per SIMD (32x32x16
+    // MFMAs; 501 registers, no spills), else the 16-key wide kernel, one head
+    // group per KV head (no partials).
     WideBwdArgs wa;
     wa.f = a;
     wa.f.dv = 256;
@@ -1229,7 +1225,11 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     wa.dbias = dbias;
     wa.part = nullptr;
     wa.nsplit = 1;
-    return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
+    if (a.ext != 0) return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
+    const int rc = run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd", true);
+    if (rc != PJX_OK) return rc;
+    const bool hb256 = bias != nullptr;
+    return dtype == PJX_DTYPE_F16 ? run_dkdv256<F16Fmt>(ba, hb256, s) : run_dkdv256<Bf16Fmt>(ba, hb256, s);
   }
   const bool hb = bias != nullptr;
   return head_dim == 128 ? run_bwd<128>(ba, dtype, hb, s) : run_bwd<64>(ba, dtype, hb, s);

@@ -177,8 +177,10 @@ struct WideBwdArgs {
 };
 
 // Runs the wide backward (dQ, then dK/dV or the latent's dC, then the partial
-// sum when nsplit > 1); returns a PJX_* status.
-int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who);
+// sum when nsplit > 1; with dq_only the dQ kernel alone, which also writes
+// delta and lse*log2e); returns a PJX_* status.
+int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who,
+                 bool dq_only = false);
 
 // Wide-head bf16 forward kernels (flash_wide.hip): D = 256 with separate K/V,
 // and the absorbed latent (K = V, rank 512 / 576, output width a.dv).

@@ -902,7 +902,7 @@ int wide_bwd_nsplit(int64_t B, int64_t Lk, int64_t Hq, int64_t Hkv) {
 }
 
 template <typename E, int D, int DV, bool SHARED>
-static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
+static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who, bool dq_only) {
   const FlashArgs& a = ba.f;
   const bool hb = a.bias != nullptr, db = ba.dbias != nullptr, ext = a.ext != 0;
   const long dq_blocks = (long)((a.Lq + kWQ - 1) / kWQ) * a.B * a.Hq;
@@ -917,7 +917,7 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
   }
 #undef PJX_DQ
   int rc = check_launch(who);
-  if (rc != PJX_OK) return rc;
+  if (rc != PJX_OK || dq_only) return rc;
   if (kv_blocks > 0) {
 #define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
     if (ext) {
@@ -946,17 +946,18 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who) {
 }
 
 template <typename E>
-static int run_wide_bwd_fmt(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
-  if (!shared && D == 256 && DV == 256) return run_wide_bwd_t<E, 256, 256, false>(ba, s, who);
-  if (shared && D == 576 && DV == 512) return run_wide_bwd_t<E, 576, 512, true>(ba, s, who);
-  if (shared && D == 576 && DV == 576) return run_wide_bwd_t<E, 576, 576, true>(ba, s, who);
-  if (shared && D == 512 && DV == 512) return run_wide_bwd_t<E, 512, 512, true>(ba, s, who);
+static int run_wide_bwd_fmt(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who,
+                            bool dq_only) {
+  if (!shared && D == 256 && DV == 256) return run_wide_bwd_t<E, 256, 256, false>(ba, s, who, dq_only);
+  if (shared && D == 576 && DV == 512) return run_wide_bwd_t<E, 576, 512, true>(ba, s, who, dq_only);
+  if (shared && D == 576 && DV == 576) return run_wide_bwd_t<E, 576, 576, true>(ba, s, who, dq_only);
+  if (shared && D == 512 && DV == 512) return run_wide_bwd_t<E, 512, 512, true>(ba, s, who, dq_only);
   return fail(PJX_ERR_INVALID, "wide backward: unsupported head widths");
 }
 
-int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who) {
-  return ba.f.f16 ? run_wide_bwd_fmt<F16Fmt>(ba, D, DV, shared, s, who)
-                  : run_wide_bwd_fmt<Bf16Fmt>(ba, D, DV, shared, s, who);
+int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who, bool dq_only) {
+  return ba.f.f16 ? run_wide_bwd_fmt<F16Fmt>(ba, D, DV, shared, s, who, dq_only)
+                  : run_wide_bwd_fmt<Bf16Fmt>(ba, D, DV, shared, s, who, dq_only);
 }
 
 }  // namespace pjx
