@@ -29,6 +29,12 @@
 //     dK^T += Q^T dS (dO^T and Q^T by transposing LDS reads).  The group's
 //     query heads accumulate in fp32 before the single rounding to 16 bits.
 //
+// D = 64 and 128 run both kernels at two waves per SIMD.  At D = 256 (16-bit,
+// no extended masks) dQ comes from the wide-head kernel of flash_wide_bwd.hip
+// and dK/dV from flash_bwd_dkdv_kernel at one wave per SIMD, the faster pair
+// on the causal 4096-token case; with extended masks both come from the
+// wide-head kernels.
+//
 // LDS tiles (both kernels) are row-major [row][dim] with 16-byte chunks
 // XOR-swizzled so that both reads of a tile are free of bank conflicts: the
 // 16-byte reads of one chunk column over 16 consecutive rows, and the

@@ -34,6 +34,12 @@
 //     groups over workgroups when one group per head-tile would leave the chip
 //     idle (MQA: 16 heads over one latent); each group writes an fp32 partial
 //     and wide_bwd_reduce_kernel sums them in a fixed order (deterministic).
+//   wide_bwd_dc_kernel -- the same workgroup and outputs as the dK/dV kernel
+//     for inputs without bias or extended masks, with the gradient update
+//     split over the waves by columns instead of keys (P and dS exchanged
+//     through LDS), so each wave reads a quarter of the transposed Q / dO
+//     fragments.  The C-ABI reaches it for the latent; flash_bwd.hip takes
+//     D = 256 dK/dV without extended masks from its own 32-key kernel.
 //
 // LDS rows are row-major [row][dim] with 16-byte chunks XOR-swizzled within
 // aligned groups of G chunks so that both read patterns of the 16x16 layout
