@@ -97,7 +97,15 @@ typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 // Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
 __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
+  // The descriptor lives in scalar registers, so base and bytes must be the
+  // same in every lane; reading them from the first lane states that to the
+  // compiler.  A value it cannot prove uniform (e.g. a clamp it computes as
+  // v_med3) would otherwise wrap every load in a per-lane waterfall loop.
+  const uint64_t p = (uint64_t)base;
+  const uint64_t pu = ((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)(p >> 32)) << 32) |
+                      (uint32_t)__builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)pu, (short)0, __builtin_amdgcn_readfirstlane((int)bytes),
+                                           0x00020000);
 }
 
 // Each lane loads 16 bytes at voffset; lane l's bytes land at lds_wave + 16*l
