@@ -40,9 +40,17 @@ HIPCC_FLAGS = [
 # wave per SIMD, and at that occupancy the compiler would put the MFMA
 # accumulators in AGPRs and copy every score out of them for the softmax;
 # forcing the VGPR form of the MFMAs keeps the scores where the softmax reads
-# them (the kernel fits in 256 VGPRs).
+# them (the kernel fits in 256 VGPRs).  flash_wide.hip: the same at one wave
+# per SIMD, and worse: with the output accumulators in AGPRs the compiler
+# copies all of them to VGPRs at the top of every key tile for the rarely
+# taken rescale (128-144 v_accvgpr_read per tile).  In the VGPR form the
+# accumulators stay in VGPRs and part of Q^T goes to AGPRs, which the MFMAs
+# read directly (latent prefill forward 5.6% faster, the dense-bias forwards
+# 4%).  flash_wide_bwd.hip keeps the default: the VGPR form made its latent
+# backward 44% slower.
 FILE_FLAGS = {
     "flash_bias_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "flash_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 
