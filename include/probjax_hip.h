@@ -140,7 +140,8 @@ int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* 
 
 /*
  * Bytes of workspace pjx_flash_bwd needs: two fp32 values per query row
- * (delta = sum_d o*do and the base-2 LSE), 8 * batch * q_heads * q_len.
+ * (sm_scale * delta, delta = sum_d o*do, and the base-2 LSE),
+ * 8 * batch * q_heads * q_len.
  */
 size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_len);
 
@@ -287,8 +288,8 @@ int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o, float* lse
                 int causal, float sm_scale, const pjx_score_mods* mods, void* stream);
 
 /*
- * Bytes of workspace pjx_mla_bwd needs for these sizes: delta and the base-2
- * LSE per query row, plus fp32 partial cache gradients of the query-head
+ * Bytes of workspace pjx_mla_bwd needs for these sizes: sm_scale * delta and
+ * the base-2 LSE per query row, plus fp32 partial cache gradients of the query-head
  * groups the key-side kernel splits the heads into (a function of the sizes
  * only).
  */

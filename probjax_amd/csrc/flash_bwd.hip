@@ -19,8 +19,9 @@
 //     dP^T = V dO^T with keys as MFMA rows, so each lane holds one query's
 //     column and its lse / delta are one register each; dQ^T += K^T dS^T with
 //     K^T read by transposing LDS reads.  It also computes delta for its rows
-//     (o and dO are read once, for dO^T) and writes delta and lse*log2e to
-//     the workspace for the second kernel.
+//     (o and dO are read once, for dO^T) and writes delta * sm_scale and
+//     lse*log2e to the workspace for the second kernel, which then forms
+//     dS = P (dP sm_scale - delta sm_scale) with one fma and one multiply.
 //   flash_bwd_dkdv_kernel -- one workgroup per (128-key tile, batch, KV head),
 //     each wave owns 32 keys whose K^T and V^T stay in registers; Q and dO
 //     tiles of 64 queries of every query head of the group stream through
@@ -195,12 +196,13 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
     }
   }
   const float delta = xor32_sum(dsum);
+  const float dsc = delta * a.scale;  // the workspace holds delta * sm_scale
   float lse2 = 0.f;
   const size_t lidx = ((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi;
   if (row_in) {
     lse2 = a.lse[lidx] * kLog2e;
     if (half == 0) {
-      ba.delta[lidx] = delta;
+      ba.delta[lidx] = dsc;
       ba.lse2[lidx] = lse2;
     }
   }
@@ -315,9 +317,13 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
-        const float t = p * (dp[kb][r] - delta);
-        if constexpr (DB) dbv[kb][r] = t;
-        s[kb][r] = t * a.scale;
+        if constexpr (DB) {
+          const float t = p * (dp[kb][r] - delta);
+          dbv[kb][r] = t;
+          s[kb][r] = t * a.scale;
+        } else {
+          s[kb][r] = p * fmaf(dp[kb][r], a.scale, -dsc);  // p (dp - delta) scale
+        }
       }
     }
     if constexpr (DB) store_dbias<BK / 32>(ba, g, dbv, k0, half, row_in);
@@ -369,7 +375,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
   constexpr int ROWB = T::ROWB, TILE_B = T::TILE_B;
   static_assert(T::ROWS == kBQs, "one Q / dO tile per stage");
   // Per stage: Q tile, dO tile, then each wave's own copy of the stage's
-  // lse*log2e and delta (64 floats each).
+  // lse*log2e and delta * sm_scale (64 floats each).
   constexpr int SMALL_B = 2 * kBQs * 4;
   constexpr int STAGE_B = 2 * TILE_B + 4 * SMALL_B;
   __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
@@ -513,7 +519,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
                              const int ql = 32 * qb + 8 * (r >> 2) + 4 * half + (r & 3);
                              const float p = fast_exp2(fmaf(x, cx, -lsm[ql]));
                              sx[r] = p;
-                             dpx[r] = p * (dpx[r] - dlm[ql]) * a.scale * gg;
+                             dpx[r] = p * fmaf(dpx[r], a.scale, -dlm[ql]) * gg;
                            });
 #pragma unroll
         for (int c = 0; c < 2; ++c) {
@@ -581,7 +587,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
       for (int gq = 0; gq < 4; ++gq) {
         const f32x4 d4 = *(const f32x4*)(dlm + 32 * qb + 8 * gq + 4 * half);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s[4 * gq + j] = s[4 * gq + j] * (dp[4 * gq + j] - d4[j]) * a.scale;
+        for (int j = 0; j < 4; ++j) s[4 * gq + j] = s[4 * gq + j] * fmaf(dp[4 * gq + j], a.scale, -d4[j]);
       }
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
@@ -682,12 +688,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
     }
   }
   const float delta = xor32_sum(dsum);
+  const float dsc = delta * a.scale;  // the workspace holds delta * sm_scale
   float lse2 = 0.f;
   const size_t lidx = ((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi;
   if (row_in) {
     lse2 = a.lse[lidx] * kLog2e;
     if (half == 0) {
-      ba.delta[lidx] = delta;
+      ba.delta[lidx] = dsc;
       ba.lse2[lidx] = lse2;
     }
   }
@@ -800,9 +807,13 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dq_f32_kernel(FlashBwdA
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
-        const float t = p * (dp[kb][r] - delta);
-        if constexpr (DB) dbv[kb][r] = t;
-        s[kb][r] = t * a.scale;
+        if constexpr (DB) {
+          const float t = p * (dp[kb][r] - delta);
+          dbv[kb][r] = t;
+          s[kb][r] = t * a.scale;
+        } else {
+          s[kb][r] = p * fmaf(dp[kb][r], a.scale, -dsc);  // p (dp - delta) scale
+        }
       }
     }
     if constexpr (DB) store_dbias<BK / 32>(ba, g, dbv, k0, half, row_in);
@@ -854,7 +865,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   static_assert(PER_T >= 1, "tile shape");
   __shared__ __attribute__((aligned(16))) float q_lds[2][BQ * KS];
   __shared__ __attribute__((aligned(16))) float d_lds[2][BQ * KS];
-  __shared__ __attribute__((aligned(16))) float ld_lds[2][2 * BQ];  // lse*log2e, delta
+  __shared__ __attribute__((aligned(16))) float ld_lds[2][2 * BQ];  // lse*log2e, delta * sm_scale
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -998,7 +1009,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
                            const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
                            const float p = fast_exp2(fmaf(x, cx, -lsm[qi]));
                            s[r] = p;
-                           ds[r] = p * (dp[r] - lsm[BQ + qi]) * a.scale * gg;
+                           ds[r] = p * fmaf(dp[r], a.scale, -lsm[BQ + qi]) * gg;
                          });
     } else {
     if constexpr (BIAS) {
@@ -1026,7 +1037,7 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
       const int qi = 8 * (r >> 2) + 4 * half + (r & 3);
       const float p = fast_exp2(fmaf(s[r], cx, -lsm[qi]));
       s[r] = p;
-      ds[r] = p * (dp[r] - lsm[BQ + qi]) * a.scale;
+      ds[r] = p * fmaf(dp[r], a.scale, -lsm[BQ + qi]);
     }
     }
     // dV^T[d][key] += dO^T P and dK^T[d][key] += Q^T dS: step r contracts
@@ -1087,7 +1098,7 @@ static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
   return check_launch("pjx_flash_bwd (dk, dv)");
 }
 
-// dQ first (it writes the delta and lse*log2e the dK/dV kernel reads), then
+// dQ first (it writes the delta * sm_scale and lse*log2e the dK/dV kernel reads), then
 // dK/dV.  Without keys only dQ (= 0) runs; without queries only dK/dV (= 0).
 template <int D, int EXT>
 static int run_bwd_f32(const FlashBwdArgs& a, bool hb, hipStream_t s) {

@@ -24,7 +24,7 @@
 //     latent one K-fragment read feeds both products.  dQ^T += K^T dS^T takes
 //     dS^T from registers as the B operand (k slot 8qd + j <-> key
 //     16(j/4) + 4qd + j%4) and K^T from transposing LDS reads in that key
-//     order.  It writes delta and lse*log2e for the second kernel.
+//     order.  It writes delta * sm_scale and lse*log2e for the second kernel.
 //   wide_bwd_dkdv_kernel -- one workgroup per (64-key tile, batch, KV head,
 //     head group); a wave owns keys kw + c with K^T (and V^T) in registers.
 //     Q and dO tiles of 32 rows stream through LDS.  S = Q K^T, dP = dO V^T
@@ -211,12 +211,13 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
     }
   }
   const float delta = xor32_sum(xor16_sum(dsum));
+  const float dsc = delta * a.scale;  // the workspace holds delta * sm_scale
   float lse2 = 0.f;
   const size_t lidx = ((size_t)b * a.Hq + h) * a.Lq + qi;
   if (row_in) {
     lse2 = a.lse[lidx] * kLog2e;
     if (qd == 0) {
-      ba.delta[lidx] = delta;
+      ba.delta[lidx] = dsc;
       ba.lse2[lidx] = lse2;
     }
   }
@@ -331,9 +332,13 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const float p = fast_exp2(fmaf(s[kb][r], cx, -lse2));
-          const float tt = p * (dp[kb][r] - delta);
-          if constexpr (DB) dbv[kb][r] = tt;
-          s[kb][r] = tt * a.scale;
+          if constexpr (DB) {
+            const float tt = p * (dp[kb][r] - delta);
+            dbv[kb][r] = tt;
+            s[kb][r] = tt * a.scale;
+          } else {
+            s[kb][r] = p * fmaf(dp[kb][r], a.scale, -dsc);  // p (dp - delta) scale
+          }
         }
     }
     if constexpr (DB) {
@@ -393,7 +398,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
   using OQ = Offs16<E, D>;
   using OD = Offs16<E, DV>;
   constexpr int QT_B = Row16<D>::TILE_B, DT_B = Row16<DV>::TILE_B;
-  // lse*log2e and delta of the tile's rows, one 64-float slot each (the
+  // lse*log2e and delta * sm_scale of the tile's rows, one 64-float slot each (the
   // 4-byte buffer->LDS load writes one float per lane; lanes 32..63 fill the
   // unused upper half)
   constexpr int SMALL_B = 2 * 64 * 4;
@@ -555,7 +560,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
         }
         const float p = keep ? fast_exp2(fmaf(x, cx, -l4[r])) : 0.f;
         sx[rb][r] = p;
-        dpx[rb][r] = p * (dpx[rb][r] - d4[r]) * a.scale * gg;
+        dpx[rb][r] = p * fmaf(dpx[rb][r], a.scale, -d4[r]) * gg;
       }
     }
     const typename E::v8 pb = pack_slots<E>(sx[0], sx[1]);
@@ -637,7 +642,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
   using OQ = Offs16<E, D>;
   using OD = Offs16<E, DV>;
   constexpr int QT_B = RQ::TILE_B, DT_B = RD::TILE_B;
-  constexpr int SMALL_B = 2 * 64 * 4;  // lse*log2e and delta of the tile's rows
+  constexpr int SMALL_B = 2 * 64 * 4;  // lse*log2e and delta * sm_scale of the tile's rows
   constexpr int STAGE_B = QT_B + DT_B + SMALL_B;
   constexpr int KS = D / 32, VS = DV / 32, ND = D / 16, NV = DV / 16;
   constexpr int NJ = ND / 4, NJV = NV / 4;  // column blocks per wave, those with dV first
@@ -783,7 +788,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
           const bool keep = key < kv_end && qr < q_hi && (!a.causal || qr >= key);
           const float p = keep ? fast_exp2(fmaf(sx[rb][r], cx, -l4[r])) : 0.f;
           sx[rb][r] = p;
-          dpx[rb][r] = p * (dpx[rb][r] - d4[r]) * a.scale;
+          dpx[rb][r] = p * fmaf(dpx[rb][r], a.scale, -d4[r]);
         }
       }
       pbv = __builtin_bit_cast(u32x4, pack_slots<E>(sx[0], sx[1]));
