@@ -16,56 +16,60 @@ namespace pjx {
 // bf16 path with a dense fp32 bias, streamed through LDS.  The bias is the
 // bulk of the bytes (4 B per score against 4*D bytes of K/V per key shared by
 // 128 queries), and per score the kernel adds it and runs the softmax: at
-// D = 64 the VALU work per score outweighs the MFMA work.  So 8 waves share
-// the 128 queries of a workgroup: waves w and w+4 share a SIMD, group 0
-// (waves 0-3) takes the even 32-key tiles and group 1 (waves 4-7) the odd
-// ones, each wave with its own online softmax for its 32 rows, and the two
-// waves of a SIMD interleave their MFMAs, exponentials and LDS reads (with 4
-// waves, one per SIMD at one workgroup per CU, nothing overlaps them).
+// D = 64 the VALU work per score outweighs the MFMA work.  So G groups of 4
+// waves share the 128 queries of a workgroup: waves w, w+4 (and w+8) share a
+// SIMD, group j takes the 32-key tiles t with t % G == j, each wave with its
+// own online softmax for its 32 rows, and the waves of a SIMD interleave
+// their MFMAs, exponentials and LDS reads (with 4 waves, one per SIMD at one
+// workgroup per CU, nothing overlaps them).  G = 2, or 3 at D = 64 for key
+// lengths up to 2048, where the third wave per SIMD hides more latency than
+// the shallower ring costs.
 //
-// Ring: a pair of tiles (one per group) is one step.  NP pair slots of 2
+// Ring: a set of G tiles (one per group) is one step.  NP set slots of G
 // stages each (K | V | bias block [128 queries][32 keys] per stage), all
-// copied by buffer->LDS loads, NP-1 pairs in flight while one is computed;
-// each group loads its own tile of a pair, a quarter per wave.  Bias rows
+// copied by buffer->LDS loads, NP-1 sets in flight while one is computed;
+// each group loads its own tile of a set, a quarter per wave.  Bias rows
 // (128 B) keep their 16-byte chunks XOR-swizzled by (row & 7).  Every path
 // issues the same loads in the same order (tiles past the last one read
 // nothing) and the loop has no early exit, so waits are partial vmcnt counts
-// the compiler can see through; one barrier per pair (after the wait for the
-// next pair, before its slot is reloaded), built from s_barrier and wavefront
-// fences so it does not wait for the pairs in flight.  At the end group 1
-// hands (max, sum, O) to group 0 through LDS; group 0 merges them and writes
-// the rows.  The products and the softmax are those of flash_fwd_bf16_kernel.
+// the compiler can see through; one barrier per set (after the wait for the
+// next set, before its slot is reloaded), built from s_barrier and wavefront
+// fences so it does not wait for the sets in flight.  At the end groups
+// 1 .. G-1 hand (max, sum, O) to group 0 through LDS; group 0 merges them and
+// writes the rows.  The products and the softmax are those of flash_fwd_bf16_kernel.
 // Requires Lk % 4 == 0 (16-byte bias chunks) and Lq*Lk*4 < 2^31 (32-bit
 // buffer offsets within one (batch, head) bias slice).
 // ---------------------------------------------------------------------------
-template <int D>
+template <int D, int G_>
 struct BiasRing {
   using T = Bf16Tile<D, 32>;
+  static constexpr int G = G_;                            // groups of 4 waves
   static constexpr int BIAS_ROWB = 32 * 4;                // 32 keys of fp32
   static constexpr int BIAS_B = kBQ * BIAS_ROWB;          // 16 KiB
   static constexpr int STAGE_B = 2 * T::TILE_B + BIAS_B;  // K | V | bias
-  static constexpr int PAIR_B = 2 * STAGE_B;
-  static constexpr int NP = (3 * PAIR_B <= 150 * 1024) ? 3 : 2;
+  static constexpr int SET_B = G * STAGE_B;  // one set: a stage per group
+  static constexpr int NP = (3 * SET_B <= 150 * 1024) ? 3 : 2;
   static constexpr int NLB = BIAS_B / (4 * 1024);         // bias loads per wave per tile
-  static constexpr int NL = 2 * T::NLD + NLB;             // loads per wave per pair
+  static constexpr int NL = 2 * T::NLD + NLB;             // loads per wave per set
   static_assert(NL * (NP - 1) < 64, "vmcnt range");
   static_assert(NP >= 2, "ring depth");
+  static_assert(NP * SET_B <= 150 * 1024, "LDS");
 };
 
-template <typename E, int D>
-__global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kernel(FlashArgs a) {
+template <typename E, int D, int G_>
+__global__ __launch_bounds__(G_ * kThreads, 1) void flash_fwd_bf16_bias_ring_kernel(FlashArgs a) {
   using T = Bf16Tile<D, 32>;
-  using R = BiasRing<D>;
-  constexpr int BK = 32, ROWB = T::ROWB, TILE_B = T::TILE_B, NP = R::NP, NL = R::NL;
+  using R = BiasRing<D, G_>;
+  constexpr int BK = 32, ROWB = T::ROWB, TILE_B = T::TILE_B, NP = R::NP, NL = R::NL, G = R::G;
   constexpr int BROWB = R::BIAS_ROWB, STAGE_B = R::STAGE_B;
   static_assert(T::BK == BK, "32-key tiles");
-  __shared__ __attribute__((aligned(1024))) unsigned char ps0[R::PAIR_B];
-  __shared__ __attribute__((aligned(1024))) unsigned char ps1[R::PAIR_B];
-  __shared__ __attribute__((aligned(1024))) unsigned char ps2[NP > 2 ? R::PAIR_B : 1024];
+  __shared__ __attribute__((aligned(1024))) unsigned char ps0[R::SET_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char ps1[R::SET_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char ps2[NP > 2 ? R::SET_B : 1024];
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int grp = w8 >> 2, w = w8 & 3;  // tile parity group, wave within the group
+  const int grp = w8 >> 2, w = w8 & 3;  // tile group (tiles t with t % G == grp), wave within it
   BlockGeom g = block_geom(a);
   g.qw = __builtin_amdgcn_readfirstlane(g.q0 + 32 * w);
   g.qi = g.qw + (tid & 31);
@@ -127,13 +131,13 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   float m_run = kMaxInit, l_run = 0.f;
 
   const int n_tiles = (g.kv_stop + BK - 1) / BK;
-  const int n_pairs = (n_tiles + 1) / 2;
+  const int n_sets = (n_tiles + G - 1) / G;
   const int q_last_w = g.qw + 31;
   const float cx = kLog2e;
 
-  // This group's tile of pair p into its stage of the pair slot.
+  // This group's tile of set p into its stage of the set's slot.
   auto issue = [&](int p, unsigned char* slot) {
-    const int k0 = (2 * p + grp) * BK;
+    const int k0 = (G * p + grp) * BK;
     unsigned char* ks = slot + grp * STAGE_B;
     const int nvalid = max(0, min(BK, g.kv_stop - k0));
     const uint32_t kvbytes =
@@ -154,7 +158,7 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   };
 
   auto compute = [&](int p, const unsigned char* slot) {
-    const int k0 = (2 * p + grp) * BK;
+    const int k0 = (G * p + grp) * BK;
     if (k0 >= g.kv_stop) return;            // past the last tile
     if (a.causal && k0 > q_last_w) return;  // tile above this wave's diagonal
     const unsigned char* ks = slot + grp * STAGE_B;
@@ -228,16 +232,16 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
     }
   };
 
-  // Pair p lives in slot p % NP.  Before computing pair p its loads have
-  // landed for every wave; after, wait for pair p+1, one barrier, then pair
+  // Set p lives in slot p % NP.  Before computing set p its loads have
+  // landed for every wave; after, wait for set p+1, one barrier, then set
   // p+NP is loaded into slot p % NP.
   issue(0, ps0);
-  wait_vmcnt<NL>();  // q's loads (issued before pair 0's) have landed
+  wait_vmcnt<NL>();  // q's loads (issued before set 0's) have landed
   issue(1, ps1);
   if constexpr (NP > 2) issue(2, ps2);
   wait_vmcnt<(NP - 1) * NL>();
   stage_barrier();
-  for (int p = 0; p < n_pairs; p += NP) {
+  for (int p = 0; p < n_sets; p += NP) {
     compute(p, ps0);
     wait_vmcnt<(NP - 2) * NL>();
     stage_barrier();
@@ -256,13 +260,15 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   wait_vmcnt<0>();
   stage_barrier();  // every wave is done with the ring
 
-  // Group 1 hands its (max, sum, O) to group 0 through LDS, lane by lane in
-  // the same register layout: O as 16-byte quads [D/32 * 4][4 waves][64 lanes]
-  // in pair slot 0 (consecutive lanes, consecutive banks), (max, sum) in slot 1.
-  static_assert((D / 32) * 4 * 256 * 16 <= R::PAIR_B && 256 * 8 <= R::PAIR_B, "hand-off fits");
-  f32x4* xo = (f32x4*)ps0 + w * 64 + lane;
-  float* xml = (float*)ps1 + 2 * (w * 64 + lane);
-  if (grp == 1) {
+  // Groups 1 .. G-1 hand their (max, sum, O) to group 0 through LDS, lane by
+  // lane in the same register layout: O as 16-byte quads [group-1][D/32 * 4]
+  // [4 waves][64 lanes] in set slot 0 (consecutive lanes, consecutive banks),
+  // (max, sum) in slot 1.
+  constexpr int QUADS = (D / 32) * 4;
+  static_assert((G - 1) * QUADS * 256 * 16 <= R::SET_B && (G - 1) * 256 * 8 <= R::SET_B, "hand-off fits");
+  if (grp > 0) {
+    f32x4* xo = (f32x4*)ps0 + ((grp - 1) * QUADS) * 256 + w * 64 + lane;
+    float* xml = (float*)ps1 + 2 * ((grp - 1) * 256 + w * 64 + lane);
 #pragma unroll
     for (int i = 0; i < D / 32; ++i)
 #pragma unroll
@@ -272,19 +278,39 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
     xml[1] = l_run;
   }
   stage_barrier();
-  if (grp == 1) return;
-  const float m1 = xml[0], l1 = xml[1];
-  const float M = fmaxf(m_run, m1);
-  const float f0 = fast_exp2(m_run - M), f1 = fast_exp2(m1 - M);
+  if (grp > 0) return;
+  float mg[G], lg[G], fg[G];
+  mg[0] = m_run;
+  lg[0] = l_run;
+  float M = m_run;
+#pragma unroll
+  for (int gi = 1; gi < G; ++gi) {
+    const float* xml = (const float*)ps1 + 2 * ((gi - 1) * 256 + w * 64 + lane);
+    mg[gi] = xml[0];
+    lg[gi] = xml[1];
+    M = fmaxf(M, mg[gi]);
+  }
+  float lsum = 0.f;
+#pragma unroll
+  for (int gi = 0; gi < G; ++gi) {
+    fg[gi] = fast_exp2(mg[gi] - M);
+    lsum = fmaf(lg[gi], fg[gi], lsum);
+  }
 #pragma unroll
   for (int i = 0; i < D / 32; ++i)
 #pragma unroll
     for (int r = 0; r < 16; r += 4) {
-      const f32x4 o1 = xo[(4 * i + r / 4) * 256];
+      f32x4 o = {acc[i][r] * fg[0], acc[i][r + 1] * fg[0], acc[i][r + 2] * fg[0], acc[i][r + 3] * fg[0]};
 #pragma unroll
-      for (int j = 0; j < 4; ++j) acc[i][r + j] = fmaf(acc[i][r + j], f0, o1[j] * f1);
+      for (int gi = 1; gi < G; ++gi) {
+        const f32x4 o1 = ((const f32x4*)ps0)[((gi - 1) * QUADS + 4 * i + r / 4) * 256 + w * 64 + lane];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] = fmaf(o1[j], fg[gi], o[j]);
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) acc[i][r + j] = o[j];
     }
-  const float l_tot = xor32_sum(fmaf(l_run, f0, l1 * f1));
+  const float l_tot = xor32_sum(lsum);
   const float inv = l_tot > 0.f ? 1.f / l_tot : 0.f;
   if (row_in) {
     uint16_t* orow = (uint16_t*)a.o + ((size_t)(g.b * a.Lq + g.qi) * a.Hq + g.h) * D;
@@ -302,13 +328,20 @@ __global__ __launch_bounds__(2 * kThreads, 1) void flash_fwd_bf16_bias_ring_kern
   }
 }
 
+constexpr int kBiasRing3MaxKeys = 2048;
+
 template <typename E>
 static void launch_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   if (head_dim == 128)
-    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 128>), dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
+    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 128, 2>), dim3((unsigned)blocks), dim3(2 * kThreads), 0,
+                       stream, a);
+  else if (a.Lk <= kBiasRing3MaxKeys)
+    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64, 3>), dim3((unsigned)blocks), dim3(3 * kThreads), 0,
+                       stream, a);
   else
-    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64>), dim3((unsigned)blocks), dim3(2 * kThreads), 0, stream, a);
+    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64, 2>), dim3((unsigned)blocks), dim3(2 * kThreads), 0,
+                       stream, a);
 }
 
 int launch_flash_bias_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {

@@ -10,6 +10,13 @@ Tolerances: bf16 output max-abs <= 2e-2 against the fp32 oracle from the same
 bf16-rounded inputs, gradients within probjax's gradient tolerance (atol
 2e-2 scaled by max(1, max|ref| / 4), rtol 1e-2); fp32 output <= 1e-5 and
 gradients <= 1e-5 * max(1, max|ref|) against the float64 oracle.
+
+The bf16 relative-position gradients are referenced to the oracle backward of
+the kernel's own bf16 forward output (the output the kernel backward receives, as
+in autograd): the learned table's far bucket sums dL/d(bias) = P (dP - delta)
+over most of the causal triangle, and one-ulp differences between two
+correctly rounded bf16 outputs move delta, and that sum, by more than the
+tolerance.  The output itself is checked against the oracle's.
 """
 
 import math
@@ -128,7 +135,8 @@ def test_relative_position_tables(device, kind, dtype):
     cdt = np.float32 if bf16 else np.float64
     o, lse = oracle.xla_attention(q, k, v, mask=omask, bias=obias, sm_scale=scale, strategy="dense",
                                   dtype=dtype, compute_dtype=cdt, return_lse=True)
-    *want, dbias = attention_backward(q, k, v, o, do, lse, mask=omask, bias=obias, sm_scale=scale,
+    o_bwd = to_np(out).astype(np.float32) if bf16 else o
+    *want, dbias = attention_backward(q, k, v, o_bwd, do, lse, mask=omask, bias=obias, sm_scale=scale,
                                       dtype=dtype, compute_dtype=cdt, return_dbias=True)
     dtable = np.zeros(table.shape, np.float64)
     per_head = dbias.sum(axis=0)  # [H, L, L]

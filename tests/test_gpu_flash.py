@@ -101,10 +101,12 @@ def test_flash_bias_kvlen(device, dtype_name):
     [
         (1, 300, 520, 4, 2, 64, False, (1, 1), None),           # partial tiles, rows past Lq, GQA, broadcast bias
         (2, 200, 200, 2, 2, 128, True, (2, 2), [150, 200]),     # D=128 ring, causal + lengths, full bias
-        (1, 1024, 1024, 2, 2, 64, False, (1, 2), [1000]),       # 16 tiles: the 3-stage ring wraps, ragged end
-        (1, 512, 192, 2, 2, 64, True, (1, 2), None),            # exactly 3 tiles
+        (1, 1024, 1024, 2, 2, 64, False, (1, 2), [1000]),       # 16 tiles in sets of 3: the ring wraps, ragged end
+        (1, 512, 192, 2, 2, 64, True, (1, 2), None),            # exactly 6 tiles
         (2, 130, 262, 2, 2, 64, True, (1, 2), [262, 5]),        # Lk % 4 != 0: bias through registers
         (1, 64, 4096, 2, 1, 128, False, (1, 2), [4000]),        # long rows, one query tile
+        (1, 96, 2048, 2, 2, 64, False, (1, 1), [1999]),         # three groups at the largest key length
+        (1, 96, 2052, 2, 2, 64, False, (1, 2), [2050]),         # two groups at D = 64 past it, 3-set ring
     ],
 )
 def test_flash_bf16_bias_matches_oracle(device, b, lq, lk, hq, hkv, d, causal, bias_bh, lengths):
