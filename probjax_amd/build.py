@@ -46,11 +46,14 @@ HIPCC_FLAGS = [
 # taken rescale (128-144 v_accvgpr_read per tile).  In the VGPR form the
 # accumulators stay in VGPRs and part of Q^T goes to AGPRs, which the MFMAs
 # read directly (latent prefill forward 5.6% faster, the dense-bias forwards
-# 4%).  flash_wide_bwd.hip keeps the default: the VGPR form made its latent
-# backward 44% slower.
+# 4%).  decode.hip: the same copies around the accumulators of the 64-row GQA
+# decode and of the fp32 decodes (GQA-8 with 8 query rows 5.7% faster, fp32
+# decode 3%; the bf16 C3 / latent decode unchanged).  flash_wide_bwd.hip keeps
+# the default: the VGPR form made its latent backward 44% slower.
 FILE_FLAGS = {
     "flash_bias_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "flash_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 
