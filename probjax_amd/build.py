@@ -48,12 +48,16 @@ HIPCC_FLAGS = [
 # read directly (latent prefill forward 5.6% faster, the dense-bias forwards
 # 4%).  decode.hip: the same copies around the accumulators of the 64-row GQA
 # decode and of the fp32 decodes (GQA-8 with 8 query rows 5.7% faster, fp32
-# decode 3%; the bf16 C3 / latent decode unchanged).  flash_wide_bwd.hip keeps
-# the default: the VGPR form made its latent backward 44% slower.
+# decode 3%; the bf16 C3 / latent decode unchanged).  flash_fwd.hip: the fp32
+# forward kernels likewise (7-8.5% faster); its 16-bit kernels use no AGPRs
+# and compile to the same code either way.  flash_wide_bwd.hip keeps the
+# default: the VGPR form made its latent backward 44% slower.  (flash_bwd.hip
+# cannot take it: the compiler fails on its D = 256 dK/dV kernel.)
 FILE_FLAGS = {
     "flash_bias_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "flash_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "flash_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 
