@@ -50,14 +50,17 @@ HIPCC_FLAGS = [
 # decode and of the fp32 decodes (GQA-8 with 8 query rows 5.7% faster, fp32
 # decode 3%; the bf16 C3 / latent decode unchanged).  flash_fwd.hip: the fp32
 # forward kernels likewise (7-8.5% faster); its 16-bit kernels use no AGPRs
-# and compile to the same code either way.  flash_wide_bwd.hip keeps the
-# default: the VGPR form made its latent backward 44% slower.  (flash_bwd.hip
-# cannot take it: the compiler fails on its D = 256 dK/dV kernel.)
+# and compile to the same code either way.  flash_bwd.hip: the fp32 backward
+# kernels (5-6% faster) and the 16-bit ones (1%); its D = 256 dK/dV kernel,
+# which the compiler fails on in that form, is built from flash_bwd256.hip in
+# the default form.  flash_wide_bwd.hip keeps the default: the VGPR form made
+# its latent backward 44% slower.
 FILE_FLAGS = {
     "flash_bias_ring.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "flash_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "decode.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "flash_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "flash_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 

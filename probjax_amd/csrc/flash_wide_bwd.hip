@@ -5,7 +5,7 @@
 // probjax differentiates absorbed `mla` through the materialised computation
 // (kernels/latent_attention.py:752-766): `mha` over K = V = the latent
 // broadcast to every head, so the cache gradient is the sum over heads of
-// dK + dV.  The math is the flash backward's (flash_bwd.hip; probjax
+// dK + dV.  The math is the flash backward's (flash_bwd_kernels.h; probjax
 // attention.py:853-1160): delta = sum_d o*do, p = exp2(s*log2e - lse*log2e),
 // ds = p (do.v^T - delta) sm_scale, dq = sum_k r(ds) k,
 // dk = sum_q r(ds)^T q, dv = sum_q r(p)^T do, fp32 accumulation (r() rounds
@@ -38,7 +38,7 @@
 //     for inputs without bias or extended masks, with the gradient update
 //     split over the waves by columns instead of keys (P and dS exchanged
 //     through LDS), so each wave reads a quarter of the transposed Q / dO
-//     fragments.  The C-ABI reaches it for the latent; flash_bwd.hip takes
+//     fragments.  The C-ABI reaches it for the latent; pjx_flash_bwd takes
 //     D = 256 dK/dV without extended masks from its own 32-key kernel.
 //
 // LDS rows are row-major [row][dim] with 16-byte chunks XOR-swizzled within
