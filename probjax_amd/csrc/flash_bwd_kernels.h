@@ -276,6 +276,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
         dp[kb] = E::mma32(vf, dof[st], dp[kb]);
       }
     }
+    PJX_SCHED_LDS_READS_AHEAD(2 * (D / 16) * (BK / 32), 3, 1);  // K / V fragments 3 MFMAs ahead
     f32x16 dbv[DB ? BK / 32 : 1];  // dL/d(bias) = P (dP - delta), kept for the store
     if constexpr (EXT == 2) {
       // modified scores, masks, P and dS = P (dP - delta) * scale * f'(s)

@@ -198,21 +198,10 @@ __global__ __launch_bounds__(kThreads, (wide_fwd_occupancy<D, BIAS, EXT>())) voi
         s[kb] = E::mma32(kf, qf[st], s[kb]);
       }
     }
-    // Issue order of the block: the first 3 K-fragment reads, then each MFMA
-    // followed by the next read, so 3 reads are in flight under the MFMAs.
-    // Left to itself the scheduler (at these register counts) waits for each
-    // read right before its MFMA: measured 17% slower on the latent prefill,
-    // 2.6% on D = 256.
-    {
-      constexpr int NS = KS * (BK / 32), PF = 3;
-      __builtin_amdgcn_sched_group_barrier(0x100, PF, 0);  // DS read
-#pragma unroll
-      for (int i = 0; i < NS - PF; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-      __builtin_amdgcn_sched_group_barrier(0x008, PF, 0);
-    }
+    // K-fragment reads 3 MFMAs ahead (left to itself the scheduler, at these
+    // register counts, waits for each read right before its MFMA: measured
+    // 17% slower on the latent prefill, 2.6% on D = 256).
+    PJX_SCHED_LDS_READS_AHEAD(KS * (BK / 32), 3, 1);
 
     // Register r of block kb holds key k0 + kb*32 + 8*(r/4) + 4*half + r%4.
     if constexpr (EXT == 2) {

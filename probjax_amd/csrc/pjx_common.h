@@ -134,6 +134,25 @@ __device__ __forceinline__ u32x2 lds_read_tr16(const void* p) {
 
 __device__ __forceinline__ bool wave_any(bool pred) { return __builtin_amdgcn_ballot_w64(pred) != 0; }
 
+// Issue order for a basic block whose N MFMAs each take an operand read from
+// LDS just before it (R reads per MFMA): the first PF MFMAs' reads, then each
+// MFMA followed by the reads of the one PF places later, so PF MFMAs' reads
+// are in flight under the MFMAs.  At high register counts the scheduler
+// otherwise issues each read right before its MFMA and waits for it.  Expand
+// after the loop that forms the MFMAs, in the same basic block.  (A macro:
+// written as an inline function, the same sequence was not applied to the
+// latent forward kernel's block.)
+#define PJX_SCHED_LDS_READS_AHEAD(N, PF, R)                                \
+  do {                                                                     \
+    static_assert((N) > (PF) && (PF) > 0, "prefetch depth");               \
+    __builtin_amdgcn_sched_group_barrier(0x100, (R) * (PF), 0); /* DS */   \
+    _Pragma("unroll") for (int i_ = 0; i_ < (N) - (PF); ++i_) {            \
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0); /* MFMA */       \
+      __builtin_amdgcn_sched_group_barrier(0x100, (R), 0);                 \
+    }                                                                      \
+    __builtin_amdgcn_sched_group_barrier(0x008, (PF), 0);                  \
+  } while (0)
+
 template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
   static_assert(N >= 0 && N < 64, "vmcnt range");
