@@ -197,7 +197,7 @@ def make_c4(dev, gen):
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / 8, kv_lengths=L_, bias=bias)  # noqa: E731
     return dict(name="C4 bias+kvlen fwd bf16 B=2 H=8 L=2048 D=64, bias f32 [8,2048,2048]",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="flash_fwd_bf16_bias_ring_kernel<Bf16Fmt,64>")
+                kernel="flash_fwd_bf16_bias_ring_kernel<Bf16Fmt,64,3>")
 
 
 def make_c5(dev, gen):
