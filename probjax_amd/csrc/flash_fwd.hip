@@ -313,19 +313,28 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 // it reads whatever the slot holds and is discarded, so the block stays
 // branch-free.
 // ---------------------------------------------------------------------------
-template <typename E, int D, int BKT, int WPC>
-__global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(FlashArgs a) {
+template <typename E, int D, int BKT, int WPC, int G = 1>
+__global__ __launch_bounds__(G * kThreads, WPC) void flash_fwd_bf16_pipe_kernel(FlashArgs a) {
   using T = Bf16Tile<D, BKT>;
   constexpr int RPW = BKT / 4;  // tile rows each wave loads
   static_assert(BKT % 32 == 0 && RPW % T::RPI == 0 && T::NLD >= 1, "tile rows per wave");
+  static_assert(G == 1 || G == 2, "one or two groups");
   constexpr int BK = T::BK, ROWB = T::ROWB, TILE_B = T::TILE_B, STAGE_B = T::STAGE_B;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
-  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[G * STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[G * STAGE_B];
 
   BlockGeom g = block_geom(a);
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = G > 1 ? w8 >> 2 : 0;     // group: the key tiles t with t % G == gi
+  const int w = G > 1 ? (w8 & 3) : w8;    // wave within the group: rows 32w .. of the q tile
+  if constexpr (G > 1) {
+    g.qw = g.q0 + 32 * w;
+    g.qi = g.qw + (tid & 31);
+  }
   g.qw = __builtin_amdgcn_readfirstlane(g.qw);
+  unsigned char* const st0 = smem0 + gi * STAGE_B;  // this group's stages
+  unsigned char* const st1 = smem1 + gi * STAGE_B;
   const int col = lane & 31, half = lane >> 5;
   const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
   const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
@@ -377,6 +386,11 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
   const int q_last_w = g.qw + 31;
   // tiles this wave uses: a causal wave stops at the tile holding its last row
   const int n_w = a.causal ? min(n_tiles, q_last_w / BK + 1) : n_tiles;
+  // this group's tiles G*s + gi: n_loc of them, the first n_wl used by this
+  // wave; n_steps (the same for every group) keeps the barriers in step
+  const int n_loc = (n_tiles - gi + G - 1) / G;
+  const int n_wl = n_w > gi ? (n_w - gi + G - 1) / G : 0;
+  const int n_steps = (n_tiles + G - 1) / G;
 
   auto issue = [&](const unsigned char* base, int t, unsigned char* dst, const uint32_t* voff) {
     const int k0 = t * BK;
@@ -491,26 +505,64 @@ __global__ __launch_bounds__(kThreads, WPC) void flash_fwd_bf16_pipe_kernel(Flas
 
   f32x16 sa[BK / 32], sb[BK / 32];
   if (n_tiles > 0) {
-    issue(Kb, 0, smem0, voffK);
-    issue(Vb, 0, smem0 + TILE_B, voffV);
-    if (n_tiles > 1) issue(Kb, 1, smem1, voffK);
+    if (n_loc > 0) {
+      issue(Kb, gi, st0, voffK);
+      issue(Vb, gi, st0 + TILE_B, voffV);
+      if (n_loc > 1) issue(Kb, G + gi, st1, voffK);
+    }
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    qk(smem0, sa);
+    if (n_loc > 0) qk(st0, sa);
   }
-  // Tile t: K in stage t%2 until iteration t-1, V in stage t%2 from iteration t.
-  for (int t = 0; t < n_tiles; t += 2) {
+  // Local tile s (global tile G*s + gi): K in stage s%2 until iteration s-1,
+  // V in stage s%2 from iteration s.
+  for (int s = 0; s < n_steps; s += 2) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 2 < n_tiles) issue(Kb, t + 2, smem0, voffK);
-    if (t + 1 < n_tiles) issue(Vb, t + 1, smem1 + TILE_B, voffV);
-    if (t < n_w) step(t, sa, smem0 + TILE_B, smem1, sb);
-    if (t + 1 >= n_tiles) break;
+    if (s + 2 < n_loc) issue(Kb, G * (s + 2) + gi, st0, voffK);
+    if (s + 1 < n_loc) issue(Vb, G * (s + 1) + gi, st1 + TILE_B, voffV);
+    if (s < n_wl) step(G * s + gi, sa, st0 + TILE_B, st1, sb);
+    if (s + 1 >= n_steps) break;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 3 < n_tiles) issue(Kb, t + 3, smem1, voffK);
-    if (t + 2 < n_tiles) issue(Vb, t + 2, smem0 + TILE_B, voffV);
-    if (t + 1 < n_w) step(t + 1, sb, smem1 + TILE_B, smem0, sa);
+    if (s + 3 < n_loc) issue(Kb, G * (s + 3) + gi, st1, voffK);
+    if (s + 2 < n_loc) issue(Vb, G * (s + 2) + gi, st0 + TILE_B, voffV);
+    if (s + 1 < n_wl) step(G * (s + 1) + gi, sb, st1 + TILE_B, st0, sa);
+  }
+  if constexpr (G > 1) {
+    // Group 1 hands (max, sum, O) to group 0 through LDS, lane by lane in the
+    // same register layout: O as 16-byte quads [D/32 * 4][4 waves][64 lanes]
+    // over stage 0 (consecutive lanes, consecutive banks), (max, sum) in
+    // stage 1; group 0 merges them.
+    static_assert((D / 32) * 4 * 256 * 16 <= G * STAGE_B && 256 * 8 <= G * STAGE_B, "hand-off fits");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // every wave is done with the ring
+    f32x4* xo = (f32x4*)smem0 + w * 64 + lane;
+    float* xml = (float*)smem1 + 2 * (w * 64 + lane);
+    if (gi == 1) {
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 4)
+          xo[(4 * i + r / 4) * 256] = f32x4{acc[i][r], acc[i][r + 1], acc[i][r + 2], acc[i][r + 3]};
+      xml[0] = m_run;
+      xml[1] = l_run;
+    }
+    __syncthreads();
+    if (gi == 1) return;
+    const float m1 = xml[0], l1 = xml[1];
+    const float M = fmaxf(m_run, m1);
+    const float f0 = fast_exp2(m_run - M), f1 = fast_exp2(m1 - M);
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const f32x4 o1 = xo[(4 * i + r / 4) * 256];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][r + j] = fmaf(acc[i][r + j], f0, o1[j] * f1);
+      }
+    l_run = fmaf(l_run, f0, l1 * f1);
+    m_run = M;
   }
 
   const float l_tot = xor32_sum(l_run);
@@ -923,9 +975,9 @@ __global__ __launch_bounds__(64 * split_waves<D>(), 1) void flash_fwd_f32_split_
 }
 
 template <typename K>
-static int launch(K kernel, const FlashArgs& a, hipStream_t stream) {
+static int launch(K kernel, const FlashArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_fwd");
 }
 
@@ -939,6 +991,8 @@ template <typename E>
 static int launch_pipe128(const FlashArgs& a, hipStream_t stream) {
   const int cus = device_cu_count();
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
+  if (blocks <= 2L * cus && (a.causal || blocks <= cus))
+    return launch(flash_fwd_bf16_pipe_kernel<E, 128, 64, 2, 2>, a, stream, 2 * kThreads);
   if (blocks < 3L * cus) return launch(flash_fwd_bf16_pipe_kernel<E, 128, 64, 2>, a, stream);
   return launch(flash_fwd_bf16_pipe_kernel<E, 128, 32, 3>, a, stream);
 }
@@ -966,7 +1020,12 @@ static int launch_h16(const FlashArgs& a, int head_dim, hipStream_t s) {
     return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 0>, a, s) : launch_pipe128<E>(a, s);
   }
   if (ring) return launch_flash_bias_ring(64, a, s);
-  return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 0>, a, s) : launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2>, a, s);
+  if (hb) return launch(flash_fwd_bf16_kernel<E, 64, true, 0>, a, s);
+  const long blocks = (long)a.n_qtiles * a.B * a.Hq;
+  const int cus = device_cu_count();
+  if (blocks <= 2L * cus && (a.causal || blocks <= cus))
+    return launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2, 2>, a, s, 2 * kThreads);
+  return launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2>, a, s);
 }
 
 // The fp32 split kernel: one workgroup per 32-row query block.

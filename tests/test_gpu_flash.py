@@ -77,6 +77,41 @@ def test_flash_bf16_matches_oracle(device, b, lq, lk, hq, hkv, d, causal):
     assert max_abs(to_np(got), ref32) <= BF16_TOL
 
 
+@pytest.mark.parametrize(
+    "b,lq,lk,hq,hkv,d,causal,lengths,dt",
+    [
+        (1, 64, 64, 1, 1, 128, True, None, "bf16"),           # one key tile: the second group has none
+        (2, 333, 333, 3, 1, 128, True, [333, 150], "bf16"),   # GQA-3, lengths, odd tile count
+        (1, 190, 700, 2, 2, 64, False, [650], "bf16"),        # non-causal, 11 tiles over two groups
+        (1, 256, 256, 2, 2, 64, True, None, "f16"),
+    ],
+)
+def test_flash_two_group_small_grids(device, b, lq, lk, hq, hkv, d, causal, lengths, dt):
+    """Grids of at most one workgroup per CU (or two, causal) run 8 waves per
+    workgroup: two groups of 4 take alternate key tiles of the same 128 rows
+    and merge (max, sum, O) through LDS."""
+    import torch
+
+    q, k, v = (oracle.round_bf16(x) if dt == "bf16" else x.astype(np.float16).astype(np.float32)
+               for x in _inputs(7, b, lq, lk, hq, hkv, d))
+    scale = 1.0 / math.sqrt(d)
+    masks = [oracle.CausalMask()] if causal else []
+    if lengths is not None:
+        masks.append(oracle.KVLenMask(np.array(lengths, np.int32)))
+    mask = None if not masks else (masks[0] if len(masks) == 1 else oracle.ComposeMask("and", *masks))
+    want, want_lse = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale, return_lse=True)
+    tdt = torch.bfloat16 if dt == "bf16" else torch.float16
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    got, lse = _flash(*(to_dev(x, device, tdt) for x in (q, k, v)), sm_scale=scale, causal=causal,
+                      kv_lengths=L, return_lse=True)
+    torch.cuda.synchronize()
+    assert max_abs(to_np(got), want) <= BF16_TOL
+    lse = to_np(lse)
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
+    fin = np.isfinite(want_lse)
+    assert max_abs(lse[fin], want_lse[fin]) <= 1e-2
+
+
 @pytest.mark.parametrize("dtype_name", ["f32", "bf16"])
 def test_flash_bias_kvlen(device, dtype_name):
     import torch
