@@ -312,6 +312,11 @@ __global__ __launch_bounds__(kThreads, 2) void flash_fwd_bf16_kernel(FlashArgs a
 // this wave will not use it (past its causal diagonal, past the last tile):
 // it reads whatever the slot holds and is discarded, so the block stays
 // branch-free.
+//
+// G = 2 (small grids): 8 waves, two groups of 4 over the same 128 rows, group
+// j taking the key tiles t with t % 2 == j through a ring of its own (the
+// loop above in the group's local tile index, the barriers in step), then
+// group 1 hands (max, sum, O) to group 0 through LDS.
 // ---------------------------------------------------------------------------
 template <typename E, int D, int BKT, int WPC, int G = 1>
 __global__ __launch_bounds__(G * kThreads, WPC) void flash_fwd_bf16_pipe_kernel(FlashArgs a) {
@@ -986,7 +991,8 @@ static int launch(K kernel, const FlashArgs& a, hipStream_t stream, int threads 
 // 2 per CU or less, as at batch*heads = 16) run 64-key tiles, whose longer
 // steps between barriers hide latency better at that occupancy (measured:
 // 87 us against 113 us at B=1, H=16, L=4096 causal; 1-1.5% slower than
-// 32-key tiles from 1024 workgroups up).
+// 32-key tiles from 1024 workgroups up).  Grids of at most one workgroup per
+// CU (two, causal) run the two-group form: 81 against 89 us there.
 template <typename E>
 static int launch_pipe128(const FlashArgs& a, hipStream_t stream) {
   const int cus = device_cu_count();
