@@ -30,6 +30,7 @@ pytestmark = pytest.mark.gpu
     ("bf16", 2, 200, 3, 72, 40, 24, 64),
     ("bf16", 1, 384, 4, 512, 128, 128, 128),
     ("bf16", 2, 33, 2, 12, 16, 12, 64),   # rank not a multiple of 8: element loads
+    ("bf16", 2, 1900, 8, 72, 96, 64, 128),  # many tiles, ragged last row tile
     ("f32", 2, 200, 3, 72, 40, 24, 64),
     ("f32", 1, 130, 2, 20, 64, 128, 128),
 ])
