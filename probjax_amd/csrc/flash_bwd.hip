@@ -32,6 +32,15 @@ static int run_bwd_h16(const FlashBwdArgs& a, bool hb, hipStream_t s) {
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
+  if constexpr (EXT == 0) {
+    // Small grids (at most one workgroup per CU, or two with a causal mask,
+    // whose key blocks differ in length): two groups of 4 waves per key block.
+    const long blocks = (long)((a.f.Lk + kBKV - 1) / kBKV) * a.f.B * a.f.Hkv;
+    const int cus = device_cu_count();
+    if (blocks <= 2L * cus && (a.f.causal || blocks <= cus))
+      return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, D, true, 0, 2>, a, s, 2 * kThreads)
+                : launch_dkdv(flash_bwd_dkdv_kernel<E, D, false, 0, 2>, a, s, 2 * kThreads);
+  }
   return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, D, true, EXT>, a, s)
             : launch_dkdv(flash_bwd_dkdv_kernel<E, D, false, EXT>, a, s);
 }

@@ -85,17 +85,18 @@ struct BwdOffsets {
   uint32_t row[D / 16];   // A = X[row][dim]: row `col` of a 32-row block, dims 16*s + 8*half
   uint32_t tlo[D / 32];   // A = X^T: transposing reads, rows 4*half + s16/4 of a 16-row step
   uint32_t thi[D / 32];   // ... and rows 8 + 4*half + s16/4
-  __device__ void init(int lane) {
+  // base: byte offset added to every offset (a wave group's stage)
+  __device__ void init(int lane, uint32_t base = 0) {
     const int col = lane & 31, half = lane >> 5;
 #pragma unroll
-    for (int s = 0; s < D / 16; ++s) row[s] = col * T::ROWB + 16 * ((2 * s + half) ^ T::swz(col));
+    for (int s = 0; s < D / 16; ++s) row[s] = base + col * T::ROWB + 16 * ((2 * s + half) ^ T::swz(col));
     const int s16 = lane & 15, grp = lane >> 4;
     const int r = 4 * half + s16 / 4;
 #pragma unroll
     for (int db = 0; db < D / 32; ++db) {
       const int chunk = 4 * db + 2 * (grp & 1) + ((s16 & 3) >> 1);
-      tlo[db] = r * T::ROWB + 16 * (chunk ^ T::swz(r)) + 8 * (s16 & 1);
-      thi[db] = (r + 8) * T::ROWB + 16 * (chunk ^ T::swz(r + 8)) + 8 * (s16 & 1);
+      tlo[db] = base + r * T::ROWB + 16 * (chunk ^ T::swz(r)) + 8 * (s16 & 1);
+      thi[db] = base + (r + 8) * T::ROWB + 16 * (chunk ^ T::swz(r + 8)) + 8 * (s16 & 1);
     }
   }
 };
@@ -369,10 +370,13 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
 }
 
 // ---------------------------------------------------------------------------
-// dK, dV: one workgroup per (128-key tile, batch, KV head).
+// dK, dV: one workgroup per (128-key tile, batch, KV head).  NG = 2 (small
+// grids): 8 waves, two groups of 4 over the same 128 keys; group j takes the
+// (query tile, head) steps t with t % 2 == j through its own 2-stage ring, and
+// at the end group 1 adds its dK / dV sums into group 0's through LDS.
 // ---------------------------------------------------------------------------
-template <typename E, int D, bool BIAS, int EXT>
-__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
+template <typename E, int D, bool BIAS, int EXT, int NG = 1>
+__global__ __launch_bounds__(NG * kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_kernel(FlashBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
   constexpr int ROWB = T::ROWB, TILE_B = T::TILE_B;
@@ -381,11 +385,16 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
   // lse*log2e and delta * sm_scale (64 floats each).
   constexpr int SMALL_B = 2 * kBQs * 4;
   constexpr int STAGE_B = 2 * TILE_B + 4 * SMALL_B;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
-  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+  static_assert(NG == 1 || NG == 2, "one or two groups");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[NG * STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[NG * STAGE_B];
 
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = NG > 1 ? w8 >> 2 : 0;   // group: the steps t with t % NG == gi
+  const int w = NG > 1 ? (w8 & 3) : w8;  // wave within the group: keys 32w .. of the tile
+  unsigned char* const st0 = smem0 + gi * STAGE_B;  // this group's stages
+  unsigned char* const st1 = smem1 + gi * STAGE_B;
   const int col = lane & 31, half = lane >> 5;
   const int BH = a.B * a.Hkv;
   const int bh = blockIdx.x % BH;
@@ -450,7 +459,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
     voff[j] = r * rowstride + 16 * (slot ^ T::swz(r));
   }
   BwdOffsets<D> off;
-  off.init(lane);
+  off.init(lane, gi * STAGE_B);  // fragment reads address the group's stage from smem0 / smem1
 
   f32x16 acck[D / 32], accv[D / 32];
 #pragma unroll
@@ -491,7 +500,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
     const int h = tile_head(t), q0 = tile_q0(t);
     const unsigned char* qs = st;
     const unsigned char* dos = st + TILE_B;
-    const float* lsm = (const float*)(st + 2 * TILE_B + w * SMALL_B);
+    const float* lsm = (const float*)(st + gi * STAGE_B + 2 * TILE_B + w * SMALL_B);
     const float* dlm = lsm + kBQs;
     const float* bbase = nullptr;
     if constexpr (BIAS) bbase = a.bias + (size_t)b * a.bias_bstride + (size_t)h * a.bias_hstride;
@@ -602,17 +611,53 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dkdv_k
     }
   };
 
-  if (n_tiles > 0) issue(0, smem0);
-  for (int t = 0; t < n_tiles; t += 2) {
+  // this group's steps NG*s + gi: n_loc of them; n_steps (the same for every
+  // group) keeps the barriers in step
+  const int n_loc = (n_tiles - gi + NG - 1) / NG;
+  const int n_steps = (n_tiles + NG - 1) / NG;
+  if (n_loc > 0) issue(gi, st0);
+  for (int s = 0; s < n_steps; s += 2) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 1 < n_tiles) issue(t + 1, smem1);
-    compute(t, smem0);
-    if (t + 1 >= n_tiles) break;
+    if (s + 1 < n_loc) issue(NG * (s + 1) + gi, st1);
+    if (s < n_loc) compute(NG * s + gi, smem0);
+    if (s + 1 >= n_steps) break;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 2 < n_tiles) issue(t + 2, smem0);
-    compute(t + 1, smem1);
+    if (s + 2 < n_loc) issue(NG * (s + 2) + gi, st0);
+    if (s + 1 < n_loc) compute(NG * (s + 1) + gi, smem1);
+  }
+  if constexpr (NG > 1) {
+    // Group 1 hands its dK^T / dV^T sums to group 0 through LDS, lane by lane
+    // in the same register layout: 16-byte quads [D/32 * 4][4 waves][64 lanes],
+    // dK over stage 0, dV over stage 1.
+    static_assert((D / 32) * 4 * 256 * 16 <= NG * STAGE_B, "hand-off fits");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // every wave is done with the rings
+    f32x4* xk = (f32x4*)smem0 + w * 64 + lane;
+    f32x4* xv = (f32x4*)smem1 + w * 64 + lane;
+    if (gi == 1) {
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 4) {
+          xk[(4 * i + r / 4) * 256] = f32x4{acck[i][r], acck[i][r + 1], acck[i][r + 2], acck[i][r + 3]};
+          xv[(4 * i + r / 4) * 256] = f32x4{accv[i][r], accv[i][r + 1], accv[i][r + 2], accv[i][r + 3]};
+        }
+    }
+    __syncthreads();
+    if (gi == 1) return;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const f32x4 k1 = xk[(4 * i + r / 4) * 256], v1 = xv[(4 * i + r / 4) * 256];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acck[i][r + j] += k1[j];
+          accv[i][r + j] += v1[j];
+        }
+      }
   }
 
   // dK, dV rows of this lane's key (zeros for keys past the valid length).
@@ -1095,9 +1140,9 @@ static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
 }
 
 template <typename K>
-static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
+static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)((a.f.Lk + kBKV - 1) / kBKV) * a.f.B * a.f.Hkv;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_bwd (dk, dv)");
 }
 

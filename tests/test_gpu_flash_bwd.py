@@ -159,3 +159,38 @@ def test_flash_bwd_f32_matches_float64_oracle(device, B, Lq, Lk, Hq, Hkv, D, cau
         tol = 1e-5 * max(1.0, float(np.max(np.abs(w))))
         err = float(np.max(np.abs(to_np(g).astype(np.float64) - w)))
         assert err <= tol, f"{name}: max err {err:.3e} > {tol:.3e}"
+
+
+@pytest.mark.parametrize("D,Hq,Hkv,L,causal", [(128, 16, 16, 2048, True), (64, 16, 4, 2048, True),
+                                                (128, 8, 8, 2048, False), (128, 4, 2, 1000, True)])
+def test_flash_bwd_small_grid_matches_large_grid(device, D, Hq, Hkv, L, causal):
+    """Small grids (at most one key block per CU, or two with a causal mask) run
+    the dK/dV kernel with two groups of waves per key block, each summing half
+    of the query tiles; the same inputs repeated over a batch large enough for
+    the one-group form give the same gradients: dq bit for bit (the same
+    kernel), dk and dv to one bf16 rounding (the same fp32 terms, summed in
+    another order)."""
+    import torch
+    from probjax_amd.hip_attention import flash_attention_bwd, flash_attention_fwd
+
+    nkb = -(-L // 128)
+    rep = (2 * 256) // (nkb * Hkv) + 1   # key blocks above two per CU of a 256-CU device
+    print(f"case D={D} Hq={Hq} Hkv={Hkv} L={L} causal={causal} rep={rep}", flush=True)
+    g = torch.Generator(device=device)
+    g.manual_seed(31)
+    bf = torch.bfloat16
+    q, do = (torch.randn((1, L, Hq, D), generator=g, device=device).to(bf) for _ in range(2))
+    k, v = (torch.randn((1, L, Hkv, D), generator=g, device=device).to(bf) for _ in range(2))
+    scale = 1.0 / math.sqrt(D)
+    o, lse = flash_attention_fwd(q, k, v, sm_scale=scale, causal=causal, return_lse=True)
+    small = flash_attention_bwd(q, k, v, o, do, lse, sm_scale=scale, causal=causal)
+    big_in = [x.expand(rep, *x.shape[1:]).contiguous() for x in (q, k, v, o, do, lse)]
+    big = flash_attention_bwd(*big_in, sm_scale=scale, causal=causal)
+    torch.cuda.synchronize()
+    assert torch.equal(big[0], small[0].expand_as(big[0])), "dq differs"
+    for name, gb, gs in zip(("dk", "dv"), big[1:], small[1:]):
+        a = gb.float()
+        b = gs.float().expand_as(a)
+        err = (a - b).abs()
+        lim = 2.0 ** -7 * b.abs() + 1e-3 * b.abs().max()
+        assert bool((err <= lim).all()), f"{name}: max err {err.max().item():.3e}"
