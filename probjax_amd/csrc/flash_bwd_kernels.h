@@ -150,23 +150,36 @@ __device__ __forceinline__ void store_dbias(const FlashBwdArgs& ba, const BlockG
 
 // ---------------------------------------------------------------------------
 // ---------------------------------------------------------------------------
-// dQ (and delta): one workgroup per (128-query tile, batch, head).
+// dQ (and delta): one workgroup per (128-query tile, batch, head).  NG = 2
+// (small grids): 8 waves, two groups of 4 over the same 128 queries; group j
+// takes the key tiles t with t % 2 == j through its own 2-stage ring, and at
+// the end group 1 adds its dQ sums into group 0's through LDS.
 // ---------------------------------------------------------------------------
-template <typename E, int D, int BIAS, int EXT>
-__global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
+template <typename E, int D, int BIAS, int EXT, int NG = 1>
+__global__ __launch_bounds__(NG * kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_kernel(FlashBwdArgs ba) {
   // BIAS: 0 none, 1 dense bias, 2 dense bias and its gradient (ba.dbias)
   constexpr bool HB = BIAS != 0, DB = BIAS == 2;
   const FlashArgs& a = ba.f;
   using T = BwdTile<D>;
   constexpr int BK = T::ROWS, ROWB = T::ROWB, TILE_B = T::TILE_B;
-  __shared__ __attribute__((aligned(1024))) unsigned char smem0[2 * TILE_B];
-  __shared__ __attribute__((aligned(1024))) unsigned char smem1[2 * TILE_B];
+  constexpr int STAGE_B = 2 * TILE_B;
+  static_assert(NG == 1 || NG == 2 && EXT == 0, "one group, or two without extended masks");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[NG * STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[NG * STAGE_B];
 
   BlockGeom g = block_geom(a);
   if constexpr (EXT > 0) ext_block_range(a, g, BK);
   const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int w8 = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gi = NG > 1 ? w8 >> 2 : 0;   // group: the key tiles t with t % NG == gi
+  const int w = NG > 1 ? (w8 & 3) : w8;  // wave within the group: rows 32w .. of the q tile
+  if constexpr (NG > 1) {
+    g.qw = g.q0 + 32 * w;
+    g.qi = g.qw + (tid & 31);
+  }
   g.qw = __builtin_amdgcn_readfirstlane(g.qw);
+  unsigned char* const st0 = smem0 + gi * STAGE_B;  // this group's stages
+  unsigned char* const st1 = smem1 + gi * STAGE_B;
   const int col = lane & 31, half = lane >> 5;
   const uint32_t rowstride = (uint32_t)a.Hkv * D * 2;
   const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)g.b * a.Lk * a.Hkv + g.hkv) * ROWB;
@@ -204,7 +217,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
   const size_t lidx = ((size_t)g.b * a.Hq + g.h) * a.Lq + g.qi;
   if (row_in) {
     lse2 = a.lse[lidx] * kLog2e;
-    if (half == 0) {
+    if (half == 0 && gi == 0) {
       ba.delta[lidx] = dsc;
       ba.lse2[lidx] = lse2;
     }
@@ -226,7 +239,7 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
     voff[j] = r * rowstride + 16 * (slot ^ T::swz(r));
   }
   BwdOffsets<D> off;
-  off.init(lane);
+  off.init(lane, gi * STAGE_B);  // fragment reads address the group's stage from smem0 / smem1
 
   f32x16 acc[D / 32];
 #pragma unroll
@@ -342,17 +355,46 @@ __global__ __launch_bounds__(kThreads, (D <= 128 ? 2 : 1)) void flash_bwd_dq_ker
         acc[db] = E::mma32(read_t<E, D>(ks, 16 * c, off.tlo[db], off.thi[db]), dsf[c], acc[db]);
   };
 
-  if (n_tiles > 0) issue(0, smem0);
-  for (int t = 0; t < n_tiles; t += 2) {
+  // this group's tiles NG*s + gi: n_loc of them; n_steps (the same for every
+  // group) keeps the barriers in step
+  const int n_loc = (n_tiles - gi + NG - 1) / NG;
+  const int n_steps = (n_tiles + NG - 1) / NG;
+  if (n_loc > 0) issue(gi, st0);
+  for (int s = 0; s < n_steps; s += 2) {
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 1 < n_tiles) issue(t + 1, smem1);
-    compute(t, smem0);
-    if (t + 1 >= n_tiles) break;
+    if (s + 1 < n_loc) issue(NG * (s + 1) + gi, st1);
+    if (s < n_loc) compute(NG * s + gi, smem0);
+    if (s + 1 >= n_steps) break;
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (t + 2 < n_tiles) issue(t + 2, smem0);
-    compute(t + 1, smem1);
+    if (s + 2 < n_loc) issue(NG * (s + 2) + gi, st0);
+    if (s + 1 < n_loc) compute(NG * (s + 1) + gi, smem1);
+  }
+  if constexpr (NG > 1) {
+    // Group 1 hands its dQ^T sums to group 0 through LDS, lane by lane in the
+    // same register layout: 16-byte quads [D/32 * 4][4 waves][64 lanes].
+    static_assert((D / 32) * 4 * 256 * 16 <= NG * STAGE_B, "hand-off fits");
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();  // every wave is done with the rings
+    f32x4* xq = (f32x4*)smem0 + w * 64 + lane;
+    if (gi == 1) {
+#pragma unroll
+      for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; r += 4)
+          xq[(4 * i + r / 4) * 256] = f32x4{acc[i][r], acc[i][r + 1], acc[i][r + 2], acc[i][r + 3]};
+    }
+    __syncthreads();
+    if (gi == 1) return;
+#pragma unroll
+    for (int i = 0; i < D / 32; ++i)
+#pragma unroll
+      for (int r = 0; r < 16; r += 4) {
+        const f32x4 q1 = xq[(4 * i + r / 4) * 256];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][r + j] += q1[j];
+      }
   }
 
   if (row_in) {
@@ -1133,9 +1175,9 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
 }
 
 template <typename K>
-static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream) {
+static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)a.f.n_qtiles * a.f.B * a.f.Hq;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_bwd (dq)");
 }
 
