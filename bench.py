@@ -135,7 +135,7 @@ def make_c2(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="C2 causal fwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3>")
+                bound="mfma", dtype="bf16", kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3,1>")
 
 
 def make_c2h(dev, gen):
@@ -149,7 +149,7 @@ def make_c2h(dev, gen):
     nbytes = 4 * B * L * H * D * 2
     fn = lambda: flash_attention_fwd(q, k, v, sm_scale=1 / math.sqrt(D), causal=True)  # noqa: E731
     return dict(name="C2 causal fwd fp16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop, bytes=nbytes,
-                bound="mfma", dtype="f16", kernel="flash_fwd_bf16_pipe_kernel<F16Fmt,128,32,3>")
+                bound="mfma", dtype="f16", kernel="flash_fwd_bf16_pipe_kernel<F16Fmt,128,32,3,1>")
 
 
 def c3_lengths(seed=0, batch=32, lo=512, hi=8192):
@@ -244,7 +244,7 @@ def make_c2b(dev, gen):
                                      workspace=ws)
     return dict(name="C2 causal bwd bf16 B=4 H=16 L=4096 D=128 (dq, dk, dv)", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_bwd_dq_kernel<Bf16Fmt,128,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0>")
+                kernel="flash_bwd_dq_kernel<Bf16Fmt,128,0,0,1> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0,1>")
 
 
 def make_c2fb(dev, gen):
@@ -265,7 +265,7 @@ def make_c2fb(dev, gen):
     nbytes = 2 * B * L * H * D * 2 * 5 + B * H * L * 4
     return dict(name="C2 causal fwd+bwd bf16 B=4 H=16 L=4096 D=128", fn=fn, flop=flop,
                 bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3> + flash_bwd_dq_kernel<Bf16Fmt,128,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0>")
+                kernel="flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,32,3,1> + flash_bwd_dq_kernel<Bf16Fmt,128,0,0,1> + flash_bwd_dkdv_kernel<Bf16Fmt,128,false,0,1>")
 
 
 def _mla_prefill_inputs(dev, gen):
@@ -308,7 +308,7 @@ def make_c5m(dev, gen):
     nbytes = B * L * R * 2 + 2 * H * D * R * 2 + 2 * B * L * H * D * 2
     return dict(name="MLA materialised causal prefill bf16 B=1 L=4096 R=512 H=16 dk=dv=128", fn=fn,
                 flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="mla_project_bf16_kernel<Bf16Fmt> + flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,64,2>")
+                kernel="mla_project_bf16_kernel<Bf16Fmt> + flash_fwd_bf16_pipe_kernel<Bf16Fmt,128,64,2,2>")
 
 
 def _latent_prefill_inputs(dev, gen):
@@ -353,7 +353,7 @@ def make_c5ab(dev, gen):
     fn = lambda: mla_bwd(q, cache, o, do, lse, sm_scale=sc, causal=True)  # noqa: E731
     return dict(name="MLA absorbed causal prefill backward bf16 B=1 L=4096 H=16 R=576 Dv=512 (dq, dcache)",
                 fn=fn, flop=flop, bytes=nbytes, bound="mfma", dtype="bf16",
-                kernel="wide_bwd_dq_kernel<Bf16Fmt,576,512,true,0,0> + wide_bwd_dkdv_kernel<Bf16Fmt,576,512,true,false,0> + wide_bwd_reduce_kernel<Bf16Fmt>")
+                kernel="wide_bwd_dq_kernel<Bf16Fmt,576,512,true,0,0> + wide_bwd_dc_kernel<Bf16Fmt,576,512,true> + wide_bwd_reduce_kernel<Bf16Fmt>")
 
 
 def make_c2w(dev, gen):
@@ -388,7 +388,7 @@ def make_c2wb(dev, gen):
     fn = lambda: flash_attention_bwd(q, k, v, o, do, lse, sm_scale=sc, causal=True, workspace=ws)  # noqa: E731
     return dict(name="causal bwd bf16 B=2 H=16 L=4096 D=256 (dq, dk, dv)", fn=fn, flop=flop, bytes=nbytes,
                 bound="mfma", dtype="bf16",
-                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,256,false,0>")
+                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,256,false,0,1>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,
@@ -558,7 +558,7 @@ def main():
                        "head_dim": 128, "mask": "causal", "flop_per_step": w["flop"]},
             "roofline": {"bound": "mfma", "achieved": round(tflops, 2), "peak": PEAK_BF16_TFLOPS,
                          "unit": "TFLOP/s", "frac": round(frac, 4),
-                         "traffic": measured_traffic("pjx::flash_fwd_bf16_pipe_kernel<pjx::Bf16Fmt, 128, 32, 3>"),
+                         "traffic": measured_traffic("pjx::flash_fwd_bf16_pipe_kernel<pjx::Bf16Fmt, 128, 32, 3, 1>"),
                          "traffic_unit": "bytes per launch (rocprofv3 FETCH_SIZE+WRITE_SIZE, copy-calibrated)",
                          "kernel": w["kernel"]},
         })
