@@ -105,6 +105,16 @@ int pjx_version(void);
 const char* pjx_last_error(void);
 
 /*
+ * Kernel instances that the calling thread's last entry-point call launched,
+ * in launch order, ';'-separated ("" if none), e.g.
+ * "flash_bwd_dq_kernel<Bf16Fmt, 128, 0, 0, 1>;flash_bwd_dkdv_kernel<...>".
+ * Diagnostics (which kernel a launcher picked for a shape); no counterpart in
+ * the reference, whose Pallas launch has one kernel per call.  Valid until the
+ * thread's next entry-point call.
+ */
+const char* pjx_last_launches(void);
+
+/*
  * Flash-attention forward.  Replaces the Pallas `mha_forward` kernel and its
  * launch (`_mha_impl_raw`, probjax/nn/pallas_kernels/kernels/attention.py:
  * 377-533, 2130-2278) for the masks/biases of the path, with the semantics of

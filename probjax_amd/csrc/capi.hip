@@ -1,19 +1,52 @@
 // Library-wide C-ABI entry points: version, error reporting.
+#include <cxxabi.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
+
+#include <string>
 
 #include "flash_common.h"
 
 namespace pjx {
 
 static thread_local char g_error[512];
+// Kernel instances launched by the calling thread's current (or last) entry
+// point call, in launch order, ';'-separated.
+static thread_local char g_launches[2048];
 
 void set_error(const char* msg) {
   strncpy(g_error, msg, sizeof(g_error) - 1);
   g_error[sizeof(g_error) - 1] = '\0';
 }
 
-void clear_error() { g_error[0] = '\0'; }
+void clear_error() {
+  g_error[0] = '\0';
+  g_launches[0] = '\0';
+}
+
+void note_launch(const char* name) {
+  const size_t n = strlen(g_launches), m = strlen(name);
+  if (n + m + 2 > sizeof(g_launches)) return;  // the log keeps the first launches that fit
+  if (n > 0) g_launches[n] = ';';
+  memcpy(g_launches + n + (n > 0), name, m + 1);
+}
+
+// typeid(KernelTag<&kern<...>>) demangles to
+// "pjx::KernelTag<&(void pjx::kern<args>(params))>"; keeps "kern<args>"
+// without namespace qualifiers.
+std::string demangled_kernel_name(const char* mangled) {
+  int st = 0;
+  char* d = abi::__cxa_demangle(mangled, nullptr, nullptr, &st);
+  std::string full = (st == 0 && d) ? d : mangled;
+  free(d);
+  size_t b = full.find("void ");
+  b = b == std::string::npos ? 0 : b + 5;
+  size_t e = full.find('(', b);
+  std::string name = full.substr(b, e == std::string::npos ? std::string::npos : e - b);
+  for (size_t p; (p = name.find("pjx::")) != std::string::npos;) name.erase(p, 5);
+  return name;
+}
 
 int check_launch(const char* where) {
   const hipError_t err = hipGetLastError();
@@ -35,14 +68,14 @@ __global__ __launch_bounds__(256) void zero_u16_kernel(uint16_t* p, size_t n) {
 int fill_u32(void* p, uint32_t value, size_t n, hipStream_t stream, const char* who) {
   if (n == 0) return PJX_OK;
   const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (uint32_t*)p, value, n);
+  launch_kernel<fill_u32_kernel>(dim3((unsigned)blocks), dim3(256), 0, stream, (uint32_t*)p, value, n);
   return check_launch(who);
 }
 
 int zero_u16(void* p, size_t n, hipStream_t stream, const char* who) {
   if (n == 0) return PJX_OK;
   const size_t blocks = std::min<size_t>((n + 255) / 256, 65536);
-  hipLaunchKernelGGL(zero_u16_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)p, n);
+  launch_kernel<zero_u16_kernel>(dim3((unsigned)blocks), dim3(256), 0, stream, (uint16_t*)p, n);
   return check_launch(who);
 }
 
@@ -125,3 +158,5 @@ int lower_score_mods(const pjx_score_mods* mods, FlashArgs& a, const char* who) 
 extern "C" int pjx_version(void) { return 100; }
 
 extern "C" const char* pjx_last_error(void) { return pjx::g_error; }
+
+extern "C" const char* pjx_last_launches(void) { return pjx::g_launches; }

@@ -952,8 +952,8 @@ static size_t ws_size(int64_t batch, int64_t groups, int64_t rows, int64_t kv_le
   return (size_t)(parts * v_dim + parts * 2) * sizeof(float);
 }
 
-template <typename K>
-static int run_decode(K kernel, DecodeArgs& a, void* workspace, size_t ws_bytes,
+template <auto K>
+static int run_decode(DecodeArgs& a, void* workspace, size_t ws_bytes,
                       hipStream_t stream, const char* name) {
   const size_t need = ws_size(a.B, a.G, a.rows, a.Lk, a.dv, a.chunk);
   if (!workspace || ws_bytes < need) return fail(PJX_ERR_WORKSPACE, "decode: workspace missing or too small");
@@ -963,11 +963,11 @@ static int run_decode(K kernel, DecodeArgs& a, void* workspace, size_t ws_bytes,
   const long blocks = (long)a.B * a.G * a.nch;
   if (blocks > 0x7fffffffL || (long)a.B * a.G * a.rows > 0x7fffffffL)
     return fail(PJX_ERR_INVALID, "decode: grid too large");
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kDecThreads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(kDecThreads), 0, stream, a);
   int rc = check_launch(name);
   if (rc) return rc;
   const long merge_threads = (long)a.B * a.G * a.rows * (a.dv / 4);
-  hipLaunchKernelGGL(decode_merge_kernel, dim3((unsigned)((merge_threads + kMergeThreads - 1) / kMergeThreads)),
+  launch_kernel<decode_merge_kernel>(dim3((unsigned)((merge_threads + kMergeThreads - 1) / kMergeThreads)),
                      dim3(kMergeThreads), 0, stream, a);
   return check_launch(name);
 }
@@ -977,23 +977,23 @@ template <typename E>
 static int run_gqa_h16(DecodeArgs& a, int head_dim, int nrb, void* ws, size_t ws_bytes, hipStream_t s,
                        const char* who) {
   if (head_dim == 128) {
-    if (nrb == 1) return run_decode(gqa_decode_kernel<E, 128, 1>, a, ws, ws_bytes, s, who);
-    if (nrb == 2) return run_decode(gqa_decode_kernel<E, 128, 2>, a, ws, ws_bytes, s, who);
-    return run_decode(gqa_decode_kernel<E, 128, 4>, a, ws, ws_bytes, s, who);
+    if (nrb == 1) return run_decode<gqa_decode_kernel<E, 128, 1>>(a, ws, ws_bytes, s, who);
+    if (nrb == 2) return run_decode<gqa_decode_kernel<E, 128, 2>>(a, ws, ws_bytes, s, who);
+    return run_decode<gqa_decode_kernel<E, 128, 4>>(a, ws, ws_bytes, s, who);
   }
-  if (nrb == 1) return run_decode(gqa_decode_kernel<E, 64, 1>, a, ws, ws_bytes, s, who);
-  if (nrb == 2) return run_decode(gqa_decode_kernel<E, 64, 2>, a, ws, ws_bytes, s, who);
-  return run_decode(gqa_decode_kernel<E, 64, 4>, a, ws, ws_bytes, s, who);
+  if (nrb == 1) return run_decode<gqa_decode_kernel<E, 64, 1>>(a, ws, ws_bytes, s, who);
+  if (nrb == 2) return run_decode<gqa_decode_kernel<E, 64, 2>>(a, ws, ws_bytes, s, who);
+  return run_decode<gqa_decode_kernel<E, 64, 4>>(a, ws, ws_bytes, s, who);
 }
 
 // The latent decode (format E) at one (rank, v_dim).
 template <typename E>
 static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, size_t ws_bytes, hipStream_t s) {
   const char* who = "pjx_mla_decode";
-  if (rank == 576 && v_dim == 512) return run_decode(mla_decode_kernel<E, 576, 512>, a, ws, ws_bytes, s, who);
-  if (rank == 576 && v_dim == 576) return run_decode(mla_decode_kernel<E, 576, 576>, a, ws, ws_bytes, s, who);
-  if (rank == 512 && v_dim == 512) return run_decode(mla_decode_kernel<E, 512, 512>, a, ws, ws_bytes, s, who);
-  if (rank == 128 && v_dim == 128) return run_decode(mla_decode_kernel<E, 128, 128>, a, ws, ws_bytes, s, who);
+  if (rank == 576 && v_dim == 512) return run_decode<mla_decode_kernel<E, 576, 512>>(a, ws, ws_bytes, s, who);
+  if (rank == 576 && v_dim == 576) return run_decode<mla_decode_kernel<E, 576, 576>>(a, ws, ws_bytes, s, who);
+  if (rank == 512 && v_dim == 512) return run_decode<mla_decode_kernel<E, 512, 512>>(a, ws, ws_bytes, s, who);
+  if (rank == 128 && v_dim == 128) return run_decode<mla_decode_kernel<E, 128, 128>>(a, ws, ws_bytes, s, who);
   return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
 }
 
@@ -1051,10 +1051,10 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   const int nrb = (int)((rows + kRows - 1) / kRows);
   if (f32) {
     if (head_dim == 128)
-      return nrb == 1 ? run_decode(gqa_decode_f32_kernel<128, 1>, a, workspace, workspace_bytes, s, who)
-                      : run_decode(gqa_decode_f32_kernel<128, 2>, a, workspace, workspace_bytes, s, who);
-    return nrb == 1 ? run_decode(gqa_decode_f32_kernel<64, 1>, a, workspace, workspace_bytes, s, who)
-                    : run_decode(gqa_decode_f32_kernel<64, 2>, a, workspace, workspace_bytes, s, who);
+      return nrb == 1 ? run_decode<gqa_decode_f32_kernel<128, 1>>(a, workspace, workspace_bytes, s, who)
+                      : run_decode<gqa_decode_f32_kernel<128, 2>>(a, workspace, workspace_bytes, s, who);
+    return nrb == 1 ? run_decode<gqa_decode_f32_kernel<64, 1>>(a, workspace, workspace_bytes, s, who)
+                    : run_decode<gqa_decode_f32_kernel<64, 2>>(a, workspace, workspace_bytes, s, who);
   }
   return a.f16 ? run_gqa_h16<F16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who)
                : run_gqa_h16<Bf16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who);

@@ -334,13 +334,13 @@ template <typename E>
 static void launch_ring(int head_dim, const FlashArgs& a, hipStream_t stream) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   if (head_dim == 128)
-    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 128, 2>), dim3((unsigned)blocks), dim3(2 * kThreads), 0,
+    launch_kernel<flash_fwd_bf16_bias_ring_kernel<E, 128, 2>>(dim3((unsigned)blocks), dim3(2 * kThreads), 0,
                        stream, a);
   else if (a.Lk <= kBiasRing3MaxKeys)
-    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64, 3>), dim3((unsigned)blocks), dim3(3 * kThreads), 0,
+    launch_kernel<flash_fwd_bf16_bias_ring_kernel<E, 64, 3>>(dim3((unsigned)blocks), dim3(3 * kThreads), 0,
                        stream, a);
   else
-    hipLaunchKernelGGL((flash_fwd_bf16_bias_ring_kernel<E, 64, 2>), dim3((unsigned)blocks), dim3(2 * kThreads), 0,
+    launch_kernel<flash_fwd_bf16_bias_ring_kernel<E, 64, 2>>(dim3((unsigned)blocks), dim3(2 * kThreads), 0,
                        stream, a);
 }
 

@@ -12,14 +12,14 @@ template <int D, int EXT>
 static int run_bwd_f32(const FlashBwdArgs& a, bool hb, hipStream_t s) {
   if (a.f.Lq > 0) {
     const bool db = a.dbias != nullptr;
-    const int rc = db ? launch_dq(flash_bwd_dq_f32_kernel<D, 2, EXT>, a, s)
-                 : hb ? launch_dq(flash_bwd_dq_f32_kernel<D, 1, EXT>, a, s)
-                      : launch_dq(flash_bwd_dq_f32_kernel<D, 0, EXT>, a, s);
+    const int rc = db ? launch_dq<flash_bwd_dq_f32_kernel<D, 2, EXT>>(a, s)
+                 : hb ? launch_dq<flash_bwd_dq_f32_kernel<D, 1, EXT>>(a, s)
+                      : launch_dq<flash_bwd_dq_f32_kernel<D, 0, EXT>>(a, s);
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
-  return hb ? launch_dkdv(flash_bwd_dkdv_f32_kernel<D, true, EXT>, a, s)
-            : launch_dkdv(flash_bwd_dkdv_f32_kernel<D, false, EXT>, a, s);
+  return hb ? launch_dkdv<flash_bwd_dkdv_f32_kernel<D, true, EXT>>(a, s)
+            : launch_dkdv<flash_bwd_dkdv_f32_kernel<D, false, EXT>>(a, s);
 }
 
 template <typename E, int D, int EXT>
@@ -33,22 +33,22 @@ static int run_bwd_h16(const FlashBwdArgs& a, bool hb, hipStream_t s) {
     int rc;
     if (small((long)a.f.n_qtiles * a.f.B * a.f.Hq)) {
       constexpr int T2 = 2 * kThreads;
-      rc = db ? launch_dq(flash_bwd_dq_kernel<E, D, 2, 0, 2>, a, s, T2)
-         : hb ? launch_dq(flash_bwd_dq_kernel<E, D, 1, 0, 2>, a, s, T2)
-              : launch_dq(flash_bwd_dq_kernel<E, D, 0, 0, 2>, a, s, T2);
+      rc = db ? launch_dq<flash_bwd_dq_kernel<E, D, 2, 0, 2>>(a, s, T2)
+         : hb ? launch_dq<flash_bwd_dq_kernel<E, D, 1, 0, 2>>(a, s, T2)
+              : launch_dq<flash_bwd_dq_kernel<E, D, 0, 0, 2>>(a, s, T2);
     } else {
-      rc = db ? launch_dq(flash_bwd_dq_kernel<E, D, 2, EXT>, a, s)
-         : hb ? launch_dq(flash_bwd_dq_kernel<E, D, 1, EXT>, a, s)
-              : launch_dq(flash_bwd_dq_kernel<E, D, 0, EXT>, a, s);
+      rc = db ? launch_dq<flash_bwd_dq_kernel<E, D, 2, EXT>>(a, s)
+         : hb ? launch_dq<flash_bwd_dq_kernel<E, D, 1, EXT>>(a, s)
+              : launch_dq<flash_bwd_dq_kernel<E, D, 0, EXT>>(a, s);
     }
     if (rc != PJX_OK) return rc;
   }
   if (a.f.Lk == 0) return PJX_OK;
   if (small((long)((a.f.Lk + kBKV - 1) / kBKV) * a.f.B * a.f.Hkv))
-    return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, D, true, 0, 2>, a, s, 2 * kThreads)
-              : launch_dkdv(flash_bwd_dkdv_kernel<E, D, false, 0, 2>, a, s, 2 * kThreads);
-  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<E, D, true, EXT>, a, s)
-            : launch_dkdv(flash_bwd_dkdv_kernel<E, D, false, EXT>, a, s);
+    return hb ? launch_dkdv<flash_bwd_dkdv_kernel<E, D, true, 0, 2>>(a, s, 2 * kThreads)
+              : launch_dkdv<flash_bwd_dkdv_kernel<E, D, false, 0, 2>>(a, s, 2 * kThreads);
+  return hb ? launch_dkdv<flash_bwd_dkdv_kernel<E, D, true, EXT>>(a, s)
+            : launch_dkdv<flash_bwd_dkdv_kernel<E, D, false, EXT>>(a, s);
 }
 
 template <int D, int EXT>

@@ -9,10 +9,10 @@ namespace pjx {
 
 int launch_dkdv256(const FlashBwdArgs& a, bool f16, bool hb, hipStream_t s) {
   if (f16)
-    return hb ? launch_dkdv(flash_bwd_dkdv_kernel<F16Fmt, 256, true, 0>, a, s)
-              : launch_dkdv(flash_bwd_dkdv_kernel<F16Fmt, 256, false, 0>, a, s);
-  return hb ? launch_dkdv(flash_bwd_dkdv_kernel<Bf16Fmt, 256, true, 0>, a, s)
-            : launch_dkdv(flash_bwd_dkdv_kernel<Bf16Fmt, 256, false, 0>, a, s);
+    return hb ? launch_dkdv<flash_bwd_dkdv_kernel<F16Fmt, 256, true, 0>>(a, s)
+              : launch_dkdv<flash_bwd_dkdv_kernel<F16Fmt, 256, false, 0>>(a, s);
+  return hb ? launch_dkdv<flash_bwd_dkdv_kernel<Bf16Fmt, 256, true, 0>>(a, s)
+            : launch_dkdv<flash_bwd_dkdv_kernel<Bf16Fmt, 256, false, 0>>(a, s);
 }
 
 }  // namespace pjx

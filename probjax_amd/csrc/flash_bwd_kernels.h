@@ -1174,17 +1174,17 @@ __global__ __launch_bounds__(kThreads, 1) void flash_bwd_dkdv_f32_kernel(FlashBw
   }
 }
 
-template <typename K>
-static int launch_dq(K kernel, const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
+template <auto K>
+static int launch_dq(const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)a.f.n_qtiles * a.f.B * a.f.Hq;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_bwd (dq)");
 }
 
-template <typename K>
-static int launch_dkdv(K kernel, const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
+template <auto K>
+static int launch_dkdv(const FlashBwdArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)((a.f.Lk + kBKV - 1) / kBKV) * a.f.B * a.f.Hkv;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_bwd (dk, dv)");
 }
 

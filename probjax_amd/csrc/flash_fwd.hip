@@ -979,10 +979,10 @@ __global__ __launch_bounds__(64 * split_waves<D>(), 1) void flash_fwd_f32_split_
   }
 }
 
-template <typename K>
-static int launch(K kernel, const FlashArgs& a, hipStream_t stream, int threads = kThreads) {
+template <auto K>
+static int launch(const FlashArgs& a, hipStream_t stream, int threads = kThreads) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(threads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(threads), 0, stream, a);
   return check_launch("pjx_flash_fwd");
 }
 
@@ -998,9 +998,9 @@ static int launch_pipe128(const FlashArgs& a, hipStream_t stream) {
   const int cus = device_cu_count();
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   if (blocks <= 2L * cus && (a.causal || blocks <= cus))
-    return launch(flash_fwd_bf16_pipe_kernel<E, 128, 64, 2, 2>, a, stream, 2 * kThreads);
-  if (blocks < 3L * cus) return launch(flash_fwd_bf16_pipe_kernel<E, 128, 64, 2>, a, stream);
-  return launch(flash_fwd_bf16_pipe_kernel<E, 128, 32, 3>, a, stream);
+    return launch<flash_fwd_bf16_pipe_kernel<E, 128, 64, 2, 2>>(a, stream, 2 * kThreads);
+  if (blocks < 3L * cus) return launch<flash_fwd_bf16_pipe_kernel<E, 128, 64, 2>>(a, stream);
+  return launch<flash_fwd_bf16_pipe_kernel<E, 128, 32, 3>>(a, stream);
 }
 
 // The 16-bit kernels (bf16 or fp16 operands, format E) for head_dim 64 / 128.
@@ -1012,34 +1012,34 @@ static int launch_h16(const FlashArgs& a, int head_dim, hipStream_t s) {
     // (1: interval masks, 2: segment ids / score modifiers as well).
     const bool full = a.ext == 2;
     if (head_dim == 128) {
-      if (full) return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<E, 128, false, 2>, a, s);
-      return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<E, 128, false, 1>, a, s);
+      if (full) return hb ? launch<flash_fwd_bf16_kernel<E, 128, true, 2>>(a, s) : launch<flash_fwd_bf16_kernel<E, 128, false, 2>>(a, s);
+      return hb ? launch<flash_fwd_bf16_kernel<E, 128, true, 1>>(a, s) : launch<flash_fwd_bf16_kernel<E, 128, false, 1>>(a, s);
     }
-    if (full) return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 2>, a, s) : launch(flash_fwd_bf16_kernel<E, 64, false, 2>, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<E, 64, true, 1>, a, s) : launch(flash_fwd_bf16_kernel<E, 64, false, 1>, a, s);
+    if (full) return hb ? launch<flash_fwd_bf16_kernel<E, 64, true, 2>>(a, s) : launch<flash_fwd_bf16_kernel<E, 64, false, 2>>(a, s);
+    return hb ? launch<flash_fwd_bf16_kernel<E, 64, true, 1>>(a, s) : launch<flash_fwd_bf16_kernel<E, 64, false, 1>>(a, s);
   }
   // Dense bias with 16-byte aligned rows and 32-bit slice offsets: the LDS
   // ring that streams the bias; otherwise bias loads into registers.
   const bool ring = hb && a.Lk % 4 == 0 && (int64_t)a.Lq * a.Lk * 4 < ((int64_t)1 << 31);
   if (head_dim == 128) {
     if (ring) return launch_flash_bias_ring(128, a, s);
-    return hb ? launch(flash_fwd_bf16_kernel<E, 128, true, 0>, a, s) : launch_pipe128<E>(a, s);
+    return hb ? launch<flash_fwd_bf16_kernel<E, 128, true, 0>>(a, s) : launch_pipe128<E>(a, s);
   }
   if (ring) return launch_flash_bias_ring(64, a, s);
-  if (hb) return launch(flash_fwd_bf16_kernel<E, 64, true, 0>, a, s);
+  if (hb) return launch<flash_fwd_bf16_kernel<E, 64, true, 0>>(a, s);
   const long blocks = (long)a.n_qtiles * a.B * a.Hq;
   const int cus = device_cu_count();
   if (blocks <= 2L * cus && (a.causal || blocks <= cus))
-    return launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2, 2>, a, s, 2 * kThreads);
-  return launch(flash_fwd_bf16_pipe_kernel<E, 64, 64, 2>, a, s);
+    return launch<flash_fwd_bf16_pipe_kernel<E, 64, 64, 2, 2>>(a, s, 2 * kThreads);
+  return launch<flash_fwd_bf16_pipe_kernel<E, 64, 64, 2>>(a, s);
 }
 
 // The fp32 split kernel: one workgroup per 32-row query block.
-template <int D, typename K>
-static int launch_split(K kernel, const FlashArgs& a, hipStream_t stream) {
+template <int D, auto K>
+static int launch_split(const FlashArgs& a, hipStream_t stream) {
   const long blocks = (long)((a.Lq + 31) / 32) * a.B * a.Hq;
   if (blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "pjx_flash_fwd: grid too large");
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(64 * split_waves<D>()), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(64 * split_waves<D>()), 0, stream, a);
   return check_launch("pjx_flash_fwd");
 }
 
@@ -1140,24 +1140,24 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   if (a.ext) {
     const bool full = a.ext == 2;
     if (head_dim == 128) {
-      if (full) return hb ? launch(flash_fwd_f32_kernel<128, true, 2>, a, s) : launch(flash_fwd_f32_kernel<128, false, 2>, a, s);
-      return hb ? launch(flash_fwd_f32_kernel<128, true, 1>, a, s) : launch(flash_fwd_f32_kernel<128, false, 1>, a, s);
+      if (full) return hb ? launch<flash_fwd_f32_kernel<128, true, 2>>(a, s) : launch<flash_fwd_f32_kernel<128, false, 2>>(a, s);
+      return hb ? launch<flash_fwd_f32_kernel<128, true, 1>>(a, s) : launch<flash_fwd_f32_kernel<128, false, 1>>(a, s);
     }
-    if (full) return hb ? launch(flash_fwd_f32_kernel<64, true, 2>, a, s) : launch(flash_fwd_f32_kernel<64, false, 2>, a, s);
-    return hb ? launch(flash_fwd_f32_kernel<64, true, 1>, a, s) : launch(flash_fwd_f32_kernel<64, false, 1>, a, s);
+    if (full) return hb ? launch<flash_fwd_f32_kernel<64, true, 2>>(a, s) : launch<flash_fwd_f32_kernel<64, false, 2>>(a, s);
+    return hb ? launch<flash_fwd_f32_kernel<64, true, 1>>(a, s) : launch<flash_fwd_f32_kernel<64, false, 1>>(a, s);
   }
   // fp32 with fewer 128-row workgroups than CUs: split each query block's
   // keys over several waves (latency-bound sizes, like the reference's CPU
   // case).
   if ((long)a.n_qtiles * batch * q_heads < 256) {
     if (head_dim == 128)
-      return hb ? launch_split<128>(flash_fwd_f32_split_kernel<128, true>, a, s)
-                : launch_split<128>(flash_fwd_f32_split_kernel<128, false>, a, s);
-    return hb ? launch_split<64>(flash_fwd_f32_split_kernel<64, true>, a, s)
-              : launch_split<64>(flash_fwd_f32_split_kernel<64, false>, a, s);
+      return hb ? launch_split<128, flash_fwd_f32_split_kernel<128, true>>(a, s)
+                : launch_split<128, flash_fwd_f32_split_kernel<128, false>>(a, s);
+    return hb ? launch_split<64, flash_fwd_f32_split_kernel<64, true>>(a, s)
+              : launch_split<64, flash_fwd_f32_split_kernel<64, false>>(a, s);
   }
-  if (head_dim == 128) return hb ? launch(flash_fwd_f32_kernel<128, true, 0>, a, s) : launch(flash_fwd_f32_kernel<128, false, 0>, a, s);
-  return hb ? launch(flash_fwd_f32_kernel<64, true, 0>, a, s) : launch(flash_fwd_f32_kernel<64, false, 0>, a, s);
+  if (head_dim == 128) return hb ? launch<flash_fwd_f32_kernel<128, true, 0>>(a, s) : launch<flash_fwd_f32_kernel<128, false, 0>>(a, s);
+  return hb ? launch<flash_fwd_f32_kernel<64, true, 0>>(a, s) : launch<flash_fwd_f32_kernel<64, false, 0>>(a, s);
 }
 
 extern "C" int pjx_mla_fwd(int dtype, const void* q, const void* cache, void* o, float* lse,

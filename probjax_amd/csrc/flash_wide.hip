@@ -323,11 +323,11 @@ __global__ __launch_bounds__(kThreads, (wide_fwd_occupancy<D, BIAS, EXT>())) voi
   }
 }
 
-template <typename K>
-static int launch_wide(K kernel, const FlashArgs& a, int n_parts, hipStream_t stream, const char* who) {
+template <auto K>
+static int launch_wide(const FlashArgs& a, int n_parts, hipStream_t stream, const char* who) {
   const long blocks = (long)a.n_qtiles * a.B * a.Hq * n_parts;
   if (blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "wide flash forward: grid too large");
-  hipLaunchKernelGGL(kernel, dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks), dim3(kThreads), 0, stream, a);
   return check_launch(who);
 }
 
@@ -339,10 +339,10 @@ static int launch_wide_fmt(const FlashArgs& a, hipStream_t s, const char* who) {
   const int np = a.dv / DVP;
   const bool hb = a.bias != nullptr;
   if (a.ext)
-    return hb ? launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 2>, a, np, s, who)
-              : launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 2>, a, np, s, who);
-  return hb ? launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 0>, a, np, s, who)
-            : launch_wide(flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 0>, a, np, s, who);
+    return hb ? launch_wide<flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 2>>(a, np, s, who)
+              : launch_wide<flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 2>>(a, np, s, who);
+  return hb ? launch_wide<flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, true, 0>>(a, np, s, who)
+            : launch_wide<flash_fwd_wide_kernel<E, D, DVP, BK, SHARED, false, 0>>(a, np, s, who);
 }
 
 template <int D, int DVP, int BK, bool SHARED>

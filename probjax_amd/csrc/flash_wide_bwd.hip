@@ -920,7 +920,7 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who, bool 
   const long kv_blocks = (long)((a.Lk + kWK - 1) / kWK) * a.B * a.Hkv * ba.nsplit;
   if (dq_blocks > 0x7fffffffL || kv_blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "wide backward: grid too large");
   const dim3 blk(kThreads);
-#define PJX_DQ(BI, EX) hipLaunchKernelGGL((wide_bwd_dq_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)dq_blocks), blk, 0, s, ba)
+#define PJX_DQ(BI, EX) launch_kernel<wide_bwd_dq_kernel<E, D, DV, SHARED, BI, EX>>(dim3((unsigned)dq_blocks), blk, 0, s, ba)
   if (ext) {
     if (db) PJX_DQ(2, 2); else if (hb) PJX_DQ(1, 2); else PJX_DQ(0, 2);
   } else {
@@ -930,13 +930,13 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who, bool 
   int rc = check_launch(who);
   if (rc != PJX_OK || dq_only) return rc;
   if (kv_blocks > 0) {
-#define PJX_KV(BI, EX) hipLaunchKernelGGL((wide_bwd_dkdv_kernel<E, D, DV, SHARED, BI, EX>), dim3((unsigned)kv_blocks), blk, 0, s, ba)
+#define PJX_KV(BI, EX) launch_kernel<wide_bwd_dkdv_kernel<E, D, DV, SHARED, BI, EX>>(dim3((unsigned)kv_blocks), blk, 0, s, ba)
     if (ext) {
       if (hb) PJX_KV(true, 2); else PJX_KV(false, 2);
     } else if (hb) {
       PJX_KV(true, 0);
     } else {
-      hipLaunchKernelGGL((wide_bwd_dc_kernel<E, D, DV, SHARED>), dim3((unsigned)kv_blocks), blk, 0, s, ba);
+      launch_kernel<wide_bwd_dc_kernel<E, D, DV, SHARED>>(dim3((unsigned)kv_blocks), blk, 0, s, ba);
     }
 #undef PJX_KV
     rc = check_launch(who);
@@ -944,11 +944,11 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who, bool 
   }
   if (ba.nsplit > 1) {
     const size_t nk = (size_t)a.B * a.Lk * a.Hkv * D;
-    hipLaunchKernelGGL(wide_bwd_reduce_kernel<E>, dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
+    launch_kernel<wide_bwd_reduce_kernel<E>>(dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
                        (const float*)ba.part, ba.nsplit, nk, (uint16_t*)ba.dk);
     if constexpr (!SHARED) {
       const size_t nv = (size_t)a.B * a.Lk * a.Hkv * DV;
-      hipLaunchKernelGGL(wide_bwd_reduce_kernel<E>, dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
+      launch_kernel<wide_bwd_reduce_kernel<E>>(dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
                          (const float*)(ba.part + (size_t)ba.nsplit * nk), ba.nsplit, nv, (uint16_t*)ba.dv);
     }
     rc = check_launch(who);

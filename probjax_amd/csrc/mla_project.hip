@@ -389,19 +389,19 @@ extern "C" int pjx_mla_project(int dtype, const void* cache, const void* wk, con
     const dim3 grid((unsigned)gx, 2 * a.ny);
     if (dtype == PJX_DTYPE_F16) {
       if (ring)
-        hipLaunchKernelGGL(mla_project_bf16_kernel<F16Fmt>, grid, dim3(256), 0, s, a);
+        launch_kernel<mla_project_bf16_kernel<F16Fmt>>(grid, dim3(256), 0, s, a);
       else
-        hipLaunchKernelGGL(mla_project_bf16_ragged_kernel<F16Fmt>, grid, dim3(256), 0, s, a);
+        launch_kernel<mla_project_bf16_ragged_kernel<F16Fmt>>(grid, dim3(256), 0, s, a);
     } else if (ring) {
-      hipLaunchKernelGGL(mla_project_bf16_kernel<Bf16Fmt>, grid, dim3(256), 0, s, a);
+      launch_kernel<mla_project_bf16_kernel<Bf16Fmt>>(grid, dim3(256), 0, s, a);
     } else {
-      hipLaunchKernelGGL(mla_project_bf16_ragged_kernel<Bf16Fmt>, grid, dim3(256), 0, s, a);
+      launch_kernel<mla_project_bf16_ragged_kernel<Bf16Fmt>>(grid, dim3(256), 0, s, a);
     }
   } else {
     a.ny = (ncols + kFN - 1) / kFN;
     const int64_t gx = (M + kFM - 1) / kFM;
     if (gx > 0x7fffffff) return fail(PJX_ERR_INVALID, "pjx_mla_project: sizes out of range");
-    hipLaunchKernelGGL(mla_project_f32_kernel, dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
+    launch_kernel<mla_project_f32_kernel>(dim3((unsigned)gx, 2 * a.ny), dim3(256), 0, s, a);
   }
   return check_launch("pjx_mla_project");
 }

@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <string>
+#include <typeinfo>
 
 #include "../../include/probjax_hip.h"
 
@@ -12,6 +14,27 @@ namespace pjx {
 
 void set_error(const char* msg);
 void clear_error();
+
+// The launch log behind pjx_last_launches(): clear_error() empties it, and
+// every kernel launch appends the instance's name (kernel_name<K>()).
+void note_launch(const char* name);
+std::string demangled_kernel_name(const char* mangled);
+template <auto K>
+struct KernelTag {};
+// "kernel<template args>" of the kernel instance K, e.g.
+// "flash_fwd_bf16_pipe_kernel<Bf16Fmt, 128, 32, 3, 1>".
+template <auto K>
+const char* kernel_name() {
+  static const std::string name = demangled_kernel_name(typeid(KernelTag<K>).name());
+  return name.c_str();
+}
+
+// Notes and enqueues one launch of kernel instance K.
+template <auto K, typename... Args>
+inline void launch_kernel(dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+  note_launch(kernel_name<K>());
+  hipLaunchKernelGGL(K, grid, block, lds, stream, args...);
+}
 
 inline int fail(int code, const char* msg) {
   set_error(msg);

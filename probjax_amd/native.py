@@ -49,6 +49,7 @@ _MODS = ctypes.POINTER(ScoreMods)
 _SIGNATURES = {
     "pjx_version": (ctypes.c_int, []),
     "pjx_last_error": (ctypes.c_char_p, []),
+    "pjx_last_launches": (ctypes.c_char_p, []),
     "pjx_flash_fwd": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64,
@@ -131,3 +132,10 @@ def check(rc: int) -> None:
         if rc == 1:
             raise ValueError(msg)
         raise NativeLibraryError(f"error {rc}: {msg}")
+
+
+def last_launches() -> list:
+    """Kernel instances (``"name<template args>"``) that the calling thread's
+    last entry-point call launched, in order (``pjx_last_launches``)."""
+    s = load().pjx_last_launches().decode(errors="replace")
+    return s.split(";") if s else []

@@ -152,3 +152,12 @@ def test_workspace_size_formula(lib):
     n = lib.pjx_decode_workspace_size(2, 8, 4, 1000, 128, 256)
     chunks = -(-1000 // 256)
     assert n == 2 * 8 * chunks * 4 * (128 + 2) * 4
+
+
+def test_launch_log_empty_after_refused_call(lib):
+    """A call refused before any launch leaves an empty launch log (the log
+    of a call lists the kernel instances it launched, in order)."""
+    rc = lib.pjx_flash_fwd(*_flash_args(D=96))
+    assert rc != native.PJX_OK
+    assert lib.pjx_last_launches() == b""
+    assert native.last_launches() == []
