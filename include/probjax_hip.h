@@ -209,22 +209,25 @@ size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
  * routes to the regular forward (kernels/attention.py:2672-2675).
  *
  * dtype PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 (full fp32 products) for q, k, v, o:
- * q [B, Lq, Hq, D]; k, v [B, Lk, Hkv, D] (Lk = KV capacity);
- * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, D];
+ * q [B, Lq, Hq, D]; k [B, Lk, Hkv, D], v [B, Lk, Hkv, Dv] (Lk = KV capacity;
+ * D = head_dim, Dv = v_dim, each 64, 128 or 256: the reference takes any D
+ * and Dv, padded to the next power of two, attention_splitkv.py:155-172);
+ * kv_lengths int32 [B] (NULL = all Lk valid); o [B, Lq, Hq, Dv];
  * lse optional fp32 [B, Hq, Lq], natural log (attention_splitkv.py:248-250).
  * The (Hq/Hkv)*Lq query rows of a KV head are packed row = g*Lq + t
- * (attention_splitkv.py:121-126); at most 64 rows per KV head in bf16 / fp16 (the
- * reference packs up to 64, :155-170), 32 in fp32.
- * Only keys < kv_lengths[b] are read.  head_dim == 128.
+ * (attention_splitkv.py:121-126), any number of them: up to 64 rows share one
+ * pass over the keys (32 in fp32 or at D or Dv 256), more run as several row
+ * groups, each streaming the keys (the reference's row blocks, :160-161).
+ * Only keys < kv_lengths[b] are read.
  * chunk: keys per work item (0 = automatic: a power of two in [128, 2048]
- *   leaving about 2048 items at full capacity; else a multiple of 128).
- * workspace: at least pjx_decode_workspace_size(B, Hkv, rows, Lk, D, chunk) bytes.
+ *   leaving about 1024 items at full capacity; else a multiple of 128).
+ * workspace: at least pjx_decode_workspace_size(B, Hkv, rows, Lk, Dv, chunk) bytes.
  */
 int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
                        const int32_t* kv_lengths, void* o, float* lse, void* workspace,
                        size_t workspace_bytes, int64_t batch, int64_t q_len,
                        int64_t kv_len, int64_t q_heads, int64_t kv_heads,
-                       int64_t head_dim, float sm_scale, int64_t chunk, void* stream);
+                       int64_t head_dim, int64_t v_dim, float sm_scale, int64_t chunk, void* stream);
 
 /*
  * Size of the library-held device array behind pjx_splitkv_decode_static:
@@ -238,16 +241,17 @@ int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
  * nothing is allocated.  No counterpart in the reference: an extra entry for
  * callers that cannot allocate (code under HIP graph capture, serving loops,
  * harnesses that forbid hipMalloc).  Arguments, results and errors as
- * pjx_splitkv_decode; sizes whose partials
- * (pjx_decode_workspace_size(batch, kv_heads, rows, kv_len, head_dim, chunk))
- * exceed the array are rejected with PJX_ERR_WORKSPACE.  Every call on one GPU
+ * pjx_splitkv_decode (every argument is checked first); sizes whose partials
+ * (pjx_decode_workspace_size(batch, kv_heads, rows, kv_len, v_dim, chunk))
+ * exceed the array are then rejected with PJX_ERR_WORKSPACE.  Every call on one GPU
  * shares that GPU's array: calls that overlap on one GPU (concurrent streams
  * or threads) race and must be serialised by the caller.
  */
 int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const void* v,
                               const int32_t* kv_lengths, void* o, float* lse, int64_t batch,
                               int64_t q_len, int64_t kv_len, int64_t q_heads, int64_t kv_heads,
-                              int64_t head_dim, float sm_scale, int64_t chunk, void* stream);
+                              int64_t head_dim, int64_t v_dim, float sm_scale, int64_t chunk,
+                              void* stream);
 
 /*
  * Latent (MLA) attention decode, absorbed form K = V = cache.  Replaces the
@@ -259,7 +263,9 @@ int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const voi
  * kv_lengths int32 [B] or NULL;
  * o [B, Lq, H, v_dim] of dtype = the first v_dim columns of mla(q, cache, None,
  * None) (v_dim == R gives the API-exact output); lse optional fp32 [B, H, Lq].
- * Lq*H <= 16.  R a multiple of 64, R <= 576; v_dim a multiple of 64, <= R.
+ * (rank, v_dim) in {(576, 512), (576, 576), (512, 512), (128, 128)}.  Any
+ * Lq*H: each 16 folded rows form a row group that streams the cache chunk by
+ * chunk (the reference's mla takes any head count, latent_attention.py:636-766).
  * chunk: keys per work item (0 = automatic, as for pjx_splitkv_decode; else a
  *   multiple of 64).
  * workspace: at least pjx_decode_workspace_size(B, 1, Lq*H, S, v_dim, chunk)

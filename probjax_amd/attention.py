@@ -51,11 +51,13 @@ HALF_DTYPES = (torch.bfloat16, torch.float16)  # the 16-bit (MFMA bf16 / fp16) k
 KERNEL_DTYPES = HALF_DTYPES + (torch.float32,)  # dtypes the kernels take
 FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 / float16 only
 FLASH_HEAD_DIMS_F32 = (64, 128)
-DECODE_HEAD_DIMS = (64, 128)
+DECODE_HEAD_DIMS = (64, 128, 256)  # head dims (q/k and v each) of the split-KV decode
 LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (16-bit)
-DECODE_MAX_ROWS = 64       # (Hq/Hkv)*Lq rows per KV head of the 16-bit split-KV decode
-DECODE_MAX_ROWS_F32 = 32   # ... of the fp32 split-KV decode
-MLA_DECODE_MAX_ROWS = 16   # Lq*H folded rows of the latent decode
+# Lq*H folded rows up to which an absorbed decode step takes the split-KV latent
+# kernel: each 16 rows form a row group that streams the cache, so up to 8
+# passes over it; longer query blocks run the latent flash kernels, whose
+# 128-row query tiles read it once per tile.
+MLA_DECODE_MAX_ROWS = 128
 MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
 BACKWARD_DTYPES = KERNEL_DTYPES  # dtypes pjx_flash_bwd takes
 
@@ -129,16 +131,9 @@ def _decode_plan(query, key, value, lm: LoweredMask, lb: LoweredBias | None):
         return None
     if query.dtype not in KERNEL_DTYPES:
         return None
-    B, l_q, h_q, d = query.shape
-    h_kv = key.shape[2]
-    if d not in DECODE_HEAD_DIMS or (h_q // h_kv) * l_q > _decode_max_rows(query.dtype):
+    if query.shape[-1] not in DECODE_HEAD_DIMS or value.shape[-1] not in DECODE_HEAD_DIMS:
         return None
     return dict(kv_lengths=lm.kv_lengths)
-
-
-def _decode_max_rows(dtype) -> int:
-    """Packed query rows per KV head the split-KV decode takes in ``dtype``."""
-    return DECODE_MAX_ROWS if dtype in HALF_DTYPES else DECODE_MAX_ROWS_F32
 
 
 def _int_tensor(x, shape, device):
@@ -290,8 +285,7 @@ def _splitkv_ok(q, k, lm: LoweredMask | None, has_bias: bool, dropout_rate: floa
         return False
     if q.dtype not in KERNEL_DTYPES or _decode_width(q.shape[-1]) is None:
         return False
-    if k.shape[2] <= 0 or q.shape[2] % k.shape[2] or \
-            (q.shape[2] // k.shape[2]) * q.shape[1] > _decode_max_rows(q.dtype):
+    if k.shape[2] <= 0 or q.shape[2] % k.shape[2]:
         return False
     if split_kv:
         return True
@@ -307,8 +301,9 @@ def use_splitkv(q, k, *, mask=None, bias=None, dropout_rate: float = 0.0,
     forces it when exact; ``None`` picks it for ``Lq <= 64`` and
     ``Lkv >= 1024``.  The HIP decode is also exact with a ``KVLenMask`` (keys
     past each length are skipped), so a length mask does not disable it here;
-    it needs bf16, head_dim <= 128 (zero-padded to 64 or 128) and
-    ``(Hq/Hkv)*Lq <= 16``.
+    it takes bf16, fp16 and fp32, head_dim <= 256 (zero-padded to 64, 128 or
+    256) and any number of packed rows ``(Hq/Hkv)*Lq`` (up to 64 per pass over
+    the keys, as the reference's row blocks, attention_splitkv.py:155-172).
     """
     lm = lower_mask(mask)
     if lm is not None and lm.row_kv_lengths is not None and getattr(q, "ndim", 0) == 4 and q.shape[1] == 1:
@@ -495,8 +490,11 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
                     block_k: int = 64, return_lse: bool = False, kv_lengths=None,
                     **unused_tuning):
     """Split-KV ("flash-decoding") forward (probjax ``splitkv_forward``,
-    kernels/attention_splitkv.py:137-250): ``q [B, Lq, Hq, D]`` bf16,
-    ``k/v [B, Lkv, Hkv, D]``; ``(Hq/Hkv)*Lq <= 16``.
+    kernels/attention_splitkv.py:137-250): bf16 / fp16 / fp32
+    ``q [B, Lq, Hq, D]``, ``k [B, Lkv, Hkv, D]``, ``v [B, Lkv, Hkv, Dv]``
+    -> ``[B, Lq, Hq, Dv]``; D and Dv up to 256 (zero-padded to 64, 128 or
+    256, as the reference pads its blocks to the next power of two,
+    :155-172), any number of packed rows ``(Hq/Hkv)*Lq``.
 
     ``num_splits`` maps to KV chunks of ``ceil(Lkv / num_splits)`` keys rounded
     up to 128 (``None``: the kernel's own choice).  ``kv_lengths`` ([B]) is the
@@ -505,10 +503,14 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
     """
     del block_k, unused_tuning
     _gqa_group(q.shape[-2], k.shape[-2])
-    d = q.shape[-1]
-    width = _decode_width(d)
-    if width is not None and width != d:
-        q, k, v = (_pad_features(x, width) for x in (q, k, v))
+    d, dv = q.shape[-1], v.shape[-1]
+    width, v_width = _decode_width(d), _decode_width(dv)
+    if width is None or v_width is None:
+        raise ValueError(f"splitkv_forward: head dims up to {DECODE_HEAD_DIMS[-1]}, got D={d}, Dv={dv}")
+    if width != d:
+        q, k = _pad_features(q, width), _pad_features(k, width)
+    if v_width != dv:
+        v = _pad_features(v, v_width)
     chunk = 0
     if num_splits is not None:
         if num_splits < 1:
@@ -517,9 +519,9 @@ def splitkv_forward(q, k, v, *, sm_scale: float, num_splits: int | None = None,
         chunk = max(128, -(-per // 128) * 128)
     res = hip.splitkv_decode(q, k, v, sm_scale=float(sm_scale), kv_lengths=kv_lengths,
                              chunk=chunk, return_lse=return_lse)
-    if width == d or width is None:
+    if v_width == dv:
         return res
-    return (res[0][..., :d], res[1]) if return_lse else res[..., :d]
+    return (res[0][..., :dv], res[1]) if return_lse else res[..., :dv]
 
 
 class _MaterializedMLAFunction(torch.autograd.Function):
@@ -666,7 +668,7 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     needs), any query length, every mask and bias of the flash route,
     differentiable in ``q`` and ``cache`` (bias data gets no gradient, as in
     the reference's VJP); latent widths up to 576 in bfloat16 / float16 (up to 128 in
-    float32).  Decode steps (``Q * H <= 16``, no gradient, no bias,
+    float32).  Decode steps (``Q * H <= 128``, no gradient, no bias,
     ``None`` / ``KVLenMask``) run the split-KV latent kernel; the rest the
     latent flash kernels, whose heads share one K = V head (the folded
     ``[B, Q*H, 1, R]`` form of the reference layer is the same call with
@@ -680,7 +682,7 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     to 128.  Decode-shaped calls that probjax's FLOP rule (:616-620) finds
     cheaper absorbed run absorbed on the latent decode kernel (no gradient
     needed, bf16, no bias, ``None`` / ``KVLenMask`` / one-row
-    ``KeyPaddingMask``, rank 128 / 512 / 576, ``Lq * H <= 16``); the rest
+    ``KeyPaddingMask``, rank 128 / 512 / 576, ``Lq * H <= 128``); the rest
     materialise.  Dropout raises ``ValueError``.
     """
     del rng, unused_tuning
@@ -732,7 +734,7 @@ def _latent_decode_lengths(q, cache, mask, bias, dv):
     """Per-batch KV lengths ("all" for none) when an absorbed call is a decode
     step the split-KV latent kernel computes exactly (no gradient, no bias,
     ``None`` / ``KVLenMask`` / one-row ``KeyPaddingMask``, bf16 / fp16, a rank and
-    output width it carries, ``Lq * H <= 16``); else None."""
+    output width it carries, ``Lq * H <= 128``); else None."""
     B, l_q, H, R = q.shape
     if bias is not None or _needs_grad(q, cache):
         return None
@@ -965,6 +967,12 @@ def _fold_low_rank(query, key, value, terms, sm_scale: float):
     return query, key, value, out_dim
 
 
+# probjax's fused route of dot_product_attention (layers/attention.py:1161-1164):
+# position-only masks and at least this many keys; other calls take Flax's einsum.
+_FUSED_MASKS = ("NoMask", "CausalMask", "LocalWindowMask", "CausalLocalWindowMask")
+_FUSED_MIN_KV_LEN = 64
+
+
 def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=None,
                           dropout_rate: float = 0.0, broadcast_dropout: bool = False,
                           deterministic=True, dtype=None, precision=None, module=None,
@@ -982,18 +990,23 @@ def dot_product_attention(query, key, value, mask=None, bias=None, dropout_rng=N
     layers/attention.py:1298-1319).
 
     Rows whose keys the mask drops entirely follow the reference's two
-    paths: with a bias (array or object) or an array mask, probjax computes
-    the call with Flax's einsum over ``mask.dense()`` (``bias is not None``
-    disables its fused route, layers/attention.py:1173, and the device routes
-    refuse a bias, attention_device.py:128), whose masking by the dtype's most
-    negative value gives such a row equal weights over every key: the mean of
-    V.  Without a bias the fused kernel's zeros stand, as in ``flex_attention``.
+    paths.  probjax takes its fused kernel only for no mask or a
+    position-only mask (``NoMask``, ``CausalMask``, ``LocalWindowMask``,
+    ``CausalLocalWindowMask``), no bias, no ``module`` / ``precision`` and at
+    least 64 keys (``_use_fused_gpu_attention``, layers/attention.py:1161-1202;
+    the device routes refuse a bias, attention_device.py:128); every other
+    call runs Flax's einsum over ``mask.dense()``, whose masking by the
+    dtype's most negative value gives such a row equal weights over every key:
+    the mean of V.  On the fused route the kernel's zeros stand, as in
+    ``flex_attention``.
     """
     if implementation not in (None, "hip"):
         raise ValueError(f"implementation must be None or 'hip', got {implementation!r}")
     batch_shape = tuple(query.shape[:-3])
     flat = [x.reshape((-1,) + tuple(x.shape[-3:])) for x in (query, key, value)]
-    flax_path = bias is not None or isinstance(mask, torch.Tensor)
+    flax_path = (bias is not None or isinstance(mask, torch.Tensor) or module is not None
+                 or precision is not None or key.shape[-3] < _FUSED_MIN_KV_LEN
+                 or (mask is not None and type(mask).__name__ not in _FUSED_MASKS))
     if isinstance(mask, torch.Tensor) or isinstance(bias, torch.Tensor):
         mask, bias = _flax_arrays(mask, bias, batch_shape, flat[0], flat[1])
     out = flex_attention(*flat, mask=mask, bias=bias, dropout_rng=dropout_rng,

@@ -50,8 +50,12 @@ struct DecodeArgs {
   int B, Lq, Lk, Hq, G, rows;
   int fold;      // 1: row = t*H + h (MLA); 0: row = gi*Lq + t (GQA)
   int chunk, nch;
-  int dv;        // output dims (<= D)
+  int dv;        // output dims
   float cx;      // sm_scale * log2(e)
+  // Query rows per row group: the rows of a KV head are split into groups of
+  // `rpg` (16 per MFMA column block of the kernel), one per blockIdx.y; each
+  // group's workgroups stream the same keys.
+  int rpg;
 };
 
 __device__ __forceinline__ void row_to_head(const DecodeArgs& a, int g, int r, int& t, int& h) {
@@ -230,11 +234,12 @@ __device__ __forceinline__ void emit_row_quad(const DecodeArgs& a, int b, int g,
 // ---------------------------------------------------------------------------
 
 // Combines the 4 waves' (max, sum, O^T) of row block rb through LDS scratch
-// red (>= 4 x 16 x D floats + 4 x 16 x 2) and emits rows 16rb .. of the item.
-// acc[i] holds O^T[dim 16i + 4*q4 + r][row 16rb + c16].
+// red (>= 4 x 16 x D floats + 4 x 16 x 2) and emits rows row0 + 16rb .. of the
+// item (D = the output dims).  acc[i] holds O^T[dim 16i + 4*q4 + r][row
+// row0 + 16rb + c16].
 template <int D>
 __device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, const f32x4* acc,
-                                             float m_run, float l_run, int rb, int b, int g,
+                                             float m_run, float l_run, int row0, int rb, int b, int g,
                                              size_t part, bool final_out) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
@@ -249,7 +254,7 @@ __device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, co
     red_ml[(w * 16 + c16) * 2 + 1] = l_run;
   }
   __syncthreads();
-  const int nr = min(16, a.rows - 16 * rb);
+  const int nr = min(16, a.rows - row0 - 16 * rb);
   for (int e = tid; e < nr * D; e += 256) {
     const int r = e / D, d = e % D;
     float M = kMaxInit;
@@ -262,23 +267,25 @@ __device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, co
       Ls = fmaf(wt, red_ml[(ww * 16 + r) * 2 + 1], Ls);
       O = fmaf(wt, red_o[(ww * 16 + r) * D + d], O);
     }
-    emit_row_elem(a, b, g, 16 * rb + r, d, part, final_out, M, Ls, O);
+    emit_row_elem(a, b, g, row0 + 16 * rb + r, d, part, final_out, M, Ls, O);
   }
 }
 
-template <int NRB>
-constexpr int decode_occupancy() { return NRB == 4 ? 1 : 2; }
+// Two workgroups per CU where the registers allow it: 16- or 32-row groups at
+// head dims up to 128.
+template <int D, int DV, int NRB>
+constexpr int decode_occupancy() { return (NRB == 4 || D > 128 || DV > 128) ? 1 : 2; }
 
-template <typename E, int D, int NRB>
-__global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kernel(DecodeArgs a) {
+template <typename E, int D, int DV, int NRB>
+__global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int KSTEPS = D / 32;  // 32-dim MFMA k-steps of Q.K
-  constexpr int NDB = D / 16;     // 16-dim output blocks
-  constexpr int DC = D / 8;       // 16-byte chunks per row
-  constexpr int VU = D / 64;      // (4 keys x 8 dims) V units per lane per 32 keys
+  constexpr int NDB = DV / 16;    // 16-dim output blocks
+  constexpr int DC = DV / 8;      // 16-byte chunks per V row
+  constexpr int VU = DV / 64;     // (4 keys x 8 dims) V units per lane per 32 keys
   constexpr int VTS = 36;         // V^T row stride (16-bit elements): 32 keys + 4 pad
-  static_assert(D % 64 == 0, "head dim");
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[4 * D * VTS];
-  static_assert(4 * D * VTS * 2 >= 4 * 16 * D * 4 + 4 * 16 * 2 * 4, "combine scratch fits");
+  static_assert(D % 64 == 0 && DV % 64 == 0, "head dims");
+  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[4 * DV * VTS];
+  static_assert(4 * DV * VTS * 2 >= 4 * 16 * DV * 4 + 4 * 16 * 2 * 4, "combine scratch fits");
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
@@ -294,10 +301,11 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
   const int w0 = c0 + w * per_wave;
   const int w1 = min(w0 + per_wave, L);
 
+  const int row0 = blockIdx.y * 16 * NRB;  // this row group's first row
   typename E::v8 qf[NRB][KSTEPS];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
-    const int row = 16 * rb + c16;
+    const int row = row0 + 16 * rb + c16;
     const bool rv = row < a.rows;
     int t = 0, h = 0;
     if (rv) row_to_head(a, g, row, t, h);
@@ -309,10 +317,10 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
       qf[rb][s] = E::as8(r);
     }
   }
-  const size_t kv_tok = (size_t)a.G * D;
+  const size_t k_tok = (size_t)a.G * D, v_tok = (size_t)a.G * DV;
   const uint16_t* Kb = a.k + ((size_t)b * a.Lk * a.G + g) * D;
-  const uint16_t* Vb = a.v + ((size_t)b * a.Lk * a.G + g) * D;
-  uint16_t* vl = vt_lds + w * D * VTS;
+  const uint16_t* Vb = a.v + ((size_t)b * a.Lk * a.G + g) * DV;
+  uint16_t* vl = vt_lds + w * DV * VTS;
 
   f32x4 acc[NRB][NDB];
 #pragma unroll
@@ -333,7 +341,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
     for (int kb = 0; kb < 2; ++kb) {
       const int key = k0 + 16 * kb + c16;
       const bool ok = key < w1;
-      const uint16_t* p = Kb + (size_t)(ok ? key : 0) * kv_tok + 8 * q4;
+      const uint16_t* p = Kb + (size_t)(ok ? key : 0) * k_tok + 8 * q4;
 #pragma unroll
       for (int s = 0; s < KSTEPS; ++s) {
         u32x4 r = {0u, 0u, 0u, 0u};
@@ -351,7 +359,7 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
       for (int j = 0; j < 4; ++j) {
         const int key = k0 + 4 * kq + j;
         u32x4 r = {0u, 0u, 0u, 0u};
-        if (key < w1) r = *(const u32x4*)(Vb + (size_t)key * kv_tok + 8 * dc);
+        if (key < w1) r = *(const u32x4*)(Vb + (size_t)key * v_tok + 8 * dc);
         vr[i][j] = r;
       }
     }
@@ -457,8 +465,8 @@ __global__ __launch_bounds__(256, decode_occupancy<NRB>()) void gqa_decode_kerne
   const size_t part = (size_t)bg * a.nch + chunk_id;
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb)
-    combine_rows<D>(a, (float*)vt_lds, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), rb, b, g,
-                    part, final_out);
+    combine_rows<DV>(a, (float*)vt_lds, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), row0, rb, b, g,
+                     part, final_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -476,12 +484,12 @@ __device__ __forceinline__ f32x4 mfma16x16x4f32(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int D, int NRB>
+template <int D, int DV, int NRB>
 __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
-  constexpr int NJ = D / 16;   // float4 groups of Q.K per lane
-  constexpr int NDB = D / 16;  // 16-dim output blocks
-  static_assert(D % 64 == 0 && NRB <= 2, "fp32 decode shape");
-  __shared__ __attribute__((aligned(16))) float red[4 * 16 * D + 4 * 16 * 2];
+  constexpr int NJ = D / 16;    // float4 groups of Q.K per lane
+  constexpr int NDB = DV / 16;  // 16-dim output blocks
+  static_assert(D % 64 == 0 && DV % 64 == 0 && NRB <= 2, "fp32 decode shape");
+  __shared__ __attribute__((aligned(16))) float red[4 * 16 * DV + 4 * 16 * 2];
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
@@ -494,14 +502,15 @@ __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
   const int w0 = c0 + w * per_wave;
   const int w1 = min(w0 + per_wave, L);
   const float* Q = (const float*)a.q;
-  const size_t kv_tok = (size_t)a.G * D;
+  const size_t k_tok = (size_t)a.G * D, v_tok = (size_t)a.G * DV;
   const float* Kb = (const float*)a.k + ((size_t)b * a.Lk * a.G + g) * D;
-  const float* Vb = (const float*)a.v + ((size_t)b * a.Lk * a.G + g) * D;
+  const float* Vb = (const float*)a.v + ((size_t)b * a.Lk * a.G + g) * DV;
+  const int row0 = blockIdx.y * 16 * NRB;  // this row group's first row
 
   f32x4 qf[NRB][NJ];
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb) {
-    const int row = 16 * rb + c16;
+    const int row = row0 + 16 * rb + c16;
     const bool rv = row < a.rows;
     int t = 0, h = 0;
     if (rv) row_to_head(a, g, row, t, h);
@@ -528,7 +537,7 @@ __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
     for (int kb = 0; kb < 2; ++kb) {
       const int key = k0 + 16 * kb + c16;
       const bool ok = key < w1;
-      const float* kp = Kb + (size_t)(ok ? key : 0) * kv_tok + 4 * q4;
+      const float* kp = Kb + (size_t)(ok ? key : 0) * k_tok + 4 * q4;
       f32x4 kf[NJ];
 #pragma unroll
       for (int j = 0; j < NJ; ++j) kf[j] = ok ? *(const f32x4*)(kp + 16 * j) : f32x4{};
@@ -549,7 +558,7 @@ __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
       for (int e = 0; e < 4; ++e) {
         const int key = k0 + 16 * kb + 4 * q4 + e;
         const bool ok = key < w1;
-        const float* vp = Vb + (size_t)(ok ? key : 0) * kv_tok + c16;
+        const float* vp = Vb + (size_t)(ok ? key : 0) * v_tok + c16;
 #pragma unroll
         for (int i = 0; i < NDB; ++i) vv[kb][e][i] = ok ? vp[16 * i] : 0.f;
       }
@@ -598,7 +607,8 @@ __global__ __launch_bounds__(256, 1) void gqa_decode_f32_kernel(DecodeArgs a) {
   const size_t part = (size_t)bg * a.nch + chunk_id;
 #pragma unroll
   for (int rb = 0; rb < NRB; ++rb)
-    combine_rows<D>(a, red, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), rb, b, g, part, final_out);
+    combine_rows<DV>(a, red, acc[rb], m_run[rb], xor32_sum(xor16_sum(l_run[rb])), row0, rb, b, g, part,
+                     final_out);
 }
 
 // ---------------------------------------------------------------------------
@@ -670,12 +680,14 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
   const int c1 = min(c0 + a.chunk, L);
   const int n_tiles = (c1 - c0 + BK - 1) / BK;
 
-  // Q^T as the B operand: lane holds query row c16, dims 32*s + 8*q4 + [0,8).
+  // Q^T as the B operand: lane holds query row row0 + c16 (16 rows per row
+  // group, blockIdx.y), dims 32*s + 8*q4 + [0,8).
+  const int row = blockIdx.y * 16 + c16;
   typename E::v8 qf[KSTEPS];
   {
-    const bool rv = c16 < a.rows;
+    const bool rv = row < a.rows;
     int t = 0, h = 0;
-    if (rv) row_to_head(a, 0, c16, t, h);
+    if (rv) row_to_head(a, 0, row, t, h);
     const uint16_t* qrow = a.q + ((size_t)(b * a.Lq + t) * a.Hq + h) * D;
 #pragma unroll
     for (int s = 0; s < KSTEPS; ++s) {
@@ -824,12 +836,12 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
   // no combine across waves.
   l_run = xor16_sum(l_run);
   l_run = xor32_sum(l_run);
-  if (c16 < a.rows) {
+  if (row < a.rows) {
     const size_t part = (size_t)b * a.nch + chunk_id;
     const bool final_out = c0 == 0 && L <= a.chunk;
 #pragma unroll
     for (int i = 0; i < NDW; ++i)
-      emit_row_quad(a, b, 0, c16, 16 * (NDW * w + i) + 4 * q4, part, final_out, m_run, l_run, acc[i]);
+      emit_row_quad(a, b, 0, row, 16 * (NDW * w + i) + 4 * q4, part, final_out, m_run, l_run, acc[i]);
   }
 }
 
@@ -961,9 +973,10 @@ static int run_decode(DecodeArgs& a, void* workspace, size_t ws_bytes,
   a.ws_o = (float*)workspace;
   a.ws_ml = a.ws_o + parts * a.dv;
   const long blocks = (long)a.B * a.G * a.nch;
-  if (blocks > 0x7fffffffL || (long)a.B * a.G * a.rows > 0x7fffffffL)
+  const long groups = ((long)a.rows + a.rpg - 1) / a.rpg;
+  if (blocks > 0x7fffffffL || groups > 65535 || (long)a.B * a.G * a.rows > 0x7fffffffL)
     return fail(PJX_ERR_INVALID, "decode: grid too large");
-  launch_kernel<K>(dim3((unsigned)blocks), dim3(kDecThreads), 0, stream, a);
+  launch_kernel<K>(dim3((unsigned)blocks, (unsigned)groups), dim3(kDecThreads), 0, stream, a);
   int rc = check_launch(name);
   if (rc) return rc;
   const long merge_threads = (long)a.B * a.G * a.rows * (a.dv / 4);
@@ -972,18 +985,45 @@ static int run_decode(DecodeArgs& a, void* workspace, size_t ws_bytes,
   return check_launch(name);
 }
 
-// The 16-bit GQA decode (format E) with nrb 16-row blocks.
-template <typename E>
-static int run_gqa_h16(DecodeArgs& a, int head_dim, int nrb, void* ws, size_t ws_bytes, hipStream_t s,
-                       const char* who) {
-  if (head_dim == 128) {
-    if (nrb == 1) return run_decode<gqa_decode_kernel<E, 128, 1>>(a, ws, ws_bytes, s, who);
-    if (nrb == 2) return run_decode<gqa_decode_kernel<E, 128, 2>>(a, ws, ws_bytes, s, who);
-    return run_decode<gqa_decode_kernel<E, 128, 4>>(a, ws, ws_bytes, s, who);
+// 16-row MFMA column blocks per row group of a GQA decode launch: up to 4 (64
+// rows, the reference's largest packed tile, attention_splitkv.py:155-170) at
+// head dims <= 128 in bf16 / fp16, else 2; more rows run as several row groups.
+static int gqa_row_blocks(int64_t rows, int64_t head_dim, int64_t v_dim, bool f32) {
+  const int64_t max_nrb = (f32 || head_dim > 128 || v_dim > 128) ? 2 : 4;
+  const int64_t need = std::min<int64_t>((rows + kRows - 1) / kRows, max_nrb);
+  return need <= 1 ? 1 : need <= 2 ? 2 : 4;
+}
+
+// One (D, DV) pair of the 16-bit GQA decode with nrb 16-row blocks per row group.
+template <typename E, int D, int DV>
+static int run_gqa_dims(DecodeArgs& a, int nrb, void* ws, size_t ws_bytes, hipStream_t s, const char* who) {
+  if (nrb == 1) return run_decode<gqa_decode_kernel<E, D, DV, 1>>(a, ws, ws_bytes, s, who);
+  if (nrb == 2) return run_decode<gqa_decode_kernel<E, D, DV, 2>>(a, ws, ws_bytes, s, who);
+  if constexpr (D <= 128 && DV <= 128) return run_decode<gqa_decode_kernel<E, D, DV, 4>>(a, ws, ws_bytes, s, who);
+  return fail(PJX_ERR_INVALID, "decode: row blocks");
+}
+
+template <int D, int DV>
+static int run_gqa_f32_dims(DecodeArgs& a, int nrb, void* ws, size_t ws_bytes, hipStream_t s, const char* who) {
+  return nrb == 1 ? run_decode<gqa_decode_f32_kernel<D, DV, 1>>(a, ws, ws_bytes, s, who)
+                  : run_decode<gqa_decode_f32_kernel<D, DV, 2>>(a, ws, ws_bytes, s, who);
+}
+
+// The GQA decode at (head_dim, v_dim), each in {64, 128, 256}: format E (bf16 /
+// fp16), or fp32 when F32.
+template <typename E, bool F32>
+static int run_gqa(DecodeArgs& a, int head_dim, int v_dim, int nrb, void* ws, size_t ws_bytes, hipStream_t s,
+                   const char* who) {
+#define PJX_GQA_DIMS(D, DV)                                                        \
+  if (head_dim == D && v_dim == DV) {                                              \
+    if constexpr (F32) return run_gqa_f32_dims<D, DV>(a, nrb, ws, ws_bytes, s, who); \
+    else return run_gqa_dims<E, D, DV>(a, nrb, ws, ws_bytes, s, who);              \
   }
-  if (nrb == 1) return run_decode<gqa_decode_kernel<E, 64, 1>>(a, ws, ws_bytes, s, who);
-  if (nrb == 2) return run_decode<gqa_decode_kernel<E, 64, 2>>(a, ws, ws_bytes, s, who);
-  return run_decode<gqa_decode_kernel<E, 64, 4>>(a, ws, ws_bytes, s, who);
+  PJX_GQA_DIMS(64, 64) PJX_GQA_DIMS(64, 128) PJX_GQA_DIMS(64, 256)
+  PJX_GQA_DIMS(128, 64) PJX_GQA_DIMS(128, 128) PJX_GQA_DIMS(128, 256)
+  PJX_GQA_DIMS(256, 64) PJX_GQA_DIMS(256, 128) PJX_GQA_DIMS(256, 256)
+#undef PJX_GQA_DIMS
+  return fail(PJX_ERR_INVALID, "decode: head_dim and v_dim must be 64, 128 or 256");
 }
 
 // The latent decode (format E) at one (rank, v_dim).
@@ -995,6 +1035,32 @@ static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, siz
   if (rank == 512 && v_dim == 512) return run_decode<mla_decode_kernel<E, 512, 512>>(a, ws, ws_bytes, s, who);
   if (rank == 128 && v_dim == 128) return run_decode<mla_decode_kernel<E, 128, 128>>(a, ws, ws_bytes, s, who);
   return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
+}
+
+// Argument checks shared by pjx_splitkv_decode and pjx_splitkv_decode_static
+// (everything but the pointers and the workspace); resolves chunk = 0.
+static int check_gqa_decode(const char* who, int dtype, int64_t batch, int64_t q_len, int64_t kv_len,
+                            int64_t q_heads, int64_t kv_heads, int64_t head_dim, int64_t v_dim,
+                            float sm_scale, int64_t* chunk) {
+  char buf[256];
+  auto bad = [&](const char* what) {
+    snprintf(buf, sizeof(buf), "%s: %s", who, what);
+    return fail(PJX_ERR_INVALID, buf);
+  };
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
+    return bad("dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
+  if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
+    return bad("bad sizes");
+  auto width = [](int64_t d) { return d == 64 || d == 128 || d == 256; };
+  if (!width(head_dim) || !width(v_dim)) return bad("head_dim and v_dim must be 64, 128 or 256");
+  if (!(sm_scale > 0.f)) return bad("sm_scale must be > 0");
+  if (*chunk == 0) *chunk = auto_chunk(batch, kv_heads, kv_len, kGqaItems);
+  if (*chunk < 128 || *chunk % 128) return bad("chunk must be a positive multiple of 128");
+  const int64_t rows = (q_heads / kv_heads) * q_len;
+  if (kv_len > (1 << 30) || batch * kv_len * kv_heads * std::max(head_dim, v_dim) > ((int64_t)1 << 40) ||
+      rows > (1 << 20) || batch * q_heads * q_len * std::max(head_dim, v_dim) > ((int64_t)1 << 40))
+    return bad("sizes out of range");
+  return PJX_OK;
 }
 
 }  // namespace pjx
@@ -1010,30 +1076,21 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
                                   const int32_t* kv_lengths, void* o, float* lse,
                                   void* workspace, size_t workspace_bytes, int64_t batch,
                                   int64_t q_len, int64_t kv_len, int64_t q_heads,
-                                  int64_t kv_heads, int64_t head_dim, float sm_scale,
+                                  int64_t kv_heads, int64_t head_dim, int64_t v_dim, float sm_scale,
                                   int64_t chunk, void* stream) {
   clear_error();
-  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
-    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
-  const bool f32 = dtype == PJX_DTYPE_F32;
+  const char* who = "pjx_splitkv_decode";
+  const int vrc = check_gqa_decode(who, dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, v_dim, sm_scale,
+                                   &chunk);
+  if (vrc != PJX_OK) return vrc;
   // an empty cache (kv_len == 0) may come as null pointers
   if (!q || !o || (batch * kv_len > 0 && (!k || !v))) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: null pointer");
-  if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
-    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: bad sizes");
-  if (head_dim != 128 && head_dim != 64) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: head_dim must be 64 or 128");
-  const int64_t rows = (q_heads / kv_heads) * q_len;
-  if (rows > (f32 ? 2 : 4) * kRows)
-    return fail(PJX_ERR_INVALID, f32 ? "pjx_splitkv_decode: (Hq/Hkv)*Lq must be <= 32 in fp32"
-                                     : "pjx_splitkv_decode: (Hq/Hkv)*Lq must be <= 64");
-  if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: sm_scale must be > 0");
-  if (chunk == 0) chunk = auto_chunk(batch, kv_heads, kv_len, kGqaItems);
-  if (chunk < 128 || chunk % 128) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: chunk must be a positive multiple of 128");
-  if (kv_len > (1 << 30) || batch * kv_len * kv_heads * head_dim > ((int64_t)1 << 40))
-    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode: sizes out of range");
+  const bool f32 = dtype == PJX_DTYPE_F32;
   if (batch == 0) return PJX_OK;
   if (kv_len == 0)
-    return write_keyless(o, lse, (size_t)(batch * q_len * q_heads * head_dim), f32, (size_t)(batch * q_heads * q_len),
-                         (hipStream_t)stream, "pjx_splitkv_decode");
+    return write_keyless(o, lse, (size_t)(batch * q_len * q_heads * v_dim), f32, (size_t)(batch * q_heads * q_len),
+                         (hipStream_t)stream, who);
+  const int64_t rows = (q_heads / kv_heads) * q_len;
   DecodeArgs a = {};
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v;
   a.lengths = kv_lengths; a.lse = lse;
@@ -1045,19 +1102,14 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   a.B = (int)batch; a.Lq = (int)q_len; a.Lk = (int)kv_len; a.Hq = (int)q_heads; a.G = (int)kv_heads;
   a.rows = (int)rows; a.fold = 0; a.chunk = (int)chunk;
   a.nch = (int)std::max<int64_t>((kv_len + chunk - 1) / chunk, 1);
-  a.dv = (int)head_dim; a.cx = sm_scale * kLog2e;
+  a.dv = (int)v_dim; a.cx = sm_scale * kLog2e;
+  const int nrb = gqa_row_blocks(rows, head_dim, v_dim, f32);
+  a.rpg = kRows * nrb;
   hipStream_t s = (hipStream_t)stream;
-  const char* who = "pjx_splitkv_decode";
-  const int nrb = (int)((rows + kRows - 1) / kRows);
-  if (f32) {
-    if (head_dim == 128)
-      return nrb == 1 ? run_decode<gqa_decode_f32_kernel<128, 1>>(a, workspace, workspace_bytes, s, who)
-                      : run_decode<gqa_decode_f32_kernel<128, 2>>(a, workspace, workspace_bytes, s, who);
-    return nrb == 1 ? run_decode<gqa_decode_f32_kernel<64, 1>>(a, workspace, workspace_bytes, s, who)
-                    : run_decode<gqa_decode_f32_kernel<64, 2>>(a, workspace, workspace_bytes, s, who);
-  }
-  return a.f16 ? run_gqa_h16<F16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who)
-               : run_gqa_h16<Bf16Fmt>(a, (int)head_dim, nrb, workspace, workspace_bytes, s, who);
+  const int d = (int)head_dim, dv = (int)v_dim;
+  if (f32) return run_gqa<Bf16Fmt, true>(a, d, dv, nrb, workspace, workspace_bytes, s, who);
+  return a.f16 ? run_gqa<F16Fmt, false>(a, d, dv, nrb, workspace, workspace_bytes, s, who)
+               : run_gqa<Bf16Fmt, false>(a, d, dv, nrb, workspace, workspace_bytes, s, who);
 }
 
 // ---------------------------------------------------------------------------
@@ -1101,15 +1153,15 @@ extern "C" int pjx_splitkv_decode_static(int dtype, const void* q, const void* k
                                          const int32_t* kv_lengths, void* o, float* lse,
                                          int64_t batch, int64_t q_len, int64_t kv_len,
                                          int64_t q_heads, int64_t kv_heads, int64_t head_dim,
-                                         float sm_scale, int64_t chunk, void* stream) {
+                                         int64_t v_dim, float sm_scale, int64_t chunk, void* stream) {
   clear_error();
   const char* who = "pjx_splitkv_decode_static";
-  if (batch < 0 || q_len <= 0 || kv_len < 0 || q_heads <= 0 || kv_heads <= 0 || q_heads % kv_heads)
-    return fail(PJX_ERR_INVALID, "pjx_splitkv_decode_static: bad sizes");
+  // every argument check of pjx_splitkv_decode first, then the size of the partials
+  const int vrc = check_gqa_decode(who, dtype, batch, q_len, kv_len, q_heads, kv_heads, head_dim, v_dim, sm_scale,
+                                   &chunk);
+  if (vrc != PJX_OK) return vrc;
   if (batch == 0) return PJX_OK;
-  const int64_t c = chunk == 0 ? auto_chunk(batch, kv_heads, kv_len, kGqaItems) : chunk;
-  if (c <= 0) return fail(PJX_ERR_INVALID, "pjx_splitkv_decode_static: chunk must be a positive multiple of 128");
-  const size_t need = ws_size(batch, kv_heads, (q_heads / kv_heads) * q_len, kv_len, head_dim, c);
+  const size_t need = ws_size(batch, kv_heads, (q_heads / kv_heads) * q_len, kv_len, v_dim, chunk);
   if (need > kScratchBytes) {
     char buf[256];
     snprintf(buf, sizeof(buf), "%s: these sizes need %zu bytes of partials, more than the %zu-byte "
@@ -1120,7 +1172,7 @@ extern "C" int pjx_splitkv_decode_static(int dtype, const void* q, const void* k
   const int rc = scratch_ptr(&ws, who);
   if (rc != PJX_OK) return rc;
   return pjx_splitkv_decode(dtype, q, k, v, kv_lengths, o, lse, ws, kScratchBytes, batch, q_len, kv_len,
-                            q_heads, kv_heads, head_dim, sm_scale, c, stream);
+                            q_heads, kv_heads, head_dim, v_dim, sm_scale, chunk, stream);
 }
 
 extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
@@ -1134,7 +1186,7 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   // an empty cache (kv_len == 0) may come as a null pointer
   if (!q || !o || (batch * kv_len > 0 && !cache)) return fail(PJX_ERR_INVALID, "pjx_mla_decode: null pointer");
   if (batch < 0 || q_len <= 0 || heads <= 0 || kv_len < 0) return fail(PJX_ERR_INVALID, "pjx_mla_decode: bad sizes");
-  if (q_len * heads > kRows) return fail(PJX_ERR_INVALID, "pjx_mla_decode: Lq*H must be <= 16");
+  if (q_len * heads > (1 << 20)) return fail(PJX_ERR_INVALID, "pjx_mla_decode: Lq*H must be <= 2^20");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_mla_decode: sm_scale must be > 0");
   if (chunk == 0) chunk = auto_chunk(batch, 1, kv_len, kMlaItems);
   if (chunk < kTile || chunk % kTile) return fail(PJX_ERR_INVALID, "pjx_mla_decode: chunk must be a positive multiple of 64");
@@ -1147,6 +1199,7 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
   a.rows = (int)(q_len * heads); a.fold = 1; a.chunk = (int)chunk;
   a.nch = (int)std::max<int64_t>((kv_len + chunk - 1) / chunk, 1);
   a.dv = (int)v_dim; a.cx = sm_scale * kLog2e;
+  a.rpg = kRows;  // one 16-row MFMA column block per row group
   hipStream_t s = (hipStream_t)stream;
   if (batch == 0) return PJX_OK;
   if (kv_len == 0)

@@ -253,32 +253,37 @@ def splitkv_decode(
     workspace=None,
 ):
     """``pjx_splitkv_decode``: bf16, fp16 or fp32 ``q [B, Lq, Hq, D]``,
-    ``k/v [B, S, Hkv, D]``; ``(Hq/Hkv)*Lq`` up to 64 (bf16 / fp16) or 32 (fp32)."""
+    ``k [B, S, Hkv, D]``, ``v [B, S, Hkv, Dv]`` -> ``o [B, Lq, Hq, Dv]``; D and
+    Dv each 64, 128 or 256, any number of packed rows ``(Hq/Hkv)*Lq``."""
     dev = _on_device(q, k, v)
-    if q.ndim != 4 or k.ndim != 4 or k.shape != v.shape:
-        raise ValueError("q must be [B, Lq, Hq, D] and k, v [B, S, Hkv, D]")
+    if q.ndim != 4 or k.ndim != 4 or v.ndim != 4 or k.shape[:3] != v.shape[:3]:
+        raise ValueError("q must be [B, Lq, Hq, D], k [B, S, Hkv, D] and v [B, S, Hkv, Dv]")
     B, Lq, Hq, D = q.shape
     _, S, Hkv, Dk = k.shape
+    Dv = v.shape[-1]
     if Dk != D or k.shape[0] != B or Hq % Hkv:
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, k {tuple(k.shape)}")
     if q.dtype not in _DTYPES or k.dtype != q.dtype or v.dtype != q.dtype:
         raise ValueError("split-KV decode takes bfloat16, float16 or float32 q, k, v of one dtype")
+    if D not in (64, 128, 256) or Dv not in (64, 128, 256):
+        raise ValueError(f"split-KV decode needs head dims 64, 128 or 256, got D={D}, Dv={Dv}")
     rows = (Hq // Hkv) * Lq
-    max_rows = 64 if q.dtype in HALF_DTYPES else 32
-    if rows > max_rows or D not in (64, 128):
-        raise ValueError(f"split-KV decode needs (Hq/Hkv)*Lq <= {max_rows} and head_dim 64 or 128")
     q, k, v = q.contiguous(), k.contiguous(), v.contiguous()
     L = _lengths(kv_lengths, B, dev)
-    nbytes = decode_workspace_bytes(B, Hkv, rows, S, D, chunk)
+    nbytes = decode_workspace_bytes(B, Hkv, rows, S, Dv, chunk)
     ws = _workspace(nbytes, dev, workspace)
-    o = torch.empty_like(q)
+    o = torch.empty((B, Lq, Hq, Dv), dtype=q.dtype, device=dev)
     lse = torch.empty((B, Hq, Lq), dtype=torch.float32, device=dev) if return_lse else None
     rc = native.load().pjx_splitkv_decode(
         _dtype_code(q), _ptr(q), _ptr(k), _ptr(v), _ptr(L), _ptr(o), _ptr(lse), _ptr(ws),
-        nbytes, B, Lq, S, Hq, Hkv, D, float(sm_scale), int(chunk), _stream(dev),
+        nbytes, B, Lq, S, Hq, Hkv, D, Dv, float(sm_scale), int(chunk), _stream(dev),
     )
     native.check(rc)
     return (o, lse) if return_lse else o
+
+
+# (rank, v_dim) pairs of the latent decode kernel (any number of folded rows).
+MLA_DECODE_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))
 
 
 def mla_decode(
@@ -294,8 +299,8 @@ def mla_decode(
         raise ValueError(f"incompatible shapes q {tuple(q.shape)}, cache {tuple(cache.shape)}")
     code = _half_code("MLA decode", q, cache)
     dv = R if v_dim is None else int(v_dim)
-    if (R, dv) not in ((576, 512), (576, 576), (512, 512), (128, 128)) or Lq * H > 16:
-        raise ValueError(f"MLA decode supports (R, v_dim) in (576,512),(576,576),(512,512),(128,128) and Lq*H <= 16; got ({R}, {dv}), Lq*H={Lq * H}")
+    if (R, dv) not in MLA_DECODE_SHAPES:
+        raise ValueError(f"MLA decode supports (R, v_dim) in (576,512),(576,576),(512,512),(128,128); got ({R}, {dv})")
     S = cache.shape[1]
     q, cache = q.contiguous(), cache.contiguous()
     L = _lengths(kv_lengths, B, dev)

@@ -65,12 +65,12 @@ _SIGNATURES = {
     "pjx_splitkv_decode": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _I64, _I64, _I64, _I64,
-         _I64, _I64, ctypes.c_float, _I64, _P],
+         _I64, _I64, _I64, ctypes.c_float, _I64, _P],
     ),
     "pjx_splitkv_decode_static": (
         ctypes.c_int,
-        [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, ctypes.c_float,
-         _I64, _P],
+        [ctypes.c_int, _P, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I64,
+         ctypes.c_float, _I64, _P],
     ),
     "pjx_mla_decode": (
         ctypes.c_int,

@@ -167,3 +167,145 @@ def test_wide_and_fp32_decode_route_to_splitkv(device, monkeypatch, dtype):
     want = oracle.xla_attention(q, k, v, mask=oracle.KVLenMask(lengths), sm_scale=1 / math.sqrt(d),
                                 compute_dtype=np.float32 if bf16 else np.float64)
     assert max_abs(to_np(out), want) <= (BF16_TOL if bf16 else 1e-5)
+
+
+# Head dims beyond 128, Dv != D and row groups: (dtype, B, Lq, S, Hq, Hkv, D, Dv,
+# lengths, chunk, launched instance).  A row group holds up to 64 packed rows
+# (4 blocks of 16) in bf16 / fp16 at D, Dv <= 128, else 32 (2 blocks); more
+# rows run as several row groups over the same keys (the reference's row
+# blocks, attention_splitkv.py:155-172).
+WIDE_CASES = [
+    ("bf16", 2, 1, 1500, 8, 2, 256, 256, [1500, 333], 256, "gqa_decode_kernel<Bf16Fmt, 256, 256, 1>"),
+    ("bf16", 3, 2, 1100, 32, 2, 256, 256, [1100, 0, 517], 0, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2>"),
+    ("f16", 2, 1, 900, 16, 4, 256, 128, [900, 129], 128, "gqa_decode_kernel<F16Fmt, 256, 128, 1>"),
+    ("bf16", 2, 3, 800, 8, 1, 128, 64, [800, 64], 128, "gqa_decode_kernel<Bf16Fmt, 128, 64, 2>"),
+    ("bf16", 2, 1, 1000, 8, 2, 64, 128, None, 256, "gqa_decode_kernel<Bf16Fmt, 64, 128, 1>"),
+    ("bf16", 1, 2, 700, 16, 1, 64, 256, [650], 128, "gqa_decode_kernel<Bf16Fmt, 64, 256, 2>"),
+    # row groups: 128 rows (two groups of 64), 96 rows (a partial second group)
+    ("bf16", 2, 16, 1200, 16, 2, 128, 128, [1200, 301], 0, "gqa_decode_kernel<Bf16Fmt, 128, 128, 4>"),
+    ("f16", 2, 3, 1000, 64, 2, 64, 64, [1000, 1], 256, "gqa_decode_kernel<F16Fmt, 64, 64, 4>"),
+    # D = 256 with 72 rows: three groups of 32, the last partial
+    ("bf16", 2, 9, 600, 16, 2, 256, 256, [600, 300], 128, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2>"),
+    # fp32: groups of 32 rows; D / Dv up to 256
+    ("f32", 2, 6, 900, 16, 2, 128, 128, [900, 450], 256, "gqa_decode_f32_kernel<128, 128, 2>"),
+    ("f32", 2, 1, 1300, 8, 2, 256, 256, [1300, 77], 0, "gqa_decode_f32_kernel<256, 256, 1>"),
+    ("f32", 2, 2, 700, 20, 2, 256, 64, [700, 0], 128, "gqa_decode_f32_kernel<256, 64, 2>"),
+    ("f32", 1, 1, 1000, 8, 1, 64, 128, None, 256, "gqa_decode_f32_kernel<64, 128, 1>"),
+]
+
+
+@pytest.mark.parametrize("dtype,b,lq,s,hq,hkv,d,dv,lengths,chunk,inst", WIDE_CASES)
+def test_splitkv_decode_head_dims_and_row_groups(device, dtype, b, lq, s, hq, hkv, d, dv, lengths, chunk, inst):
+    """Split-KV decode at D, Dv in {64, 128, 256} (Dv != D included) and past
+    64 packed rows (32 in fp32), against the oracle: bf16 / fp16 within 2e-2
+    of the fp32 oracle on the same rounded inputs (fp16 also closer than the
+    bf16-mode oracle), fp32 within 1e-5 of the float64 oracle; LSE +inf
+    exactly for empty sequences.  The launched instance is asserted."""
+    import torch
+    from probjax_amd import native
+    from probjax_amd.hip_attention import splitkv_decode
+
+    rows = (hq // hkv) * lq
+    print(f"split-KV {dtype} B={b} Lq={lq} S={s} Hq={hq} Hkv={hkv} D={d} Dv={dv} rows={rows} -> {inst}", flush=True)
+    q, k, v = rng_normal(13, (b, lq, hq, d), (b, s, hkv, d), (b, s, hkv, dv))
+    low = dtype != "f32"
+    if low:
+        rnd = oracle.round_bf16 if dtype == "bf16" else oracle.round_f16
+        q, k, v = (rnd(x) for x in (q, k, v))
+    scale = 1.0 / math.sqrt(d)
+    mask = None if lengths is None else oracle.KVLenMask(np.array(lengths, np.int32))
+    want, want_lse = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale, strategy="tiled", return_lse=True,
+                                          dtype=dtype, compute_dtype=np.float32 if low else np.float64)
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
+    got, lse = splitkv_decode(*(to_dev(x, device, tdt) for x in (q, k, v)), sm_scale=scale,
+                              kv_lengths=L, chunk=chunk, return_lse=True)
+    launched = native.last_launches()
+    torch.cuda.synchronize()
+    assert launched[0] == inst, launched
+    assert got.shape == (b, lq, hq, dv) and got.dtype == tdt
+    err = max_abs(to_np(got), want)
+    print(f"  max-abs {err:.3e}", flush=True)
+    assert err <= (BF16_TOL if low else 1e-5)
+    if dtype == "f16":
+        want_bf = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale, strategy="tiled", dtype="bf16")
+        d_got = np.sqrt(np.mean((to_np(got).astype(np.float64) - want) ** 2))
+        d_bf = np.sqrt(np.mean((want_bf.astype(np.float64) - want) ** 2))
+        assert d_got <= 0.5 * d_bf
+    lse = to_np(lse)
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
+    fin = np.isfinite(want_lse)
+    assert max_abs(lse[fin], want_lse[fin]) <= (1e-3 if low else 1e-5)
+
+
+@pytest.mark.parametrize(
+    "b,lq,h,s,r,dv,lengths,chunk",
+    [
+        (2, 1, 32, 700, 576, 512, [700, 333], 0),           # 2 row groups of 16
+        (3, 1, 128, 600, 576, 512, [600, 0, 65], 128),       # 8 row groups, an empty sequence
+        (2, 2, 40, 500, 512, 512, None, 128),                # Lq = 2: 80 folded rows, t*H + h
+        (2, 1, 20, 800, 128, 128, [800, 17], 0),             # 20 rows: a partial second group
+    ],
+)
+def test_mla_decode_row_groups(device, b, lq, h, s, r, dv, lengths, chunk):
+    """The latent decode past 16 folded rows: each 16 rows form a row group
+    streaming the cache chunk by chunk (the reference's mla takes any head
+    count, latent_attention.py:636-766), against the oracle within 2e-2."""
+    import torch
+    from probjax_amd import native
+    from probjax_amd.hip_attention import mla_decode
+
+    print(f"MLA decode B={b} Lq={lq} H={h} S={s} R={r} Dv={dv} rows={lq * h}", flush=True)
+    q, cache = (oracle.round_bf16(x) for x in rng_normal(14, (b, lq, h, r), (b, s, r)))
+    scale = 1.0 / math.sqrt(192)
+    mask = None if lengths is None else oracle.KVLenMask(np.array(lengths, np.int32))
+    shared = cache[:, :, None, :]
+    want, want_lse = oracle.xla_attention(q, shared, shared, mask=mask, sm_scale=scale, strategy="tiled",
+                                          return_lse=True)
+    want = want[..., :dv]
+    L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
+    got, lse = mla_decode(to_dev(q, device, torch.bfloat16), to_dev(cache, device, torch.bfloat16),
+                          sm_scale=scale, v_dim=dv, kv_lengths=L, chunk=chunk, return_lse=True)
+    launched = native.last_launches()
+    torch.cuda.synchronize()
+    assert launched[0] == f"mla_decode_kernel<Bf16Fmt, {r}, {dv}>", launched
+    err = max_abs(to_np(got), want)
+    print(f"  max-abs {err:.3e}", flush=True)
+    assert err <= BF16_TOL
+    lse = to_np(lse)
+    np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
+    fin = np.isfinite(want_lse)
+    assert max_abs(lse[fin], want_lse[fin]) <= 1e-3
+
+
+def test_splitkv_forward_head_dims(device):
+    """probjax's splitkv_forward with qk head dim 192 and value head dim 96
+    (padded to the kernel's 256 / 128) matches the oracle at the true dims;
+    mha sends a D = 192 decode step to the split-KV kernel."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd import native
+
+    b, lq, s, hq, hkv, d, dv = 2, 1, 2048, 16, 4, 192, 96
+    q, k, v = (oracle.round_bf16(x) for x in rng_normal(15, (b, lq, hq, d), (b, s, hkv, d), (b, s, hkv, dv)))
+    lengths = np.array([2048, 1111], np.int32)
+    scale = 1.0 / math.sqrt(d)
+    want, want_lse = oracle.xla_attention(q, k, v, mask=oracle.KVLenMask(lengths), sm_scale=scale, return_lse=True)
+    tq, tk, tv = (to_dev(x, device, torch.bfloat16) for x in (q, k, v))
+    L = torch.from_numpy(lengths).to(device)
+    got, lse = A.splitkv_forward(tq, tk, tv, sm_scale=scale, kv_lengths=L, return_lse=True)
+    torch.cuda.synchronize()
+    assert got.shape == (b, lq, hq, dv)
+    assert max_abs(to_np(got), want) <= BF16_TOL
+    assert max_abs(to_np(lse), want_lse) <= 1e-3
+    # mha (Dv = D): the decode route pads 192 to 256
+    v2 = oracle.round_bf16(rng_normal(16, (b, s, hkv, d))[0])
+    want2 = oracle.xla_attention(q, k, v2, mask=oracle.KVLenMask(lengths), sm_scale=scale)
+    from probjax_amd.masks import KVLenMask
+
+    assert A.use_splitkv(tq, tk, mask=KVLenMask(L))
+    out = A.mha(tq, tk, to_dev(v2, device, torch.bfloat16), mask=KVLenMask(L), sm_scale=scale)
+    launched = native.last_launches()
+    torch.cuda.synchronize()
+    assert launched[0] == "gqa_decode_kernel<Bf16Fmt, 256, 256, 1>", launched
+    assert max_abs(to_np(out), want2) <= BF16_TOL

@@ -104,6 +104,10 @@ _CASES = [
     ("kvlen_zero_array_bias", 48, 80, 4, 2, 64, "kvlen0", "array"),
     ("kvlen_zero_dense_object", 48, 80, 2, 1, 128, "kvlen0", "dense_object"),
     ("padded_d96", 64, 64, 2, 2, 96, "array", "array"),
+    # no bias: KVLenMask is not one of probjax's fused masks, so Flax's einsum
+    ("kvlen_zero_no_bias", 48, 80, 4, 2, 64, "kvlen0", None),
+    # a fused mask type under 64 keys: Flax's einsum too (rows 42.. keep no key)
+    ("window_short_keys", 48, 40, 4, 4, 64, "window2", None),
 ]
 
 
@@ -112,9 +116,11 @@ _CASES = [
 def test_flax_semantics_cases(device, dtype, case):
     """Array masks alone, biases alone, Lq != Lk, per-head masks, an object
     bias with an array mask, and object masks whose rows drop every key
-    (KVLenMask with a zero length) together with a bias: wherever probjax
-    takes the Flax einsum (a bias, or an array mask), such rows are the mean
-    of V, with dV = dO / Lk and no gradient to q, k or the bias there."""
+    (KVLenMask with a zero length, with and without a bias; a local window
+    over fewer than 64 keys): wherever probjax takes the Flax einsum (a bias,
+    an array mask, a mask outside its fused set, fewer than 64 keys), such
+    rows are the mean of V, with dV = dO / Lk and no gradient to q, k or the
+    bias there."""
     import torch
     from probjax_amd import attention as A
     from probjax_amd import masks as M
@@ -143,6 +149,11 @@ def test_flax_semantics_cases(device, dtype, case):
         lengths = np.array([Lk, 0, Lk - 17], np.int32)
         keep = np.broadcast_to((np.arange(Lk)[None, :] < lengths[:, None])[:, None, None, :], (B, 1, Lq, Lk))
         mask_arg = M.KVLenMask(torch.from_numpy(lengths).to(device))
+    elif mkind == "window2":
+        d = np.arange(Lq)[:, None] - np.arange(Lk)[None, :]
+        keep = np.broadcast_to(((d >= 0) & (d <= 2))[None, None], (B, 1, Lq, Lk))
+        assert not keep[0, 0, -1].any()  # the last rows keep no key
+        mask_arg = M.LocalWindowMask(2, 0)
     bias_ref = None
     bias_arg = None
     tb = None

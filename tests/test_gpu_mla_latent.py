@@ -168,9 +168,10 @@ def test_absorbed_mla_forward_and_grads(device, case):
 
 
 def test_absorbed_prefill_routes(device, monkeypatch):
-    """Decode-shaped calls without gradients keep the split-KV latent kernel;
-    a causal mask, a bias, Lq*H > 16 or a gradient take the latent flash
-    kernels (one call each, through pjx_mla_fwd / pjx_mla_bwd)."""
+    """Decode-shaped calls without gradients (up to 128 folded rows: each 16
+    form a row group of the split-KV latent kernel) keep that kernel; a causal
+    mask, a bias, Lq*H > 128 or a gradient take the latent flash kernels (one
+    call each, through pjx_mla_fwd / pjx_mla_bwd)."""
     import torch
     from probjax_amd import attention as A
     from probjax_amd import hip_attention as hip
@@ -194,7 +195,11 @@ def test_absorbed_prefill_routes(device, monkeypatch):
     assert calls == ["mla_fwd"]
     calls.clear()
     q2 = to_dev(rng_normal(41, (2, 4, 16, 576))[0], device, torch.bfloat16)
-    A.mla(q2, tc, sm_scale=0.1)
+    A.mla(q2, tc, sm_scale=0.1)  # 64 folded rows: four row groups of the decode
+    assert calls == ["mla_decode"]
+    calls.clear()
+    q3 = to_dev(rng_normal(42, (2, 9, 16, 576))[0], device, torch.bfloat16)
+    A.mla(q3, tc, sm_scale=0.1)  # 144 folded rows: a query block for the flash kernels
     assert calls == ["mla_fwd"]
     calls.clear()
     tq.requires_grad_(True)

@@ -76,24 +76,26 @@ def test_use_splitkv_only_for_exact_cases():
     assert not A.use_splitkv(q3, k3)
     q4, k4, _ = _qkv(hq=64, hkv=2)                              # 32 rows per KV head
     assert A.use_splitkv(q4, k4, split_kv=True)
-    q4b, k4b, _ = _qkv(hq=64, hkv=2, lq=3)                      # 96 rows: past the reference's 64
-    assert not A.use_splitkv(q4b, k4b, split_kv=True)
+    q4b, k4b, _ = _qkv(hq=64, hkv=2, lq=3)                      # 96 rows: two row groups
+    assert A.use_splitkv(q4b, k4b, split_kv=True)
     q5, k5, _ = _qkv(dtype=torch.float32)
     assert A.use_splitkv(q5, k5)                                # fp32 split-KV
-    q5b, k5b, _ = _qkv(dtype=torch.float32, hq=64, hkv=1)       # 64 rows: fp32 takes up to 32
-    assert not A.use_splitkv(q5b, k5b, split_kv=True)
-    # head dims up to 128 are zero-padded to a kernel width; wider ones are not
+    q5b, k5b, _ = _qkv(dtype=torch.float32, hq=64, hkv=1)       # 64 fp32 rows: two row groups
+    assert A.use_splitkv(q5b, k5b, split_kv=True)
+    # head dims up to 256 are zero-padded to a kernel width; wider ones are not
     q6, k6 = torch.zeros(1, 1, 8, 96, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 96, dtype=torch.bfloat16)
     assert A.use_splitkv(q6, k6)
     q7, k7 = torch.zeros(1, 1, 8, 160, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 160, dtype=torch.bfloat16)
-    assert not A.use_splitkv(q7, k7, split_kv=True)
+    assert A.use_splitkv(q7, k7, split_kv=True)
+    q8, k8 = torch.zeros(1, 1, 8, 300, dtype=torch.bfloat16), torch.zeros(1, 2048, 2, 300, dtype=torch.bfloat16)
+    assert not A.use_splitkv(q8, k8, split_kv=True)
 
 
 def test_kernel_width_and_padding():
     ds = (1, 32, 64, 65, 96, 128, 129, 256, 257)
     assert [A._kernel_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
     assert [A._kernel_width(d, torch.float32) for d in ds] == [64, 64, 64, 128, 128, 128, None, None, None]
-    assert [A._decode_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, None, None, None]
+    assert [A._decode_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
     assert [A._latent_width(r, torch.bfloat16) for r in (100, 200, 300, 512, 513, 576, 577)] == \
         [128, 256, 512, 512, 576, 576, None]
     assert [A._latent_width(r, torch.float32) for r in (100, 200, 576)] == [128, None, None]

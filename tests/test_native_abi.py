@@ -124,27 +124,46 @@ def test_flash_empty_batch_is_a_no_op(lib):
 def test_decode_rejects_invalid_arguments(lib):
     P = ctypes.c_void_p
     ok = [native.PJX_DTYPE_BF16, P(1), P(1), P(1), None, P(1), None, P(1), 1 << 30,
-          1, 1, 64, 32, 8, 128, 0.1, 0, None]
-    bad_rows = list(ok)
-    bad_rows[12] = 8 * 65  # (Hq/Hkv)*Lq = 65 rows > 64
-    assert lib.pjx_splitkv_decode(*bad_rows) == 1
-    assert "<= 64" in lib.pjx_last_error().decode()
+          1, 1, 64, 32, 8, 128, 128, 0.1, 0, None]
+    bad_dim = list(ok)
+    bad_dim[14] = 96  # head dims 64, 128, 256
+    assert lib.pjx_splitkv_decode(*bad_dim) == 1
+    assert "head_dim and v_dim" in lib.pjx_last_error().decode()
+    bad_vdim = list(ok)
+    bad_vdim[15] = 512
+    assert lib.pjx_splitkv_decode(*bad_vdim) == 1
+    assert "head_dim and v_dim" in lib.pjx_last_error().decode()
     bad_chunk = list(ok)
-    bad_chunk[16] = 100
+    bad_chunk[17] = 100
     assert lib.pjx_splitkv_decode(*bad_chunk) == 1
     assert "chunk" in lib.pjx_last_error().decode()
-    f32 = list(ok)
-    f32[0] = native.PJX_DTYPE_F32
-    f32[12] = 8 * 33  # 33 rows: fp32 takes up to 32
-    assert lib.pjx_splitkv_decode(*f32) == 1
-    assert "<= 32 in fp32" in lib.pjx_last_error().decode()
     bad_dtype = list(ok)
     bad_dtype[0] = 7
     assert lib.pjx_splitkv_decode(*bad_dtype) == 1
+    assert "dtype" in lib.pjx_last_error().decode()
+    bad_heads = list(ok)
+    bad_heads[12] = 30  # Hq not a multiple of Hkv
+    assert lib.pjx_splitkv_decode(*bad_heads) == 1
     mla = [native.PJX_DTYPE_BF16, P(1), P(1), None, P(1), None, P(1), 1 << 30,
            1, 1, 16, 64, 300, 512, 0.1, 0, None]
     assert lib.pjx_mla_decode(*mla) == 1
     assert "rank" in lib.pjx_last_error().decode() or "supported" in lib.pjx_last_error().decode()
+
+
+def test_static_decode_checks_arguments_before_size(lib):
+    """pjx_splitkv_decode_static runs every argument check of
+    pjx_splitkv_decode before sizing its partials: a bad head dim or chunk is
+    PJX_ERR_INVALID whatever the sizes, and B = 0 with a bad dtype is refused."""
+    big = [1, None, None, None, None, None, None, 256, 1, 1 << 20, 16, 16]
+    for dt, d, dv, chunk, msg in ((native.PJX_DTYPE_BF16, 96, 128, 0, "head_dim"),
+                                  (native.PJX_DTYPE_BF16, 128, 128, 100, "chunk"),
+                                  (7, 128, 128, 0, "dtype")):
+        args = list(big)
+        args[0] = dt
+        assert lib.pjx_splitkv_decode_static(*args, d, dv, 0.1, chunk, None) == 1
+        assert msg in lib.pjx_last_error().decode()
+    zero_batch = [7, None, None, None, None, None, None, 0, 1, 100, 8, 8, 128, 128, 0.1, 0, None]
+    assert lib.pjx_splitkv_decode_static(*zero_batch) == 1
 
 
 def test_workspace_size_formula(lib):

@@ -34,12 +34,13 @@ def _call_both(device, B, S, Hq, Hkv, D, Lq, lengths, seed):
         lse = torch.full((B, Hq, Lq), float("nan"), dtype=torch.float32, device=device)
         ptrs = [ctypes.c_void_p(t.data_ptr()) for t in (tq, tk, tv, L, o, lse)]
         if static:
-            rc = lib.pjx_splitkv_decode_static(native.PJX_DTYPE_BF16, *ptrs, B, Lq, S, Hq, Hkv, D, scale, 0, stream)
+            rc = lib.pjx_splitkv_decode_static(native.PJX_DTYPE_BF16, *ptrs, B, Lq, S, Hq, Hkv, D, D, scale, 0,
+                                               stream)
         else:
             nbytes = int(lib.pjx_decode_workspace_size(B, Hkv, rows, S, D, 0))
             ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
             rc = lib.pjx_splitkv_decode(native.PJX_DTYPE_BF16, *ptrs, ctypes.c_void_p(ws.data_ptr()), nbytes,
-                                        B, Lq, S, Hq, Hkv, D, scale, 0, stream)
+                                        B, Lq, S, Hq, Hkv, D, D, scale, 0, stream)
         native.check(rc)
         torch.cuda.synchronize()
         outs.append((o, lse))
@@ -70,10 +71,10 @@ def test_static_decode_refuses_sizes_past_its_array(device):
     B, S, Hq, Hkv, D = 256, 1 << 20, 16, 16, 128
     need = int(lib.pjx_decode_workspace_size(B, Hkv, 1, S, D, 0))
     assert need > native.PJX_DECODE_STATIC_SCRATCH_BYTES
-    # the size check runs before any pointer is used or kernel launched
-    dummy = ctypes.c_void_p(16)
-    rc = lib.pjx_splitkv_decode_static(native.PJX_DTYPE_BF16, dummy, dummy, dummy, None, dummy, None,
-                                       B, 1, S, Hq, Hkv, D, 0.1, 0,
+    # the size check runs before any pointer is used or kernel launched; with
+    # null pointers a regression past it would be refused, not launched
+    rc = lib.pjx_splitkv_decode_static(native.PJX_DTYPE_BF16, None, None, None, None, None, None,
+                                       B, 1, S, Hq, Hkv, D, D, 0.1, 0,
                                        ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream))
     assert rc == 3
     assert "scratch" in lib.pjx_last_error().decode()
