@@ -49,8 +49,8 @@ from .masks import (LoweredBias, LoweredMask, dense_keep, dense_relpos, dense_su
 HIP_ARCH = "gfx950"
 HALF_DTYPES = (torch.bfloat16, torch.float16)  # the 16-bit (MFMA bf16 / fp16) kernels
 KERNEL_DTYPES = HALF_DTYPES + (torch.float32,)  # dtypes the kernels take
-FLASH_HEAD_DIMS = (64, 128, 256)  # 256: bfloat16 / float16 only
-FLASH_HEAD_DIMS_F32 = (64, 128)
+FLASH_HEAD_DIMS = (64, 128, 256)
+FLASH_HEAD_DIMS_F32 = (64, 128, 256)
 DECODE_HEAD_DIMS = (64, 128, 256)  # head dims (q/k and v each) of the split-KV decode
 LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (16-bit)
 # Lq*H folded rows up to which an absorbed decode step takes the split-KV latent
@@ -667,7 +667,7 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
     which is all a caller that multiplies by ``W_UV`` of width ``v_dim``
     needs), any query length, every mask and bias of the flash route,
     differentiable in ``q`` and ``cache`` (bias data gets no gradient, as in
-    the reference's VJP); latent widths up to 576 in bfloat16 / float16 (up to 128 in
+    the reference's VJP); latent widths up to 576 in bfloat16 / float16 (up to 256 in
     float32).  Decode steps (``Q * H <= 128``, no gradient, no bias,
     ``None`` / ``KVLenMask``) run the split-KV latent kernel; the rest the
     latent flash kernels, whose heads share one K = V head (the folded

@@ -91,8 +91,8 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: negative or zero size");
   if (q_heads % kv_heads != 0)
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: q_heads must be a multiple of kv_heads");
-  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PJX_DTYPE_F32))
-    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64 or 128 (or 256 in bf16 / fp16)");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PJX_ERR_INVALID, "pjx_flash_bwd: head_dim must be 64, 128 or 256");
   if (!(sm_scale > 0.f)) return fail(PJX_ERR_INVALID, "pjx_flash_bwd: sm_scale must be > 0");
   if (bias && !((bias_batch == 1 || bias_batch == batch) && (bias_heads == 1 || bias_heads == q_heads)))
     return fail(PJX_ERR_INVALID, "pjx_flash_bwd: bias must be [1|B, 1|Hq, Lq, Lk]");
@@ -142,6 +142,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   ba.dq = dq; ba.dk = dk; ba.dv = dv;
   ba.dbias = dbias;
   hipStream_t s = (hipStream_t)stream;
+  if (head_dim == 256 && f32) return run_flash_f32_wide_bwd(ba, s);
   if (head_dim == 256) {
     // dQ (and delta, lse*log2e): the 16-row wide kernel.  dK/dV: without
     // extended masks the 32-key kernel above at one wave per SIMD (32x32x16

@@ -1194,4 +1194,7 @@ static int launch_dkdv(const FlashBwdArgs& a, hipStream_t stream, int threads = 
 // VGPR form).  Returns a PJX_* status.
 int launch_dkdv256(const FlashBwdArgs& a, bool f16, bool hb, hipStream_t s);
 
+// fp32 backward at head dim 256 (dQ then dK/dV, flash_f32_wide.hip).
+int run_flash_f32_wide_bwd(const FlashBwdArgs& ba, hipStream_t s);
+
 }  // namespace pjx

@@ -32,6 +32,9 @@ struct FlashArgs {
 constexpr int kBQ = 128;
 constexpr int kThreads = 256;
 
+// fp32 forward at head dim 256 (flash_f32_wide.hip).  Returns a PJX_* status.
+int launch_flash_f32_wide(const FlashArgs& a, hipStream_t s);
+
 // Per-block geometry shared by both dtype paths.
 struct BlockGeom {
   int b, h, hkv, q0, qw, qi;

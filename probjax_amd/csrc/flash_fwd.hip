@@ -1120,8 +1120,8 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
   clear_error();
   if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16 && dtype != PJX_DTYPE_F32)
     return fail(PJX_ERR_INVALID, "pjx_flash_fwd: dtype must be PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32");
-  if (head_dim != 64 && head_dim != 128 && !(head_dim == 256 && dtype != PJX_DTYPE_F32))
-    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64 or 128 (or 256 in bf16 / fp16)");
+  if (head_dim != 64 && head_dim != 128 && head_dim != 256)
+    return fail(PJX_ERR_INVALID, "pjx_flash_fwd: head_dim must be 64, 128 or 256");
   FlashArgs a;
   bool empty;
   int rc = make_flash_args(a, "pjx_flash_fwd", q, k, v, o, lse, kv_lengths, bias, bias_batch,
@@ -1134,7 +1134,7 @@ extern "C" int pjx_flash_fwd(int dtype, const void* q, const void* k, const void
                          (size_t)(batch * q_heads * q_len), s, "pjx_flash_fwd");
   const bool hb = bias != nullptr;
   a.f16 = dtype == PJX_DTYPE_F16;
-  if (head_dim == 256) return launch_flash_wide256(a, s);
+  if (head_dim == 256) return dtype == PJX_DTYPE_F32 ? launch_flash_f32_wide(a, s) : launch_flash_wide256(a, s);
   if (dtype == PJX_DTYPE_BF16) return launch_h16<Bf16Fmt>(a, (int)head_dim, s);
   if (dtype == PJX_DTYPE_F16) return launch_h16<F16Fmt>(a, (int)head_dim, s);
   if (a.ext) {

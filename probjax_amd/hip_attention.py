@@ -144,8 +144,8 @@ def flash_attention_fwd(
         raise ValueError("q, k, v must share a dtype")
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128) and not (D == 256 and q.dtype in HALF_DTYPES):
-        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16 / fp16)")
+    if D not in (64, 128, 256):
+        raise ValueError(f"head_dim {D} not supported (64, 128 or 256)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     code = _dtype_code(q)
@@ -199,8 +199,8 @@ def flash_attention_bwd(
     code = _dtype_code(q)
     if Hq % Hkv:
         raise ValueError(f"query heads {Hq} must be a multiple of kv heads {Hkv}")
-    if D not in (64, 128) and not (D == 256 and q.dtype in HALF_DTYPES):
-        raise ValueError(f"head_dim {D} not supported (64 or 128, or 256 in bf16 / fp16)")
+    if D not in (64, 128, 256):
+        raise ValueError(f"head_dim {D} not supported (64, 128 or 256)")
     if not sm_scale > 0:
         raise ValueError("sm_scale must be > 0")
     q, k, v, o, do = (t.contiguous() for t in (q, k, v, o, do))

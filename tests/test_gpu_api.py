@@ -151,7 +151,7 @@ def test_route_falls_through_for_unsupported_on_device(device):
     assert A.hip_attention_or_none(q, q, q, mask=None, bias=None, dropout_rate=0.0, sm_scale=0.1) is None
     with pytest.raises(ValueError, match="head_dim 300"):
         A.mha(q, q, q)
-    q32 = torch.zeros(1, 16, 2, 160, dtype=torch.float32, device=device)  # fp32 kernels stop at 128
+    q32 = torch.zeros(1, 16, 2, 260, dtype=torch.float32, device=device)  # fp32 kernels stop at 256
     assert A.hip_attention_or_none(q32, q32, q32, mask=None, bias=None, dropout_rate=0.0, sm_scale=0.1) is None
-    with pytest.raises(ValueError, match="head_dim 160"):
+    with pytest.raises(ValueError, match="head_dim 260"):
         A.mha(q32, q32, q32)

@@ -94,11 +94,11 @@ def test_use_splitkv_only_for_exact_cases():
 def test_kernel_width_and_padding():
     ds = (1, 32, 64, 65, 96, 128, 129, 256, 257)
     assert [A._kernel_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
-    assert [A._kernel_width(d, torch.float32) for d in ds] == [64, 64, 64, 128, 128, 128, None, None, None]
+    assert [A._kernel_width(d, torch.float32) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
     assert [A._decode_width(d) for d in ds] == [64, 64, 64, 128, 128, 128, 256, 256, None]
     assert [A._latent_width(r, torch.bfloat16) for r in (100, 200, 300, 512, 513, 576, 577)] == \
         [128, 256, 512, 512, 576, 576, None]
-    assert [A._latent_width(r, torch.float32) for r in (100, 200, 576)] == [128, None, None]
+    assert [A._latent_width(r, torch.float32) for r in (100, 200, 300, 576)] == [128, 256, None, None]
     x = torch.randn(2, 3, 4, 40, requires_grad=True)
     y = A._pad_features(x, 64)
     assert y.shape == (2, 3, 4, 64) and torch.equal(y[..., :40], x) and not y[..., 40:].any()
@@ -196,8 +196,8 @@ def test_mha_and_mla_refuse_off_device():
     wk, wv = torch.zeros(16, 96, 576, dtype=torch.bfloat16), torch.zeros(16, 64, 576, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="ROCm device"):
         A.mla(qd, c, wk, wv)
-    with pytest.raises(ValueError, match="head dims up to 128"):
-        A.mla(torch.zeros(2, 4, 16, 192), c.float(), torch.zeros(16, 192, 576), torch.zeros(16, 128, 576))
+    with pytest.raises(ValueError, match="head dims up to 256"):
+        A.mla(torch.zeros(2, 4, 16, 300), c.float(), torch.zeros(16, 300, 576), torch.zeros(16, 128, 576))
     with pytest.raises(ValueError, match="no dropout"):
         A.mla(qd, c, wk, wv, dropout_rate=0.1)
 
@@ -344,7 +344,7 @@ def test_low_rank_fold_matches_oracle(dtype):
         assert not got[..., n:].float().any()
     with pytest.raises(ValueError, match="positive sm_scale"):
         A._fold_low_rank(tq, tk, tv, terms, 0.0)
-    assert A._fold_low_rank(torch.zeros(1, 4, 4, 128), torch.zeros(1, 4, 4, 128), torch.zeros(1, 4, 4, 128),
+    assert A._fold_low_rank(torch.zeros(1, 4, 4, 256), torch.zeros(1, 4, 4, 256), torch.zeros(1, 4, 4, 256),
                             terms[:1], 0.1) is None
     with pytest.raises(ValueError, match="same rank"):
         M.LowRankBias(torch.zeros(2, 4, 3), torch.zeros(2, 4, 2))
