@@ -27,7 +27,13 @@ H=16, R=576, 512 value columns) and ``C5AB`` its backward (``pjx_mla_bwd``);
 ``cpu_baseline`` times the numpy restatement of probjax's XLA CPU path
 (``oracle.xla_attention``, 256x256 tiles with causal tile skipping) on one
 (batch, head) slice of the headline workload on the host cores, and scales it
-to TFLOP/s.  It is a reported baseline only.
+to TFLOP/s; its ``decode`` entry times the same path on the first 4 of C3's
+32 sequences, as GB/s of the bytes that slice must read.  Both are reported
+baselines only.
+
+``--summarize-trace DIR`` prints, per workload, the kernels of the timed
+steps of a ``rocprofv3 --kernel-trace --marker-trace`` run of this script
+(each workload's timed steps sit in a roctx range).
 """
 
 from __future__ import annotations
@@ -66,6 +72,9 @@ def _parse():
                         "forward+backward); default all")
     p.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                    help="only run a plain device copy of MIB MiB (counter calibration) and exit")
+    p.add_argument("--summarize-trace", default="", metavar="DIR",
+                   help="only summarise a rocprofv3 --kernel-trace --marker-trace csv run of this script "
+                        "(the kernels of each workload's timed steps) and exit; needs no GPU")
     p.add_argument("--gemm-calibration", type=int, default=0, metavar="N",
                    help="only time a library bf16 GEMM N x N x N (torch.matmul -> hipBLASLt), the "
                         "practical MFMA ceiling on this box, and exit")
@@ -412,15 +421,23 @@ def _settle(fn, seconds):
         torch.cuda.synchronize()
 
 
-def _time(fn, steps, warmup, settle_s=0.0):
+TIMED_RANGE = "pjx-timed:"  # roctx range name prefix around each workload's timed steps
+
+
+def _time(fn, steps, warmup, settle_s=0.0, label=None):
     """Wall time of `steps` back-to-back calls between device syncs, and the
-    per-call average from HIP events recorded on the launch stream."""
+    per-call average from HIP events recorded on the launch stream.  With a
+    label, the timed steps (and nothing else) sit in a roctx range
+    ``pjx-timed:<label>``, so a ``rocprofv3 --kernel-trace --marker-trace``
+    run can quote the kernels of exactly those steps (``--summarize-trace``)."""
     import torch
 
     _settle(fn, settle_s)
     for _ in range(warmup):
         fn()
     torch.cuda.synchronize()
+    if label is not None:
+        torch.cuda.nvtx.range_push(TIMED_RANGE + label)
     stream = torch.cuda.current_stream()
     e0 = torch.cuda.Event(enable_timing=True)
     e1 = torch.cuda.Event(enable_timing=True)
@@ -431,7 +448,46 @@ def _time(fn, steps, warmup, settle_s=0.0):
     e1.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    if label is not None:
+        torch.cuda.nvtx.range_pop()
     return wall / steps * 1e3, e0.elapsed_time(e1) / steps
+
+
+def summarize_trace(trace_dir):
+    """Per workload, the kernels dispatched inside its timed range in a
+    ``rocprofv3 --kernel-trace --marker-trace --output-format csv`` run of this
+    script (``*_kernel_trace.csv``, ``*_marker_api_trace.csv`` in trace_dir):
+    calls, average / min / max duration, and the workload's kernel time per
+    step (sum of durations / steps).  Prints a markdown table."""
+    import csv
+    import glob
+    import re
+
+    def one(pattern):
+        files = glob.glob(os.path.join(trace_dir, "**", pattern), recursive=True)
+        if len(files) != 1:
+            raise SystemExit(f"--summarize-trace: expected one {pattern} under {trace_dir}, found {files}")
+        with open(files[0]) as f:
+            return list(csv.DictReader(f))
+
+    ranges = [(r["Function"][len(TIMED_RANGE):], int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+              for r in one("*marker_api_trace.csv") if r["Function"].startswith(TIMED_RANGE)]
+    def short(name):
+        return re.sub(r"^void |\(.*$", "", name.replace("(anonymous namespace)::", ""))
+
+    kernels = [(short(r["Kernel_Name"]), int(r["Start_Timestamp"]), int(r["End_Timestamp"]))
+               for r in one("*kernel_trace.csv")]
+    print("| workload | kernel | calls | avg µs | min µs | max µs | kernel µs per step |")
+    print("|---|---|---|---|---|---|---|")
+    for label, t0, t1 in ranges:
+        per = {}
+        for name, k0, k1 in kernels:
+            if k0 >= t0 and k1 <= t1:
+                per.setdefault(name, []).append((k1 - k0) / 1e3)
+        steps = max((len(v) for v in per.values()), default=1)
+        for name, d in sorted(per.items(), key=lambda kv: -sum(kv[1])):
+            print(f"| {label} | `{name}` | {len(d)} | {sum(d) / len(d):.1f} | {min(d):.1f} | {max(d):.1f} | "
+                  f"{sum(d) / steps:.1f} |")
 
 
 def _rates(w, ms):
@@ -486,10 +542,8 @@ def cpu_baseline(target_s=10.0):
         el = time.perf_counter() - t0
         if el >= target_s or n >= 1000:
             break
-    if limiter is not None:
-        limiter.unregister() if hasattr(limiter, "unregister") else None
     per = el / n
-    return {
+    out = {
         "value": flop / per / 1e12,
         "unit": "TFLOP/s",
         "cores": threads,
@@ -497,10 +551,40 @@ def cpu_baseline(target_s=10.0):
         "sample": f"numpy restatement of xla_attention (256x256 tiles, causal tile skip, bf16 P "
                   f"rounding), one (b,h) slice 1x4096x1x128 of C2, {n} runs, {per * 1e3:.1f} ms each",
     }
+    # the decode half of the metric: a slice of C3 (its first sequences, the
+    # same seeded lengths), GB/s of the valid K/V rows + q + o it must read
+    nb, S, Hq, Hkv, D = 4, 8192, 32, 8, 128
+    lens = c3_lengths()[:nb]
+    q = oracle.round_bf16(rng.standard_normal((nb, 1, Hq, D), dtype=np.float32))
+    k, v = (oracle.round_bf16(rng.standard_normal((nb, S, Hkv, D), dtype=np.float32)) for _ in range(2))
+    nbytes = int(lens.sum()) * Hkv * D * 2 * 2 + 2 * nb * Hq * D * 2
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.xla_attention(q, k, v, mask=oracle.KVLenMask(lens), sm_scale=1 / math.sqrt(D), dtype="bf16")
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= target_s / 2 or n >= 1000:
+            break
+    if limiter is not None:
+        limiter.unregister() if hasattr(limiter, "unregister") else None
+    per = el / n
+    out["decode"] = {
+        "value": nbytes / per / 1e9,
+        "unit": "GB/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"numpy restatement of xla_attention with KVLenMask, bf16 P rounding: the first {nb} "
+                  f"of C3's 32 sequences (lengths {lens.tolist()}, Hq=32 over Hkv=8, D=128, capacity "
+                  f"{S}), {n} runs, {per * 1e3:.1f} ms each; GB/s of the valid K/V rows + q + o",
+    }
+    return out
 
 
 def main():
     args = _parse()
+    if args.summarize_trace:
+        summarize_trace(args.summarize_trace)
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (got --gpus {args.gpus}); "
               "the path's multi-GPU sharding is design-only", file=sys.stderr)
@@ -528,7 +612,7 @@ def main():
     head = None
     for key in only:
         w = MAKERS[key](dev, gen)
-        wall_ms, ev_ms = _time(w["fn"], args.steps, args.warmup, args.settle)
+        wall_ms, ev_ms = _time(w["fn"], args.steps, args.warmup, args.settle, label=key)
         tflops, gbs, frac = _rates(w, ev_ms)
         row = {"workload": w["name"], "ms": round(ev_ms, 5), "wall_ms": round(wall_ms, 5),
                "tflops": round(tflops, 2), "gbs": round(gbs, 1),
@@ -566,7 +650,7 @@ def main():
         r = results["C3"]
         out["decode_roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": PEAK_HBM_GBS,
                                   "unit": "GB/s", "frac": r["roofline_frac"],
-                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<pjx::Bf16Fmt, 128, 1>"),
+                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<pjx::Bf16Fmt, 128, 128, 1>"),
                                   "kernel": "gqa_decode_kernel<Bf16Fmt, 128, 128, 1> + decode_merge_kernel"}
     out["configs"] = results
     if not args.no_cpu_baseline:
