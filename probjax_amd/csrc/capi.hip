@@ -33,17 +33,26 @@ void note_launch(const char* name) {
 }
 
 // typeid(KernelTag<&kern<...>>) demangles to
-// "pjx::KernelTag<&(void pjx::kern<args>(params))>"; keeps "kern<args>"
+// "pjx::KernelTag<&(void pjx::kern<args>(params))>" for a template kernel and
+// "pjx::KernelTag<&pjx::kern>" for a plain one; keeps "kern<args>" / "kern"
 // without namespace qualifiers.
 std::string demangled_kernel_name(const char* mangled) {
   int st = 0;
   char* d = abi::__cxa_demangle(mangled, nullptr, nullptr, &st);
   std::string full = (st == 0 && d) ? d : mangled;
   free(d);
-  size_t b = full.find("void ");
-  b = b == std::string::npos ? 0 : b + 5;
-  size_t e = full.find('(', b);
-  std::string name = full.substr(b, e == std::string::npos ? std::string::npos : e - b);
+  for (size_t p; (p = full.find("(anonymous namespace)::")) != std::string::npos;) full.erase(p, 23);
+  const size_t t = full.find("KernelTag<");
+  std::string name = full;
+  if (t != std::string::npos) {
+    const size_t e = full.rfind('>');
+    name = full.substr(t + 10, e == std::string::npos || e < t + 10 ? std::string::npos : e - t - 10);
+  }
+  if (!name.empty() && name[0] == '&') name.erase(0, 1);
+  if (!name.empty() && name[0] == '(') name.erase(0, 1);
+  if (name.compare(0, 5, "void ") == 0) name.erase(0, 5);
+  const size_t paren = name.find('(');
+  if (paren != std::string::npos) name.erase(paren);
   for (size_t p; (p = name.find("pjx::")) != std::string::npos;) name.erase(p, 5);
   return name;
 }
