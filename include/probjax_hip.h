@@ -263,7 +263,8 @@ int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const voi
  * kv_lengths int32 [B] or NULL;
  * o [B, Lq, H, v_dim] of dtype = the first v_dim columns of mla(q, cache, None,
  * None) (v_dim == R gives the API-exact output); lse optional fp32 [B, H, Lq].
- * (rank, v_dim) in {(576, 512), (576, 576), (512, 512), (128, 128)}.  Any
+ * (rank, v_dim) in {(576, 512), (576, 576), (512, 512), (256, 256), (128, 128),
+ * (64, 64)}.  Any
  * Lq*H: each 16 folded rows form a row group that streams the cache chunk by
  * chunk (the reference's mla takes any head count, latent_attention.py:636-766).
  * chunk: keys per work item (0 = automatic, as for pjx_splitkv_decode; else a

@@ -58,7 +58,16 @@ LATENT_WIDTHS = (512, 576)  # latent ranks of the wide absorbed-mla kernels (16-
 # passes over it; longer query blocks run the latent flash kernels, whose
 # 128-row query tiles read it once per tile.
 MLA_DECODE_MAX_ROWS = 128
-MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))  # (rank, v_dim)
+MLA_SHAPES = ((576, 512), (576, 576), (512, 512), (256, 256), (128, 128), (64, 64))  # (rank, v_dim)
+
+
+def _mla_decode_shape(rank: int, v_dim: int):
+    """The latent decode kernel's (rank, v_dim) that carries a latent of width
+    ``rank`` and the first ``v_dim`` output columns: the narrowest rank >= rank
+    (zero-padded: zero features change no score), then the narrowest output
+    width >= v_dim (the extra columns are sliced off); None when too wide."""
+    fits = [(r, d) for r, d in MLA_SHAPES if r >= rank and d >= v_dim]
+    return min(fits) if fits else None
 BACKWARD_DTYPES = KERNEL_DTYPES  # dtypes pjx_flash_bwd takes
 
 # Split-KV decode thresholds (probjax kernels/attention.py:2649-2650).
@@ -725,8 +734,11 @@ def mla(q, cache, wk=None, wv=None, *, mask=None, bias=None, rng=None,
         raise ValueError(f"v_dim must be in [1, {R}], got {dv}")
     lengths = _latent_decode_lengths(q, cache, mask, bias, dv)
     if lengths is not None:
-        return hip.mla_decode(q, cache, sm_scale=float(sm_scale), v_dim=dv,
-                              kv_lengths=None if isinstance(lengths, str) else lengths)
+        rk, dvk = _mla_decode_shape(R, dv)
+        qk, ck = (q, cache) if rk == R else (_pad_features(q, rk), _pad_features(cache, rk))
+        out = hip.mla_decode(qk, ck, sm_scale=float(sm_scale), v_dim=dvk,
+                             kv_lengths=None if isinstance(lengths, str) else lengths)
+        return out if dvk == dv else out[..., :dv]
     return _mla_latent(q, cache, mask=mask, bias=bias, sm_scale=float(sm_scale), v_dim=dv)
 
 
@@ -734,13 +746,14 @@ def _latent_decode_lengths(q, cache, mask, bias, dv):
     """Per-batch KV lengths ("all" for none) when an absorbed call is a decode
     step the split-KV latent kernel computes exactly (no gradient, no bias,
     ``None`` / ``KVLenMask`` / one-row ``KeyPaddingMask``, bf16 / fp16, a rank and
-    output width it carries, ``Lq * H <= 128``); else None."""
+    output width it carries (zero-padded up to the next kernel rank,
+    ``_mla_decode_shape``), ``Lq * H <= 128``); else None."""
     B, l_q, H, R = q.shape
     if bias is not None or _needs_grad(q, cache):
         return None
     if q.dtype != cache.dtype or q.dtype not in HALF_DTYPES:
         return None
-    if (R, dv) not in MLA_SHAPES or l_q * H > MLA_DECODE_MAX_ROWS:
+    if _mla_decode_shape(R, dv) is None or l_q * H > MLA_DECODE_MAX_ROWS:
         return None
     lm = lower_mask(mask)
     if lm is None:

@@ -1033,8 +1033,11 @@ static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, siz
   if (rank == 576 && v_dim == 512) return run_decode<mla_decode_kernel<E, 576, 512>>(a, ws, ws_bytes, s, who);
   if (rank == 576 && v_dim == 576) return run_decode<mla_decode_kernel<E, 576, 576>>(a, ws, ws_bytes, s, who);
   if (rank == 512 && v_dim == 512) return run_decode<mla_decode_kernel<E, 512, 512>>(a, ws, ws_bytes, s, who);
+  if (rank == 256 && v_dim == 256) return run_decode<mla_decode_kernel<E, 256, 256>>(a, ws, ws_bytes, s, who);
   if (rank == 128 && v_dim == 128) return run_decode<mla_decode_kernel<E, 128, 128>>(a, ws, ws_bytes, s, who);
-  return fail(PJX_ERR_INVALID, "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (128,128)");
+  if (rank == 64 && v_dim == 64) return run_decode<mla_decode_kernel<E, 64, 64>>(a, ws, ws_bytes, s, who);
+  return fail(PJX_ERR_INVALID,
+              "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (256,256), (128,128), (64,64)");
 }
 
 // Argument checks shared by pjx_splitkv_decode and pjx_splitkv_decode_static

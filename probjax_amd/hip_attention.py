@@ -283,7 +283,7 @@ def splitkv_decode(
 
 
 # (rank, v_dim) pairs of the latent decode kernel (any number of folded rows).
-MLA_DECODE_SHAPES = ((576, 512), (576, 576), (512, 512), (128, 128))
+MLA_DECODE_SHAPES = ((576, 512), (576, 576), (512, 512), (256, 256), (128, 128), (64, 64))
 
 
 def mla_decode(
@@ -300,7 +300,7 @@ def mla_decode(
     code = _half_code("MLA decode", q, cache)
     dv = R if v_dim is None else int(v_dim)
     if (R, dv) not in MLA_DECODE_SHAPES:
-        raise ValueError(f"MLA decode supports (R, v_dim) in (576,512),(576,576),(512,512),(128,128); got ({R}, {dv})")
+        raise ValueError(f"MLA decode supports (R, v_dim) in {MLA_DECODE_SHAPES}; got ({R}, {dv})")
     S = cache.shape[1]
     q, cache = q.contiguous(), cache.contiguous()
     L = _lengths(kv_lengths, B, dev)

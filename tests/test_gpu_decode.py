@@ -66,6 +66,8 @@ def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, ch
         (1, 1, 16, 4096, 576, 512, [4096], 8192),            # one chunk: the chunk kernel writes the output
         (5, 1, 3, 257, 576, 576, [257, 256, 2, 128, 129], 128),  # 3 rows
         (6, 1, 4, 600, 512, 512, [600, 320, 320, 5, -1, 700], 128),  # ties, clamped lengths
+        (2, 1, 16, 900, 256, 256, [900, 33], 0),             # rank 256
+        (3, 1, 8, 500, 64, 64, [500, 0, 64], 128),           # rank 64, an empty sequence
     ],
 )
 def test_mla_decode_matches_oracle(device, b, lq, h, s, r, dv, lengths, chunk):
@@ -309,3 +311,30 @@ def test_splitkv_forward_head_dims(device):
     torch.cuda.synchronize()
     assert launched[0] == "gqa_decode_kernel<Bf16Fmt, 256, 256, 1>", launched
     assert max_abs(to_np(out), want2) <= BF16_TOL
+
+
+@pytest.mark.parametrize("r,dv,want_inst", [(200, 150, "mla_decode_kernel<Bf16Fmt, 256, 256>"),
+                                            (576, 300, "mla_decode_kernel<Bf16Fmt, 576, 512>"),
+                                            (40, 40, "mla_decode_kernel<Bf16Fmt, 64, 64>")])
+def test_mla_decode_route_pads_rank(device, r, dv, want_inst):
+    """Absorbed mla decode steps at a latent width between the kernel ranks
+    zero-pad q and the cache to the next rank (zero features change no score)
+    and slice the output columns, keeping the split-KV latent kernel."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd import native
+    from probjax_amd.masks import KVLenMask
+
+    b, h, s = 2, 16, 700
+    q, cache = (oracle.round_bf16(x) for x in rng_normal(17, (b, 1, h, r), (b, s, r)))
+    lengths = np.array([700, 255], np.int32)
+    scale = 1.0 / math.sqrt(192)
+    shared = cache[:, :, None, :]
+    want = oracle.xla_attention(q, shared, shared, mask=oracle.KVLenMask(lengths), sm_scale=scale)[..., :dv]
+    out = A.mla(to_dev(q, device, torch.bfloat16), to_dev(cache, device, torch.bfloat16), sm_scale=scale,
+                v_dim=dv, mask=KVLenMask(torch.from_numpy(lengths).to(device)))
+    launched = native.last_launches()
+    torch.cuda.synchronize()
+    assert launched[0] == want_inst, launched
+    assert out.shape == (b, 1, h, dv)
+    assert max_abs(to_np(out), want) <= BF16_TOL

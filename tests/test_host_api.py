@@ -461,3 +461,18 @@ def test_flax_empty_rows_fill():
     lse0 = torch.full((B, Hq, Lq), float("inf"))
     z = torch.zeros(B, Lq, Hq, D)
     assert torch.equal(A._flax_empty_rows(z, lse0, v0), z)
+
+
+def test_mla_decode_shape_rule():
+    """The latent decode's (rank, v_dim) for a latent width and output width:
+    the narrowest kernel rank that holds the width, then the narrowest output
+    width that holds the requested columns."""
+    assert A._mla_decode_shape(576, 512) == (576, 512)
+    assert A._mla_decode_shape(576, 576) == (576, 576)
+    assert A._mla_decode_shape(576, 300) == (576, 512)
+    assert A._mla_decode_shape(512, 512) == (512, 512)
+    assert A._mla_decode_shape(300, 300) == (512, 512)
+    assert A._mla_decode_shape(200, 150) == (256, 256)
+    assert A._mla_decode_shape(128, 128) == (128, 128)
+    assert A._mla_decode_shape(40, 40) == (64, 64)
+    assert A._mla_decode_shape(600, 512) is None
