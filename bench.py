@@ -183,7 +183,7 @@ def make_c3(dev, gen):
     fn = lambda: splitkv_decode(q, k, v, sm_scale=1 / math.sqrt(D), kv_lengths=L, workspace=ws)  # noqa: E731
     return dict(name="C3 GQA split-KV decode bf16 B=32 Hq=32 Hkv=8 D=128 S=8192 ragged",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="gqa_decode_kernel<Bf16Fmt, 128, 128, 1> + decode_merge_kernel", sum_len=tot)
+                kernel="gqa_decode_kernel<Bf16Fmt, 128, 128, 1, true> + decode_merge_kernel", sum_len=tot)
 
 
 def c4_lengths(seed=0, batch=2, length=2048):
@@ -650,8 +650,8 @@ def main():
         r = results["C3"]
         out["decode_roofline"] = {"bound": "hbm", "achieved": r["gbs"], "peak": PEAK_HBM_GBS,
                                   "unit": "GB/s", "frac": r["roofline_frac"],
-                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<pjx::Bf16Fmt, 128, 128, 1>"),
-                                  "kernel": "gqa_decode_kernel<Bf16Fmt, 128, 128, 1> + decode_merge_kernel"}
+                                  "traffic": measured_traffic("pjx::gqa_decode_kernel<pjx::Bf16Fmt, 128, 128, 1, true>"),
+                                  "kernel": "gqa_decode_kernel<Bf16Fmt, 128, 128, 1, true> + decode_merge_kernel"}
     out["configs"] = results
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline()

@@ -222,6 +222,10 @@ size_t pjx_decode_workspace_size(int64_t batch, int64_t groups, int64_t rows,
  * chunk: keys per work item (0 = automatic: a power of two in [128, 2048]
  *   leaving about 1024 items at full capacity; else a multiple of 128).
  * workspace: at least pjx_decode_workspace_size(B, Hkv, rows, Lk, Dv, chunk) bytes.
+ * Caches whose capacity B*Lk*Hkv*(D+Dv) exceeds 768 MiB of 16-bit data are
+ * read with non-temporal loads (they do not fit the 256 MB MALL); smaller
+ * ones with ordinary loads.  The environment variable PJX_DECODE_STREAM=0 or
+ * =1 forces either; results are identical.
  */
 int pjx_splitkv_decode(int dtype, const void* q, const void* k, const void* v,
                        const int32_t* kv_lengths, void* o, float* lse, void* workspace,

@@ -24,6 +24,7 @@
 // Inputs are bf16 or fp16 (the kernels are templated on the 16-bit format;
 // the v_mfma_*_bf16 named here are v_mfma_*_f16 for fp16) or fp32 (GQA only).
 #include <stdio.h>
+#include <stdlib.h>
 
 #include <atomic>
 
@@ -276,16 +277,30 @@ __device__ __forceinline__ void combine_rows(const DecodeArgs& a, float* red, co
 template <int D, int DV, int NRB>
 constexpr int decode_occupancy() { return (NRB == 4 || D > 128 || DV > 128) ? 1 : 2; }
 
-template <typename E, int D, int DV, int NRB>
+template <typename E, int D, int DV, int NRB, bool STREAM>
 __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_decode_kernel(DecodeArgs a) {
   constexpr int KSTEPS = D / 32;  // 32-dim MFMA k-steps of Q.K
   constexpr int NDB = DV / 16;    // 16-dim output blocks
   constexpr int DC = DV / 8;      // 16-byte chunks per V row
   constexpr int VU = DV / 64;     // (4 keys x 8 dims) V units per lane per 32 keys
   constexpr int VTS = 36;         // V^T row stride (16-bit elements): 32 keys + 4 pad
+  constexpr int CR = D / 8;       // 16-byte chunks per K row
+  constexpr int KLD = D / 16;     // K chunks per lane per 32-key step (32 * CR / 64 = 2 * KSTEPS)
   static_assert(D % 64 == 0 && DV % 64 == 0, "head dims");
   __shared__ __attribute__((aligned(16))) uint16_t vt_lds[4 * DV * VTS];
+  __shared__ __attribute__((aligned(16))) uint16_t k_lds[STREAM ? 4 * 32 * D : 8];  // per wave: 32 key rows
   static_assert(4 * DV * VTS * 2 >= 4 * 16 * DV * 4 + 4 * 16 * 2 * 4, "combine scratch fits");
+  // STREAM: chunk swizzle of K row r in the wave's K slab, a bijection of the
+  // row's 16-byte chunks that sends the same chunk of 16 consecutive rows to
+  // 16 different bank groups (rows of 128, 256 or 512 bytes)
+  auto kswz = [](int r) { return CR >= 16 ? (r & 15) : ((r >> 1) & (CR - 1)); };
+  // STREAM: K/V are read once per call, past what the 256 MB MALL holds, with
+  // non-temporal loads (measured on this layout: ~7.0 TB/s with full 128-byte
+  // lines, against ~5.9 TB/s for ordinary loads)
+  auto ld16 = [](const uint16_t* p) -> u32x4 {
+    if constexpr (STREAM) return __builtin_nontemporal_load((const u32x4*)p);
+    else return *(const u32x4*)p;
+  };
 
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int c16 = lane & 15, q4 = lane >> 4;
@@ -334,20 +349,44 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
     l_run[rb] = 0.f;
   }
 
-  u32x4 kr[2][KSTEPS];
+  // K: without STREAM, loaded straight into the A operand (kr[kb * KSTEPS + s]
+  // holds 16 bytes of key 16*kb + c16 at dims 32*s + 8*q4: each load covers
+  // 64 bytes of 16 rows).  With STREAM, rows are loaded whole (CR consecutive
+  // lanes per row, full 128-byte lines, which non-temporal loads need) into
+  // kr[i] = chunk u % CR of row u / CR, u = lane + 64*i, and staged through
+  // the wave's K slab, chunk c of row r at c ^ kswz(r).
+  u32x4 kr[KLD];
   u32x4 vr[VU][4];
+  uint16_t* kl = k_lds + (STREAM ? w * 32 * D : 0);
   auto load_k = [&](int k0) {
+    if constexpr (STREAM) {
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      const int key = k0 + 16 * kb + c16;
-      const bool ok = key < w1;
-      const uint16_t* p = Kb + (size_t)(ok ? key : 0) * k_tok + 8 * q4;
-#pragma unroll
-      for (int s = 0; s < KSTEPS; ++s) {
+      for (int i = 0; i < KLD; ++i) {
+        const int u = lane + 64 * i, key = k0 + u / CR;
         u32x4 r = {0u, 0u, 0u, 0u};
-        if (ok) r = *(const u32x4*)(p + 32 * s);
-        kr[kb][s] = r;
+        if (key < w1) r = ld16(Kb + (size_t)key * k_tok + 8 * (u % CR));
+        kr[i] = r;
       }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int key = k0 + 16 * kb + c16;
+        const bool ok = key < w1;
+        const uint16_t* p = Kb + (size_t)(ok ? key : 0) * k_tok + 8 * q4;
+#pragma unroll
+        for (int s = 0; s < KSTEPS; ++s) {
+          u32x4 r = {0u, 0u, 0u, 0u};
+          if (ok) r = *(const u32x4*)(p + 32 * s);
+          kr[kb * KSTEPS + s] = r;
+        }
+      }
+    }
+  };
+  auto store_k = [&]() {
+#pragma unroll
+    for (int i = 0; i < KLD; ++i) {
+      const int u = lane + 64 * i, row = u / CR;
+      *(u32x4*)(kl + row * D + 8 * ((u % CR) ^ kswz(row))) = kr[i];
     }
   };
   auto load_v = [&](int k0) {
@@ -359,7 +398,7 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
       for (int j = 0; j < 4; ++j) {
         const int key = k0 + 4 * kq + j;
         u32x4 r = {0u, 0u, 0u, 0u};
-        if (key < w1) r = *(const u32x4*)(Vb + (size_t)key * v_tok + 8 * dc);
+        if (key < w1) r = ld16(Vb + (size_t)key * v_tok + 8 * dc);
         vr[i][j] = r;
       }
     }
@@ -392,18 +431,44 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
   for (int k0 = w0; k0 < w1; k0 += 32) {
     const int kn = k0 + 32;
     store_vt();
-    if (kn < w1) load_v(kn);
-    // S^T for keys k0 + 16*kb + 4*q4 + r (register r), query row 16rb + c16.
+    if constexpr (STREAM) {
+      store_k();
+      wave_lds_sync();
+      if (kn < w1) {
+        load_v(kn);
+        load_k(kn);
+      }
+    } else {
+      if (kn < w1) load_v(kn);
+    }
+    // S^T for keys k0 + 16*kb + 4*q4 + r (register r), query row 16rb + c16;
+    // the A operand of k-step st: dims 32*st + 8*q4 of key 16*kb + c16.
     f32x4 s[NRB][2];
-#pragma unroll
-    for (int rb = 0; rb < NRB; ++rb)
+    if constexpr (STREAM) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        s[rb][kb] = f32x4{};
+        const int row = 16 * kb + c16;
 #pragma unroll
-        for (int st = 0; st < KSTEPS; ++st) s[rb][kb] = E::mma16(E::as8(kr[kb][st]), qf[rb][st], s[rb][kb]);
+        for (int st = 0; st < KSTEPS; ++st) {
+          const u32x4 kf = *(const u32x4*)(kl + row * D + 8 * ((4 * st + q4) ^ kswz(row)));
+#pragma unroll
+          for (int rb = 0; rb < NRB; ++rb)
+            s[rb][kb] = E::mma16(E::as8(kf), qf[rb][st], st == 0 ? f32x4{} : s[rb][kb]);
+        }
       }
-    if (kn < w1) load_k(kn);
+    } else {
+#pragma unroll
+      for (int rb = 0; rb < NRB; ++rb)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb) {
+          s[rb][kb] = f32x4{};
+#pragma unroll
+          for (int st = 0; st < KSTEPS; ++st)
+            s[rb][kb] = E::mma16(E::as8(kr[kb * KSTEPS + st]), qf[rb][st], s[rb][kb]);
+        }
+    }
+    if constexpr (!STREAM)
+      if (kn < w1) load_k(kn);
     if (kn > w1) {
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb)
@@ -995,12 +1060,19 @@ static int gqa_row_blocks(int64_t rows, int64_t head_dim, int64_t v_dim, bool f3
 }
 
 // One (D, DV) pair of the 16-bit GQA decode with nrb 16-row blocks per row group.
-template <typename E, int D, int DV>
-static int run_gqa_dims(DecodeArgs& a, int nrb, void* ws, size_t ws_bytes, hipStream_t s, const char* who) {
-  if (nrb == 1) return run_decode<gqa_decode_kernel<E, D, DV, 1>>(a, ws, ws_bytes, s, who);
-  if (nrb == 2) return run_decode<gqa_decode_kernel<E, D, DV, 2>>(a, ws, ws_bytes, s, who);
-  if constexpr (D <= 128 && DV <= 128) return run_decode<gqa_decode_kernel<E, D, DV, 4>>(a, ws, ws_bytes, s, who);
+template <typename E, int D, int DV, bool STREAM>
+static int run_gqa_nrb(DecodeArgs& a, int nrb, void* ws, size_t ws_bytes, hipStream_t s, const char* who) {
+  if (nrb == 1) return run_decode<gqa_decode_kernel<E, D, DV, 1, STREAM>>(a, ws, ws_bytes, s, who);
+  if (nrb == 2) return run_decode<gqa_decode_kernel<E, D, DV, 2, STREAM>>(a, ws, ws_bytes, s, who);
+  if constexpr (D <= 128 && DV <= 128) return run_decode<gqa_decode_kernel<E, D, DV, 4, STREAM>>(a, ws, ws_bytes, s, who);
   return fail(PJX_ERR_INVALID, "decode: row blocks");
+}
+
+template <typename E, int D, int DV>
+static int run_gqa_dims(DecodeArgs& a, int nrb, bool streamed, void* ws, size_t ws_bytes, hipStream_t s,
+                        const char* who) {
+  return streamed ? run_gqa_nrb<E, D, DV, true>(a, nrb, ws, ws_bytes, s, who)
+                  : run_gqa_nrb<E, D, DV, false>(a, nrb, ws, ws_bytes, s, who);
 }
 
 template <int D, int DV>
@@ -1012,12 +1084,12 @@ static int run_gqa_f32_dims(DecodeArgs& a, int nrb, void* ws, size_t ws_bytes, h
 // The GQA decode at (head_dim, v_dim), each in {64, 128, 256}: format E (bf16 /
 // fp16), or fp32 when F32.
 template <typename E, bool F32>
-static int run_gqa(DecodeArgs& a, int head_dim, int v_dim, int nrb, void* ws, size_t ws_bytes, hipStream_t s,
-                   const char* who) {
-#define PJX_GQA_DIMS(D, DV)                                                        \
-  if (head_dim == D && v_dim == DV) {                                              \
-    if constexpr (F32) return run_gqa_f32_dims<D, DV>(a, nrb, ws, ws_bytes, s, who); \
-    else return run_gqa_dims<E, D, DV>(a, nrb, ws, ws_bytes, s, who);              \
+static int run_gqa(DecodeArgs& a, int head_dim, int v_dim, int nrb, bool streamed, void* ws, size_t ws_bytes,
+                   hipStream_t s, const char* who) {
+#define PJX_GQA_DIMS(D, DV)                                                                   \
+  if (head_dim == D && v_dim == DV) {                                                         \
+    if constexpr (F32) return run_gqa_f32_dims<D, DV>(a, nrb, ws, ws_bytes, s, who);            \
+    else return run_gqa_dims<E, D, DV>(a, nrb, streamed, ws, ws_bytes, s, who);               \
   }
   PJX_GQA_DIMS(64, 64) PJX_GQA_DIMS(64, 128) PJX_GQA_DIMS(64, 256)
   PJX_GQA_DIMS(128, 64) PJX_GQA_DIMS(128, 128) PJX_GQA_DIMS(128, 256)
@@ -1038,6 +1110,21 @@ static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, siz
   if (rank == 64 && v_dim == 64) return run_decode<mla_decode_kernel<E, 64, 64>>(a, ws, ws_bytes, s, who);
   return fail(PJX_ERR_INVALID,
               "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (256,256), (128,128), (64,64)");
+}
+
+// Whether the 16-bit GQA decode streams K/V with non-temporal loads (the
+// STREAM kernels).  Ordinary loads leave the cache in the 256 MB MALL, which
+// repeated calls over a cache that (nearly) fits then hit: measured +3% to
+// +17% for STREAM at 537 MB of capacity (~290 MB valid); past that, STREAM
+// reads faster (-4% to -9% at 1 GB and more).  The lengths stay on the device,
+// so the rule uses the capacity: STREAM above kStreamBytes (3x the MALL).
+// PJX_DECODE_STREAM=0 / =1 in the environment forces either kernel.
+constexpr int64_t kStreamBytes = (int64_t)768 << 20;
+static bool decode_streams_kv(int64_t batch, int64_t kv_len, int64_t kv_heads, int64_t head_dim, int64_t v_dim) {
+  const char* env = getenv("PJX_DECODE_STREAM");
+  if (env && env[0] == '0' && env[1] == '\0') return false;
+  if (env && env[0] == '1' && env[1] == '\0') return true;
+  return batch * kv_len * kv_heads * (head_dim + v_dim) * 2 > kStreamBytes;
 }
 
 // Argument checks shared by pjx_splitkv_decode and pjx_splitkv_decode_static
@@ -1110,9 +1197,10 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   a.rpg = kRows * nrb;
   hipStream_t s = (hipStream_t)stream;
   const int d = (int)head_dim, dv = (int)v_dim;
-  if (f32) return run_gqa<Bf16Fmt, true>(a, d, dv, nrb, workspace, workspace_bytes, s, who);
-  return a.f16 ? run_gqa<F16Fmt, false>(a, d, dv, nrb, workspace, workspace_bytes, s, who)
-               : run_gqa<Bf16Fmt, false>(a, d, dv, nrb, workspace, workspace_bytes, s, who);
+  const bool streamed = !f32 && decode_streams_kv(batch, kv_len, kv_heads, head_dim, v_dim);
+  if (f32) return run_gqa<Bf16Fmt, true>(a, d, dv, nrb, false, workspace, workspace_bytes, s, who);
+  return a.f16 ? run_gqa<F16Fmt, false>(a, d, dv, nrb, streamed, workspace, workspace_bytes, s, who)
+               : run_gqa<Bf16Fmt, false>(a, d, dv, nrb, streamed, workspace, workspace_bytes, s, who);
 }
 
 // ---------------------------------------------------------------------------

@@ -33,9 +33,16 @@ BF16_TOL = 2e-2
         (300, 1, 256, 4, 1, 64, [(37 * i) % 300 - 20 for i in range(300)], 128),
     ],
 )
-def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, chunk):
+@pytest.mark.parametrize("streamed", ["0", "1"])
+def test_splitkv_decode_matches_oracle(device, monkeypatch, streamed, b, lq, s, hq, hkv, d, lengths, chunk):
+    """Both GQA decode kernels: the one that leaves K/V cacheable and the
+    streaming one (non-temporal loads, K staged through LDS), which the
+    capacity rule picks past 768 MiB of K/V and PJX_DECODE_STREAM forces."""
     import torch
+    from probjax_amd import native
     from probjax_amd.hip_attention import splitkv_decode
+
+    monkeypatch.setenv("PJX_DECODE_STREAM", streamed)
 
     q, k, v = (oracle.round_bf16(x) for x in rng_normal(10, (b, lq, hq, d), (b, s, hkv, d), (b, s, hkv, d)))
     scale = 1.0 / math.sqrt(d)
@@ -45,7 +52,11 @@ def test_splitkv_decode_matches_oracle(device, b, lq, s, hq, hkv, d, lengths, ch
     L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
     got, lse = splitkv_decode(*(to_dev(x, device, torch.bfloat16) for x in (q, k, v)), sm_scale=scale,
                               kv_lengths=L, chunk=chunk, return_lse=True)
+    launched = native.last_launches()
     torch.cuda.synchronize()
+    if b > 0:
+        assert launched[0].startswith("gqa_decode_kernel<Bf16Fmt") and launched[0].endswith(
+            ", true>" if streamed == "1" else ", false>"), launched
     assert max_abs(to_np(got), want) <= BF16_TOL
     lse = to_np(lse)
     np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))  # empty rows: +inf
@@ -177,17 +188,17 @@ def test_wide_and_fp32_decode_route_to_splitkv(device, monkeypatch, dtype):
 # rows run as several row groups over the same keys (the reference's row
 # blocks, attention_splitkv.py:155-172).
 WIDE_CASES = [
-    ("bf16", 2, 1, 1500, 8, 2, 256, 256, [1500, 333], 256, "gqa_decode_kernel<Bf16Fmt, 256, 256, 1>"),
-    ("bf16", 3, 2, 1100, 32, 2, 256, 256, [1100, 0, 517], 0, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2>"),
-    ("f16", 2, 1, 900, 16, 4, 256, 128, [900, 129], 128, "gqa_decode_kernel<F16Fmt, 256, 128, 1>"),
-    ("bf16", 2, 3, 800, 8, 1, 128, 64, [800, 64], 128, "gqa_decode_kernel<Bf16Fmt, 128, 64, 2>"),
-    ("bf16", 2, 1, 1000, 8, 2, 64, 128, None, 256, "gqa_decode_kernel<Bf16Fmt, 64, 128, 1>"),
-    ("bf16", 1, 2, 700, 16, 1, 64, 256, [650], 128, "gqa_decode_kernel<Bf16Fmt, 64, 256, 2>"),
+    ("bf16", 2, 1, 1500, 8, 2, 256, 256, [1500, 333], 256, "gqa_decode_kernel<Bf16Fmt, 256, 256, 1, false>"),
+    ("bf16", 3, 2, 1100, 32, 2, 256, 256, [1100, 0, 517], 0, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2, false>"),
+    ("f16", 2, 1, 900, 16, 4, 256, 128, [900, 129], 128, "gqa_decode_kernel<F16Fmt, 256, 128, 1, false>"),
+    ("bf16", 2, 3, 800, 8, 1, 128, 64, [800, 64], 128, "gqa_decode_kernel<Bf16Fmt, 128, 64, 2, false>"),
+    ("bf16", 2, 1, 1000, 8, 2, 64, 128, None, 256, "gqa_decode_kernel<Bf16Fmt, 64, 128, 1, false>"),
+    ("bf16", 1, 2, 700, 16, 1, 64, 256, [650], 128, "gqa_decode_kernel<Bf16Fmt, 64, 256, 2, false>"),
     # row groups: 128 rows (two groups of 64), 96 rows (a partial second group)
-    ("bf16", 2, 16, 1200, 16, 2, 128, 128, [1200, 301], 0, "gqa_decode_kernel<Bf16Fmt, 128, 128, 4>"),
-    ("f16", 2, 3, 1000, 64, 2, 64, 64, [1000, 1], 256, "gqa_decode_kernel<F16Fmt, 64, 64, 4>"),
+    ("bf16", 2, 16, 1200, 16, 2, 128, 128, [1200, 301], 0, "gqa_decode_kernel<Bf16Fmt, 128, 128, 4, false>"),
+    ("f16", 2, 3, 1000, 64, 2, 64, 64, [1000, 1], 256, "gqa_decode_kernel<F16Fmt, 64, 64, 4, false>"),
     # D = 256 with 72 rows: three groups of 32, the last partial
-    ("bf16", 2, 9, 600, 16, 2, 256, 256, [600, 300], 128, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2>"),
+    ("bf16", 2, 9, 600, 16, 2, 256, 256, [600, 300], 128, "gqa_decode_kernel<Bf16Fmt, 256, 256, 2, false>"),
     # fp32: groups of 32 rows; D / Dv up to 256
     ("f32", 2, 6, 900, 16, 2, 128, 128, [900, 450], 256, "gqa_decode_f32_kernel<128, 128, 2>"),
     ("f32", 2, 1, 1300, 8, 2, 256, 256, [1300, 77], 0, "gqa_decode_f32_kernel<256, 256, 1>"),
@@ -238,6 +249,17 @@ def test_splitkv_decode_head_dims_and_row_groups(device, dtype, b, lq, s, hq, hk
     np.testing.assert_array_equal(np.isposinf(lse), np.isposinf(want_lse))
     fin = np.isfinite(want_lse)
     assert max_abs(lse[fin], want_lse[fin]) <= (1e-3 if low else 1e-5)
+
+
+@pytest.mark.parametrize("dtype,b,lq,s,hq,hkv,d,dv,lengths,chunk,inst", [c for c in WIDE_CASES if c[0] != "f32"])
+def test_splitkv_decode_streamed_head_dims_and_row_groups(device, monkeypatch, dtype, b, lq, s, hq, hkv, d, dv,
+                                                          lengths, chunk, inst):
+    """The streaming GQA decode instances at every head-dim pair and row-block
+    count of the cases above (forced with PJX_DECODE_STREAM=1), to the same
+    bar against the oracle."""
+    monkeypatch.setenv("PJX_DECODE_STREAM", "1")
+    test_splitkv_decode_head_dims_and_row_groups(device, dtype, b, lq, s, hq, hkv, d, dv, lengths, chunk,
+                                                 inst.replace(", false>", ", true>"))
 
 
 @pytest.mark.parametrize(
@@ -309,7 +331,7 @@ def test_splitkv_forward_head_dims(device):
     out = A.mha(tq, tk, to_dev(v2, device, torch.bfloat16), mask=KVLenMask(L), sm_scale=scale)
     launched = native.last_launches()
     torch.cuda.synchronize()
-    assert launched[0] == "gqa_decode_kernel<Bf16Fmt, 256, 256, 1>", launched
+    assert launched[0] == "gqa_decode_kernel<Bf16Fmt, 256, 256, 1, false>", launched
     assert max_abs(to_np(out), want2) <= BF16_TOL
 
 
@@ -338,3 +360,26 @@ def test_mla_decode_route_pads_rank(device, r, dv, want_inst):
     assert launched[0] == want_inst, launched
     assert out.shape == (b, 1, h, dv)
     assert max_abs(to_np(out), want) <= BF16_TOL
+
+
+@pytest.mark.parametrize("dtype,d,dv,lq", [("bf16", 128, 128, 1), ("f16", 64, 256, 2), ("bf16", 256, 64, 5)])
+def test_streamed_decode_is_bitwise_equal(device, monkeypatch, dtype, d, dv, lq):
+    """The streaming and the ordinary GQA decode kernels compute the same
+    products in the same order: outputs and LSE are bitwise equal."""
+    import torch
+    from probjax_amd import native
+    from probjax_amd.hip_attention import splitkv_decode
+
+    b, s, hq, hkv = 3, 1700, 16, 2
+    tdt = torch.bfloat16 if dtype == "bf16" else torch.float16
+    q, k, v = (to_dev(x, device, tdt) for x in rng_normal(17, (b, lq, hq, d), (b, s, hkv, d), (b, s, hkv, dv)))
+    L = torch.tensor([1700, 999, 37], dtype=torch.int32, device=device)
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("PJX_DECODE_STREAM", flag)
+        out[flag] = splitkv_decode(q, k, v, sm_scale=0.1, kv_lengths=L, chunk=256, return_lse=True)
+        launched = native.last_launches()
+        assert launched[0].endswith(", true>" if flag == "1" else ", false>"), launched
+    torch.cuda.synchronize()
+    assert torch.equal(out["0"][0], out["1"][0])
+    assert torch.equal(out["0"][1], out["1"][1])
