@@ -222,7 +222,7 @@ def make_c5(dev, gen):
     fn = lambda: mla_decode(q, cache, sm_scale=1 / math.sqrt(192), v_dim=DV, workspace=ws)  # noqa: E731
     return dict(name="C5 MLA absorbed decode bf16 B=16 H=16 S=4096 R=576 Dv=512",
                 fn=fn, flop=flop, bytes=nbytes, bound="hbm", dtype="bf16",
-                kernel="mla_decode_kernel<Bf16Fmt,576,512> + decode_merge_kernel")
+                kernel="mla_decode_kernel<Bf16Fmt, 576, 512, false> + decode_merge_kernel")
 
 
 def _c2_train_inputs(dev, gen):

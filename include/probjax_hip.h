@@ -138,7 +138,7 @@ const char* pjx_last_launches(void);
  * mods: extended masks / score modifiers (pjx_score_mods) or NULL.
  *
  * dtype: PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 for q, k, v, o.  head_dim
- * in {64, 128}, or 256 in bf16 / fp16 (k and v share it; the reference's fused path takes
+ * in {64, 128, 256} (k and v share it; the reference's fused path takes
  * head_dim <= 256, layers/attention.py:1193-1195).  sm_scale must be > 0.
  */
 int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* o,
@@ -181,7 +181,7 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.  mods: the
  * forward's (pjx_score_mods) or NULL.
  * dtype: PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 (all fp32 products, no
- * roundings).  head_dim in {64, 128}, or 256 in bf16 / fp16.
+ * roundings).  head_dim in {64, 128, 256}.
  */
 int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                   const void* dout, const float* lse, void* dq, void* dk, void* dv,
@@ -275,6 +275,9 @@ int pjx_splitkv_decode_static(int dtype, const void* q, const void* k, const voi
  *   multiple of 64).
  * workspace: at least pjx_decode_workspace_size(B, 1, Lq*H, S, v_dim, chunk)
  * bytes with the same chunk.
+ * Latents of more than 512 MiB (B*S*R 16-bit values) are read with
+ * non-temporal loads, smaller ones with ordinary loads; PJX_DECODE_STREAM=0
+ * or =1 forces either, with identical results.
  */
 int pjx_mla_decode(int dtype, const void* q, const void* cache, const int32_t* kv_lengths,
                    void* o, float* lse, void* workspace, size_t workspace_bytes,

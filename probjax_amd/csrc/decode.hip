@@ -720,7 +720,7 @@ struct LatentTile {
   }
 };
 
-template <typename E, int D, int DV>
+template <typename E, int D, int DV, bool STREAM>
 __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a) {
   using T = LatentTile<D>;
   constexpr int BK = T::BK, ROWB = T::ROWB, NLD = T::NLD, GRP = T::GRP;
@@ -805,7 +805,11 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
     const uint32_t bytes = __builtin_amdgcn_readfirstlane(max(0, min(BK, c1 - k0)) * ROWB);
     const rsrc_t rs = make_rsrc(Kb + (size_t)k0 * ROWB, bytes);
 #pragma unroll
-    for (int j = 0; j < NLD; ++j) buffer_load_lds16(rs, ks + (NLD * w + j) * 1024, voff[j]);
+    for (int j = 0; j < NLD; ++j) {
+      // STREAM: non-temporal loads for caches past the MALL (as in gqa_decode_kernel)
+      if constexpr (STREAM) buffer_load_lds16_nt(rs, ks + (NLD * w + j) * 1024, voff[j]);
+      else buffer_load_lds16(rs, ks + (NLD * w + j) * 1024, voff[j]);
+    }
   };
 
   // One tile: wave w forms S^T for its 16 keys and shares it; every wave runs
@@ -1098,33 +1102,45 @@ static int run_gqa(DecodeArgs& a, int head_dim, int v_dim, int nrb, bool streame
   return fail(PJX_ERR_INVALID, "decode: head_dim and v_dim must be 64, 128 or 256");
 }
 
-// The latent decode (format E) at one (rank, v_dim).
-template <typename E>
-static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, size_t ws_bytes, hipStream_t s) {
+// The latent decode (format E) at one (rank, v_dim); STREAM instances when
+// `streamed`.
+template <typename E, bool STREAM>
+static int run_mla_rank(DecodeArgs& a, int64_t rank, int64_t v_dim, void* ws, size_t ws_bytes, hipStream_t s) {
   const char* who = "pjx_mla_decode";
-  if (rank == 576 && v_dim == 512) return run_decode<mla_decode_kernel<E, 576, 512>>(a, ws, ws_bytes, s, who);
-  if (rank == 576 && v_dim == 576) return run_decode<mla_decode_kernel<E, 576, 576>>(a, ws, ws_bytes, s, who);
-  if (rank == 512 && v_dim == 512) return run_decode<mla_decode_kernel<E, 512, 512>>(a, ws, ws_bytes, s, who);
-  if (rank == 256 && v_dim == 256) return run_decode<mla_decode_kernel<E, 256, 256>>(a, ws, ws_bytes, s, who);
-  if (rank == 128 && v_dim == 128) return run_decode<mla_decode_kernel<E, 128, 128>>(a, ws, ws_bytes, s, who);
-  if (rank == 64 && v_dim == 64) return run_decode<mla_decode_kernel<E, 64, 64>>(a, ws, ws_bytes, s, who);
+  if (rank == 576 && v_dim == 512) return run_decode<mla_decode_kernel<E, 576, 512, STREAM>>(a, ws, ws_bytes, s, who);
+  if (rank == 576 && v_dim == 576) return run_decode<mla_decode_kernel<E, 576, 576, STREAM>>(a, ws, ws_bytes, s, who);
+  if (rank == 512 && v_dim == 512) return run_decode<mla_decode_kernel<E, 512, 512, STREAM>>(a, ws, ws_bytes, s, who);
+  if (rank == 256 && v_dim == 256) return run_decode<mla_decode_kernel<E, 256, 256, STREAM>>(a, ws, ws_bytes, s, who);
+  if (rank == 128 && v_dim == 128) return run_decode<mla_decode_kernel<E, 128, 128, STREAM>>(a, ws, ws_bytes, s, who);
+  if (rank == 64 && v_dim == 64) return run_decode<mla_decode_kernel<E, 64, 64, STREAM>>(a, ws, ws_bytes, s, who);
   return fail(PJX_ERR_INVALID,
               "pjx_mla_decode: supported (rank, v_dim): (576,512), (576,576), (512,512), (256,256), (128,128), (64,64)");
 }
 
-// Whether the 16-bit GQA decode streams K/V with non-temporal loads (the
-// STREAM kernels).  Ordinary loads leave the cache in the 256 MB MALL, which
+template <typename E>
+static int run_mla_h16(DecodeArgs& a, int64_t rank, int64_t v_dim, bool streamed, void* ws, size_t ws_bytes,
+                       hipStream_t s) {
+  return streamed ? run_mla_rank<E, true>(a, rank, v_dim, ws, ws_bytes, s)
+                  : run_mla_rank<E, false>(a, rank, v_dim, ws, ws_bytes, s);
+}
+
+// Whether the 16-bit GQA and latent decodes stream the cache with
+// non-temporal loads (the STREAM kernels).  Ordinary loads leave the cache in the 256 MB MALL, which
 // repeated calls over a cache that (nearly) fits then hit: measured +3% to
 // +17% for STREAM at 537 MB of capacity (~290 MB valid); past that, STREAM
 // reads faster (-4% to -9% at 1 GB and more).  The lengths stay on the device,
 // so the rule uses the capacity: STREAM above kStreamBytes (3x the MALL).
+// The latent decode reads every cached row whole (no ragged tail in the
+// measured cases) and crosses over earlier: STREAM measured +1% at 302 MB and
+// -10% at 604 MB of latent (R = 576), so its threshold is kStreamBytesLatent.
 // PJX_DECODE_STREAM=0 / =1 in the environment forces either kernel.
 constexpr int64_t kStreamBytes = (int64_t)768 << 20;
-static bool decode_streams_kv(int64_t batch, int64_t kv_len, int64_t kv_heads, int64_t head_dim, int64_t v_dim) {
+constexpr int64_t kStreamBytesLatent = (int64_t)512 << 20;
+static bool decode_streams_kv(int64_t cache_bytes, int64_t threshold) {
   const char* env = getenv("PJX_DECODE_STREAM");
   if (env && env[0] == '0' && env[1] == '\0') return false;
   if (env && env[0] == '1' && env[1] == '\0') return true;
-  return batch * kv_len * kv_heads * (head_dim + v_dim) * 2 > kStreamBytes;
+  return cache_bytes > threshold;
 }
 
 // Argument checks shared by pjx_splitkv_decode and pjx_splitkv_decode_static
@@ -1197,7 +1213,7 @@ extern "C" int pjx_splitkv_decode(int dtype, const void* q, const void* k, const
   a.rpg = kRows * nrb;
   hipStream_t s = (hipStream_t)stream;
   const int d = (int)head_dim, dv = (int)v_dim;
-  const bool streamed = !f32 && decode_streams_kv(batch, kv_len, kv_heads, head_dim, v_dim);
+  const bool streamed = !f32 && decode_streams_kv(batch * kv_len * kv_heads * (head_dim + v_dim) * 2, kStreamBytes);
   if (f32) return run_gqa<Bf16Fmt, true>(a, d, dv, nrb, false, workspace, workspace_bytes, s, who);
   return a.f16 ? run_gqa<F16Fmt, false>(a, d, dv, nrb, streamed, workspace, workspace_bytes, s, who)
                : run_gqa<Bf16Fmt, false>(a, d, dv, nrb, streamed, workspace, workspace_bytes, s, who);
@@ -1297,6 +1313,8 @@ extern "C" int pjx_mla_decode(int dtype, const void* q, const void* cache,
     return write_keyless(o, lse, (size_t)(batch * q_len * heads * v_dim), false, (size_t)(batch * heads * q_len), s,
                          "pjx_mla_decode");
   a.f16 = dtype == PJX_DTYPE_F16;
-  return a.f16 ? run_mla_h16<F16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s)
-               : run_mla_h16<Bf16Fmt>(a, rank, v_dim, workspace, workspace_bytes, s);
+  // the latent is K and V at once: capacity B * S * R 16-bit values
+  const bool streamed = decode_streams_kv(batch * kv_len * rank * 2, kStreamBytesLatent);
+  return a.f16 ? run_mla_h16<F16Fmt>(a, rank, v_dim, streamed, workspace, workspace_bytes, s)
+               : run_mla_h16<Bf16Fmt>(a, rank, v_dim, streamed, workspace, workspace_bytes, s);
 }

@@ -116,6 +116,12 @@ __device__ __forceinline__ void buffer_load_lds16(rsrc_t r, void* lds_wave, uint
                                            voffset, soffset, 0, 0);
 }
 
+// buffer_load_lds16 with the non-temporal hint (data read once per call).
+__device__ __forceinline__ void buffer_load_lds16_nt(rsrc_t r, void* lds_wave, uint32_t voffset) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 16,
+                                           voffset, 0, 0, 2 /* nt */);
+}
+
 // Each lane loads 4 bytes at voffset; lane l's bytes land at lds_wave + 4*l.
 __device__ __forceinline__ void buffer_load_lds4(rsrc_t r, void* lds_wave, uint32_t voffset) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_wave, 4,

@@ -271,14 +271,18 @@ def test_splitkv_decode_streamed_head_dims_and_row_groups(device, monkeypatch, d
         (2, 1, 20, 800, 128, 128, [800, 17], 0),             # 20 rows: a partial second group
     ],
 )
-def test_mla_decode_row_groups(device, b, lq, h, s, r, dv, lengths, chunk):
+@pytest.mark.parametrize("streamed", ["0", "1"])
+def test_mla_decode_row_groups(device, monkeypatch, streamed, b, lq, h, s, r, dv, lengths, chunk):
     """The latent decode past 16 folded rows: each 16 rows form a row group
     streaming the cache chunk by chunk (the reference's mla takes any head
-    count, latent_attention.py:636-766), against the oracle within 2e-2."""
+    count, latent_attention.py:636-766), against the oracle within 2e-2; both
+    the cacheable kernel and the streaming one (non-temporal loads), which the
+    capacity rule picks past 512 MiB of latent and PJX_DECODE_STREAM forces."""
     import torch
     from probjax_amd import native
     from probjax_amd.hip_attention import mla_decode
 
+    monkeypatch.setenv("PJX_DECODE_STREAM", streamed)
     print(f"MLA decode B={b} Lq={lq} H={h} S={s} R={r} Dv={dv} rows={lq * h}", flush=True)
     q, cache = (oracle.round_bf16(x) for x in rng_normal(14, (b, lq, h, r), (b, s, r)))
     scale = 1.0 / math.sqrt(192)
@@ -292,7 +296,7 @@ def test_mla_decode_row_groups(device, b, lq, h, s, r, dv, lengths, chunk):
                           sm_scale=scale, v_dim=dv, kv_lengths=L, chunk=chunk, return_lse=True)
     launched = native.last_launches()
     torch.cuda.synchronize()
-    assert launched[0] == f"mla_decode_kernel<Bf16Fmt, {r}, {dv}>", launched
+    assert launched[0] == f"mla_decode_kernel<Bf16Fmt, {r}, {dv}, {'true' if streamed == '1' else 'false'}>", launched
     err = max_abs(to_np(got), want)
     print(f"  max-abs {err:.3e}", flush=True)
     assert err <= BF16_TOL
@@ -335,9 +339,9 @@ def test_splitkv_forward_head_dims(device):
     assert max_abs(to_np(out), want2) <= BF16_TOL
 
 
-@pytest.mark.parametrize("r,dv,want_inst", [(200, 150, "mla_decode_kernel<Bf16Fmt, 256, 256>"),
-                                            (576, 300, "mla_decode_kernel<Bf16Fmt, 576, 512>"),
-                                            (40, 40, "mla_decode_kernel<Bf16Fmt, 64, 64>")])
+@pytest.mark.parametrize("r,dv,want_inst", [(200, 150, "mla_decode_kernel<Bf16Fmt, 256, 256, false>"),
+                                            (576, 300, "mla_decode_kernel<Bf16Fmt, 576, 512, false>"),
+                                            (40, 40, "mla_decode_kernel<Bf16Fmt, 64, 64, false>")])
 def test_mla_decode_route_pads_rank(device, r, dv, want_inst):
     """Absorbed mla decode steps at a latent width between the kernel ranks
     zero-pad q and the cache to the next rank (zero features change no score)
@@ -380,6 +384,27 @@ def test_streamed_decode_is_bitwise_equal(device, monkeypatch, dtype, d, dv, lq)
         out[flag] = splitkv_decode(q, k, v, sm_scale=0.1, kv_lengths=L, chunk=256, return_lse=True)
         launched = native.last_launches()
         assert launched[0].endswith(", true>" if flag == "1" else ", false>"), launched
+    torch.cuda.synchronize()
+    assert torch.equal(out["0"][0], out["1"][0])
+    assert torch.equal(out["0"][1], out["1"][1])
+
+
+def test_streamed_mla_decode_is_bitwise_equal(device, monkeypatch):
+    """The streaming and the cacheable latent decode kernels differ only in the
+    load hint: outputs and LSE are bitwise equal."""
+    import torch
+    from probjax_amd import native
+    from probjax_amd.hip_attention import mla_decode
+
+    b, s, h, r, dv = 3, 1300, 24, 576, 512
+    q, cache = (to_dev(x, device, torch.bfloat16) for x in rng_normal(18, (b, 1, h, r), (b, s, r)))
+    L = torch.tensor([1300, 640, 5], dtype=torch.int32, device=device)
+    out = {}
+    for flag in ("0", "1"):
+        monkeypatch.setenv("PJX_DECODE_STREAM", flag)
+        out[flag] = mla_decode(q, cache, sm_scale=0.07, v_dim=dv, kv_lengths=L, return_lse=True)
+        launched = native.last_launches()
+        assert launched[0] == f"mla_decode_kernel<Bf16Fmt, {r}, {dv}, {'true' if flag == '1' else 'false'}>", launched
     torch.cuda.synchronize()
     assert torch.equal(out["0"][0], out["1"][0])
     assert torch.equal(out["0"][1], out["1"][1])
