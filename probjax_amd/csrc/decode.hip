@@ -824,11 +824,20 @@ __global__ __launch_bounds__(kDecThreads, 1) void mla_decode_kernel(DecodeArgs a
       const typename E::v8 kf = E::as8(*(const u32x4*)(ks + offK[st % SPG] + 16 * GRP * (st / SPG)));
       s = E::mma16(kf, qf[st], s);
     }
-    if (k0 + BK > c1) {
+    // Keys at or past c1 -> -inf, selected on every tile (a no-op on full
+    // ones) so that the score passes through the vector ALU before its LDS
+    // store.  Stored straight from the MFMA accumulator, one instruction
+    // after the last MFMA, the value written was sometimes not the finished
+    // one when other waves shared the SIMD's matrix pipe (ranks <= 256 run
+    // 2-7 workgroups per CU): wrong scores for 4 keys of a row, changing from
+    // run to run; 32 wait states before the store, or one workgroup per CU,
+    // made every result exact.  A vector-ALU read of an MFMA result is
+    // covered by the compiler's MFMA hazard waits; the LDS store's data read
+    // was not.
+    {
       const int lim = c1 - (k0 + 16 * w + 4 * q4);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
-        if (r >= lim) s[r] = -INFINITY;
+      for (int r = 0; r < 4; ++r) s[r] = r < lim ? s[r] : -INFINITY;
     }
     sx[w * 64 + lane] = s;
     stage_barrier();

@@ -408,3 +408,30 @@ def test_streamed_mla_decode_is_bitwise_equal(device, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(out["0"][0], out["1"][0])
     assert torch.equal(out["0"][1], out["1"][1])
+
+
+@pytest.mark.parametrize("r,lq,h", [(256, 2, 40), (128, 2, 40), (64, 2, 40), (256, 1, 64)])
+def test_mla_decode_shared_cu_repeatable(device, r, lq, h):
+    """Ranks <= 256 run several latent-decode workgroups per CU, whose waves
+    share each SIMD's matrix pipe.  With 128-key chunks (two tiles per item)
+    and several row groups, scores once reached their LDS exchange before the
+    last MFMA had finished with them: wrong terms for a few rows that changed
+    from run to run.  Four calls on the same inputs must agree bitwise and
+    with the oracle."""
+    import torch
+    from probjax_amd.hip_attention import mla_decode
+
+    b, s, chunk = 3, 2372, 128
+    print(f"latent decode repeat R={r} Lq={lq} H={h} S={s} chunk={chunk}", flush=True)
+    q, cache = (oracle.round_bf16(x) for x in rng_normal(404, (b, lq, h, r), (b, s, r)))
+    scale = 1.0 / math.sqrt(192)
+    shared = cache[:, :, None, :]
+    want, want_lse = oracle.xla_attention(q, shared, shared, sm_scale=scale, strategy="dense", dtype="bf16",
+                                          return_lse=True)
+    qd, cd = to_dev(q, device, torch.bfloat16), to_dev(cache, device, torch.bfloat16)
+    outs = [mla_decode(qd, cd, sm_scale=scale, v_dim=r, chunk=chunk, return_lse=True) for _ in range(4)]
+    torch.cuda.synchronize()
+    for o, lse in outs[1:]:
+        assert torch.equal(o, outs[0][0]) and torch.equal(lse, outs[0][1])
+    assert max_abs(to_np(outs[0][0]), want) <= BF16_TOL
+    assert max_abs(to_np(outs[0][1]), want_lse) <= 1e-4
