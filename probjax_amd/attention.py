@@ -43,7 +43,7 @@ import os
 import torch
 
 from . import hip_attention as hip
-from .masks import (LoweredBias, LoweredMask, dense_keep, dense_relpos, dense_supported, lower_bias,
+from .masks import (LoweredBias, LoweredMask, dense_distance, dense_keep, dense_relpos, dense_supported, lower_bias,
                     lower_mask, split_low_rank_bias)
 
 HIP_ARCH = "gfx950"
@@ -270,6 +270,12 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
     if lb is not None and lb.dense is not None:
         lb.dense = lb.dense.to(device=query.device, dtype=torch.float32)
     extra = [] if mask_bias is None else [mask_bias]
+    if lb is not None and lb.dense_more:
+        extra += [t.to(device=query.device, dtype=torch.float32) for t in lb.dense_more]
+        lb.dense_more = None
+    if lb is not None and lb.distance:
+        extra += [dense_distance(kind, alpha, h_q, l_q, key.shape[1], query.device) for kind, alpha in lb.distance]
+        lb.distance = None
     if lb is not None and lb.relpos:
         for term in lb.relpos:
             rows = (term.bias_table if hasattr(term, "bias_table") else term.table).shape[0]

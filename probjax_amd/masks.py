@@ -519,6 +519,8 @@ class LoweredBias:
     head_scales: object = None  # [H|1]
     constant: float = 0.0
     relpos: list = None  # T5 / learned relative-position terms, added to ``dense`` per call
+    distance: list = None  # further (kind, alpha) distance terms past the first, added to ``dense`` per call
+    dense_more: list = None  # further DenseBias tensors, added to ``dense`` per call
 
     @property
     def extended(self) -> bool:
@@ -558,20 +560,24 @@ def lower_bias(bias):
     for p in parts:
         pn = _name(p)
         if pn == "DenseBias":
-            if lb.dense is not None:
-                return False
             b = p.bias
-            lb.dense = b if isinstance(b, torch.Tensor) else torch.as_tensor(b)
+            b = b if isinstance(b, torch.Tensor) else torch.as_tensor(b)
+            if lb.dense is None:
+                lb.dense = b
+            else:  # a sum of dense terms: one tensor (SumBias, attention_mask_bias.py:551-577)
+                lb.dense_more = (lb.dense_more or []) + [b]
         elif pn == "ConstantBias":
             lb.constant += float(p.value)
         elif pn in ("T5RelativePositionBias", "LearnedRelativePositionBias"):
             lb.relpos = (lb.relpos or []) + [p]
         elif pn in ("CausalAlibiBias", "SymmetricAlibiBias", "DistanceDecayBias"):
-            if lb.alibi is not None:
-                return False
-            lb.alibi = {"CausalAlibiBias": "causal", "SymmetricAlibiBias": "symmetric",
-                        "DistanceDecayBias": "decay"}[pn]
-            lb.alibi_alpha = float(getattr(p, "alpha", 1.0))
+            kind = {"CausalAlibiBias": "causal", "SymmetricAlibiBias": "symmetric",
+                    "DistanceDecayBias": "decay"}[pn]
+            alpha = float(getattr(p, "alpha", 1.0))
+            if lb.alibi is None:
+                lb.alibi, lb.alibi_alpha = kind, alpha
+            else:  # the kernels evaluate one distance term; further ones go dense
+                lb.distance = (lb.distance or []) + [(kind, alpha)]
     return lb
 
 
@@ -718,6 +724,19 @@ def _t5_bucket_lut(rel, num_buckets, max_distance, bidirectional):
     ).astype(np.float32)
     large = np.minimum(nb - 1, large.astype(np.int64))
     return np.where(rp < max_exact, rp, large) + sign
+
+
+def dense_distance(kind, alpha, h_q, l_q, l_k, device):
+    """``[1, H|1, Lq, Lk]`` fp32 values of a distance bias: CausalAlibiBias
+    ``-2^-(h+1) * relu(q - k)`` (attention_mask_bias.py:2223-2255),
+    SymmetricAlibiBias ``-2^-(h+1) * |q - k|`` (:2355-2380) or
+    DistanceDecayBias ``-alpha * |q - k|`` (:2387-2414)."""
+    d = (torch.arange(l_q, device=device)[:, None] - torch.arange(l_k, device=device)[None, :]).to(torch.float32)
+    f = d.clamp_min(0.0) if kind == "causal" else d.abs()
+    if kind == "decay":
+        return (-float(alpha) * f)[None, None]
+    slopes = torch.pow(2.0, -(torch.arange(h_q, device=device, dtype=torch.float32) + 1.0))
+    return -(slopes[:, None, None] * f[None])[None]
 
 
 def dense_relpos(term, l_q, l_k, device):

@@ -259,11 +259,30 @@ def test_lower_score_modifiers():
     assert lb.alibi == "decay" and lb.alibi_alpha == 0.3 and lb.dense is not None
     assert M.lower_bias(M.SoftCappingBias(30.0)).softcap == 30.0
     assert M.lower_bias(M.PerHeadScaleBias([1.0, 2.0])).head_scales.tolist() == [1.0, 2.0]
-    # a non-additive modifier inside a sum, two dense biases, two ALiBi terms: not taken
+    # a non-additive modifier inside a sum: not taken
     assert M.lower_bias(M.SoftCappingBias(5.0) + M.ConstantBias(1.0)) is False
+    # two dense biases, or a second distance term: the first stays in the
+    # kernel, the rest are added to the dense bias per call
     d = M.DenseBias(torch.zeros(1, 1, 2, 2))
-    assert M.lower_bias(d + d) is False
-    assert M.lower_bias(M.CausalAlibiBias() + M.SymmetricAlibiBias()) is False
+    lb = M.lower_bias(d + d)
+    assert lb.dense is not None and len(lb.dense_more) == 1
+    lb = M.lower_bias(M.CausalAlibiBias() + M.SymmetricAlibiBias() + M.DistanceDecayBias(0.2))
+    assert lb.alibi == "causal" and lb.distance == [("symmetric", 1.0), ("decay", 0.2)]
+
+
+def test_dense_distance_matches_oracle():
+    import numpy as np
+
+    import oracle
+
+    for lq, lk in ((5, 5), (3, 9), (9, 2)):
+        for kind, mine in (("causal", oracle.CausalAlibiBias()), ("symmetric", oracle.SymmetricAlibiBias()),
+                           ("decay", oracle.DistanceDecayBias(0.37))):
+            got = M.dense_distance(kind, 0.37, 3, lq, lk, "cpu")[0]
+            assert got.shape[-2:] == (lq, lk) and got.shape[0] in (1, 3)
+            for h in range(3):
+                want = mine(np.zeros((lq, lk), np.float32), h, np.arange(lq), np.arange(lk))
+                np.testing.assert_allclose(got[h if got.shape[0] == 3 else 0].numpy(), want, rtol=0, atol=1e-6)
 
 
 def test_score_mods_arguments():
