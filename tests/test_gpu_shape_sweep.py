@@ -281,3 +281,69 @@ def test_latent_prefill_sweep(device, dt, b, lq, h, s, r, dv, causal, lengths):
                        kv_lengths=L, return_lse=True)
     torch.cuda.synchronize()
     _latent_check(got, lse, want[..., :dv], want_lse)
+
+
+def _latent_grad_cases(n, seed):
+    rng = np.random.default_rng(seed)
+    shapes = ((576, 512), (576, 576), (512, 512), (400, 400), (256, 256), (128, 128), (96, 96))
+    out = []
+    while len(out) < n:
+        r, dv = shapes[int(rng.integers(len(shapes)))]
+        dt = str(rng.choice(["bf16", "f16"] + (["f32"] if r <= 256 else [])))
+        b, h = int(rng.integers(1, 3)), int(rng.integers(1, 5))
+        lq, s = int(rng.integers(2, 260)), int(rng.integers(1, 330))
+        if b * h * lq * s * r > 6e7:
+            continue
+        mask = [None, "causal", "kvlen", "window"][int(rng.integers(4))]
+        bias = [None, None, "dense", "alibi"][int(rng.integers(4))]
+        out.append((dt, b, lq, h, s, r, dv, mask, bias))
+    return out
+
+
+@pytest.mark.parametrize("dt,b,lq,h,s,r,dv,mask,bias", _latent_grad_cases(20, 66))
+def test_latent_grad_sweep(device, dt, b, lq, h, s, r, dv, mask, bias):
+    """Absorbed ``mla(q, cache, None, None)`` with gradients (dq, dcache) over
+    random ranks (padded ones included), heads, lengths, masks and biases,
+    checked as tests/test_gpu_mla_latent.py checks its cases."""
+    import torch
+    from probjax_amd import attention as A
+    from probjax_amd import masks as M
+    from tests.test_gpu_mla_latent import _check_grads, _mask_objects
+
+    print(f"latent grads {dt} B={b} Lq={lq} H={h} S={s} R={r} Dv={dv} mask={mask} bias={bias}", flush=True)
+    q, cache, do = rng_normal(606, (b, lq, h, r), (b, s, r), (b, lq, h, dv))
+    low = dt != "f32"
+    if low:
+        q, cache, do = (oracle.round_to(x, dt) for x in (q, cache, do))
+    scale = 1.0 / math.sqrt(192 if r == 576 else r)
+    mm, om = _mask_objects(mask, b, lq, s, device)
+    mb = ob = None
+    if bias == "dense":
+        (bt,) = rng_normal(607, (1, h, lq, s), scale=0.5)
+        mb, ob = M.DenseBias(to_dev(bt, device, torch.float32)), oracle.DenseBias(bt)
+    elif bias == "alibi":
+        mb, ob = M.CausalAlibiBias(), oracle.CausalAlibiBias()
+    t = _tdt(dt)
+    tq, tc = (to_dev(x, device, t).requires_grad_(True) for x in (q, cache))
+    out = A.mla(tq, tc, None, None, mask=mm, bias=mb, sm_scale=scale, v_dim=dv)
+    (out.float() * to_dev(do, device, torch.float32)).sum().backward()
+    torch.cuda.synchronize()
+    shared = cache[:, :, None, :]
+    cdt = np.float32 if low else np.float64
+    want = oracle.xla_attention(q, shared, shared, mask=om, bias=ob, sm_scale=scale, strategy="dense",
+                                dtype="f32", compute_dtype=cdt)
+    err = max_abs(to_np(out), want[..., :dv])
+    print(f"  output max-abs {err:.3e}", flush=True)
+    assert err <= (HALF_TOL if low else F32_TOL)
+    dop = np.concatenate([do, np.zeros(do.shape[:-1] + (r - dv,), np.float32)], axis=-1)
+
+    def grads(mode, compute):
+        o, lse = oracle.xla_attention(q, shared, shared, mask=om, bias=ob, sm_scale=scale, strategy="dense",
+                                      dtype=mode, compute_dtype=compute, return_lse=True)
+        dq, dk, dv_ = attention_backward(q, shared, shared, o, dop, lse, mask=om, bias=ob, sm_scale=scale,
+                                         dtype=mode, compute_dtype=compute)
+        return np.asarray(dq, np.float64), (np.asarray(dk, np.float64) + np.asarray(dv_, np.float64))[:, :, 0]
+
+    exact = grads("f32", np.float64)
+    mode = grads(dt, np.float32) if low else (None, None)
+    _check_grads([("dq", to_np(tq.grad), exact[0], mode[0]), ("dcache", to_np(tc.grad), exact[1], mode[1])], low)
