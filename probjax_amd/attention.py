@@ -271,7 +271,12 @@ def _eligible(query, key, value, *, mask, bias, dropout_rate):
         lb.dense = lb.dense.to(device=query.device, dtype=torch.float32)
     extra = [] if mask_bias is None else [mask_bias]
     if lb is not None and lb.dense_more:
-        extra += [t.to(device=query.device, dtype=torch.float32) for t in lb.dense_more]
+        for t in lb.dense_more:
+            # each term of a dense sum must itself broadcast to [B, Hq, Lq, Lk]
+            if t.ndim != 4 or tuple(t.shape[-2:]) != (l_q, key.shape[1]) or t.shape[0] not in (1, B) \
+                    or t.shape[1] not in (1, h_q):
+                return None
+            extra.append(t.to(device=query.device, dtype=torch.float32))
         lb.dense_more = None
     if lb is not None and lb.distance:
         extra += [dense_distance(kind, alpha, h_q, l_q, key.shape[1], query.device) for kind, alpha in lb.distance]

@@ -150,6 +150,21 @@ def test_eligibility_rejects_without_touching_a_device(monkeypatch):
     assert A._flash_plan(q96, q96, q96, M.LoweredMask(), None) is None
 
 
+def test_bias_sums_lower_to_one_dense_term(monkeypatch):
+    """Several dense terms of a SumBias (any broadcast shapes) become one
+    tensor, a second distance term its dense values; a term that does not
+    broadcast to [B, Hq, Lq, Lk] makes the route fall through."""
+    monkeypatch.setattr(A, "hip_device", lambda t: True)
+    q, k = torch.zeros(2, 8, 2, 64), torch.zeros(2, 10, 2, 64)
+    b1, b2 = torch.randn(1, 2, 8, 10), torch.randn(2, 1, 8, 10)
+    _, lb = A._eligible(q, k, k, mask=None, bias=M.DenseBias(b1) + M.DenseBias(b2), dropout_rate=0.0)
+    assert torch.equal(lb.dense, b1 + b2)
+    _, lb = A._eligible(q, k, k, mask=None, bias=M.CausalAlibiBias() + M.DistanceDecayBias(0.5), dropout_rate=0.0)
+    assert lb.alibi == "causal" and torch.equal(lb.dense, M.dense_distance("decay", 0.5, 2, 8, 10, "cpu"))
+    bad = M.DenseBias(b1) + M.DenseBias(torch.zeros(3, 1, 8, 10))
+    assert A._eligible(q, k, k, mask=None, bias=bad, dropout_rate=0.0) is None
+
+
 def test_flex_attention_argument_checks():
     q, k, v = _qkv(hq=4, hkv=2)
     with pytest.raises(ValueError, match="same dtype"):
