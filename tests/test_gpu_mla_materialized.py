@@ -31,6 +31,9 @@ pytestmark = pytest.mark.gpu
     ("bf16", 1, 384, 4, 512, 128, 128, 128),
     ("bf16", 2, 33, 2, 12, 16, 12, 64),   # rank not a multiple of 8: element loads
     ("bf16", 2, 1900, 8, 72, 96, 64, 128),  # many tiles, ragged last row tile
+    ("bf16", 1, 4096, 16, 512, 128, 128, 128),     # the bench's C5P shape
+    ("bf16", 2, 2100, 12, 200, 100, 72, 128),      # ragged rows, padded head dims, rank 200
+    ("f16", 3, 1500, 20, 136, 64, 64, 64),         # 1280 columns: 5 column tiles
     ("f32", 2, 200, 3, 72, 40, 24, 64),
     ("f32", 1, 130, 2, 20, 64, 128, 128),
 ])
@@ -41,20 +44,27 @@ def test_projection_matches_numpy(device, dtype, B, S, H, R, dk, dv, width):
     print(f"project {dtype} B={B} S={S} H={H} R={R} dk={dk} dv={dv} width={width}", flush=True)
     cache, = rng_normal(60, (B, S, R))
     wk, wv = rng_normal(61, (H, dk, R), (H, dv, R), scale=1 / math.sqrt(R))
-    bf16 = dtype == "bf16"
+    from probjax_amd import native
+
+    bf16 = dtype != "f32"   # 16-bit (bf16 or fp16)
     if bf16:
-        cache, wk, wv = (oracle.round_bf16(x) for x in (cache, wk, wv))
-    tdt = torch.bfloat16 if bf16 else torch.float32
+        cache, wk, wv = (oracle.round_to(x, dtype) for x in (cache, wk, wv))
+    tdt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[dtype]
     k, v = hip.mla_project(*(to_dev(x, device, tdt) for x in (cache, wk, wv)), width=width)
+    launched = native.last_launches()
     torch.cuda.synchronize()
+    if bf16:
+        ring = R % 8 == 0
+        assert launched[0].startswith("mla_project_bf16_kernel" if ring else "mla_project_bf16_ragged_kernel"), launched
     for got, w, dim in ((k, wk, dk), (v, wv, dv)):
         got = to_np(got).astype(np.float64)
-        want = np.einsum("bsr,hdr->bshd", cache.astype(np.float64), w.astype(np.float64))
+        want = (cache.reshape(-1, R).astype(np.float64) @ w.reshape(-1, R).astype(np.float64).T).reshape(B, S, H, dim)
         assert got.shape == (B, S, H, width)
         assert not got[..., dim:].any(), "padded channels must be zero"
         err = np.abs(got[..., :dim] - want)
         if bf16:
-            assert (err <= 2.0 ** -7 * np.abs(want) + 1e-6).all(), f"max err {err.max():.3e}"
+            step = 2.0 ** -7 if dtype == "bf16" else 2.0 ** -10   # one 16-bit rounding step
+            assert (err <= step * np.abs(want) + 1e-6).all(), f"max err {err.max():.3e}"
         else:
             assert (err <= 1e-5 * np.maximum(1.0, np.abs(want))).all(), f"max err {err.max():.3e}"
 
