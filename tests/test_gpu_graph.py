@@ -1,9 +1,13 @@
-"""The kernels under HIP graph capture: a captured step (flash forward and
-backward, split-KV decode with a caller workspace, the no-allocation decode,
-the latent decode) replayed several times, with new inputs written in place
-and unrelated eager work between replays, must give what eager calls give on
-the same inputs, bitwise.  The library records no memset into a graph (zero
-fills are kernels), and its launches take the capturing stream.
+"""The kernels under HIP graph capture and under concurrent callers.
+
+* A captured step (flash forward and backward, split-KV decode with a caller
+  workspace, the no-allocation decode, the latent decode) replayed several
+  times, with new inputs written in place and unrelated eager work between
+  replays, must give what eager calls give on the same inputs, bitwise.  The
+  library records no memset into a graph (zero fills are kernels), and its
+  launches take the capturing stream.
+* Several host threads on their own streams at once (the boundary's
+  contract: handlers are stateless and reentrant) give what one thread gives.
 """
 
 import ctypes
@@ -74,3 +78,57 @@ def test_graph_replays_match_eager(device):
         torch.cuda.synchronize()
         for i, (a, b) in enumerate(zip(got, want)):
             assert torch.equal(a, b), f"replay {rep}, output {i}"
+
+
+def test_concurrent_host_threads_and_streams(device):
+    """The entry points keep no state between calls (error text and launch log
+    are per host thread): four host threads, each on its own stream, running
+    the forward, backward and split-KV decode on their own inputs at the same
+    time give what one thread gives on the same inputs, bitwise."""
+    import threading
+
+    import torch
+    from probjax_amd.hip_attention import flash_attention_bwd, flash_attention_fwd, splitkv_decode
+
+    g = torch.Generator(device=device)
+    g.manual_seed(91)
+    bf = torch.bfloat16
+
+    def make(i):
+        r = lambda *s: torch.randn(s, generator=g, device=device).to(bf)  # noqa: E731
+        return dict(q=r(1, 512 + 64 * i, 4, 128), k=r(1, 512 + 64 * i, 2, 128), v=r(1, 512 + 64 * i, 2, 128),
+                    do=r(1, 512 + 64 * i, 4, 128), qd=r(2, 1, 8, 64), kd=r(2, 3000, 1, 64), vd=r(2, 3000, 1, 64),
+                    L=torch.tensor([3000, 1111 * (i + 1)], dtype=torch.int32, device=device))
+
+    def work(x):
+        o, lse = flash_attention_fwd(x["q"], x["k"], x["v"], sm_scale=0.09, causal=True, return_lse=True)
+        dq, dk, dv = flash_attention_bwd(x["q"], x["k"], x["v"], o, x["do"], lse, sm_scale=0.09, causal=True)
+        od = splitkv_decode(x["qd"], x["kd"], x["vd"], sm_scale=0.12, kv_lengths=x["L"])
+        return [o, lse, dq, dk, dv, od]
+
+    inputs = [make(i) for i in range(4)]
+    want = [work(x) for x in inputs]
+    torch.cuda.synchronize()
+    got = [None] * 4
+    errors = []
+
+    def run(i):
+        try:
+            s = torch.cuda.Stream(device)
+            with torch.cuda.stream(s):
+                for _ in range(3):
+                    res = work(inputs[i])
+                s.synchronize()
+            got[i] = res
+        except Exception as e:  # surfaced below
+            errors.append(e)
+
+    threads = [threading.Thread(target=run, args=(i,)) for i in range(4)]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors, errors
+    for i in range(4):
+        for j, (a, b) in enumerate(zip(got[i], want[i])):
+            assert torch.equal(a, b), f"thread {i}, output {j}"
