@@ -43,12 +43,22 @@
 //
 // LDS rows are row-major [row][dim] with 16-byte chunks XOR-swizzled within
 // aligned groups of G chunks so that both read patterns of the 16x16 layout
-// are free of bank conflicts: 16 lanes reading one chunk of 16 consecutive
-// rows (b128 row fragments), and 32 lanes reading a 32-byte chunk pair of 8
-// consecutive rows (transposing reads).  Rows of whole 256-byte bank lines
-// (D = 256, 512; G = 16): swz(r) = 2(r&7) + ((r>>3)&1).  Rows of an odd
-// number of half lines (D = 576; G = 8), odd rows starting half a line later:
-// swz(r) = 2((r>>1)&3) + ((r>>3)&1).
+// are free of bank conflicts on gfx950's LDS (64 banks of 4 bytes):
+//   * row fragments (ds_read_b128; lane l reads chunk 4e + l/16 of row l%16):
+//     the LDS serves 16 lanes per cycle, lanes 0-7 with 24-31, 8-15 with
+//     16-23, 32-39 with 56-63 and 40-47 with 48-55 (measured with
+//     SQ_LDS_BANK_CONFLICT on probe patterns), so rows r and r+8 of chunks
+//     4e and 4e+1 (or 4e+2 and 4e+3) meet in one cycle and must take
+//     different 16-byte bank groups;
+//   * transposing reads (ds_read_b64_tr_b16): 32 lanes read a 32-byte chunk
+//     pair of 8 consecutive rows.
+// Rows of whole 256-byte bank lines (D = 256, 512; G = 16): swz(r) = 2(r&7),
+// which sends rows r < 8 of chunk 4e to even bank groups and rows r >= 8 of
+// chunk 4e+1 to odd ones.  Rows of an odd number of half lines (D = 576;
+// G = 8), odd rows starting half a line later: swz(r) = r&6.  (Swizzles that
+// are a bijection on the 16 rows of one chunk, such as 2(r&7) + ((r>>3)&1),
+// put those row pairs in one bank group: each row fragment read then takes
+// two LDS cycles per 16 lanes instead of one.)
 #include "flash_common.h"
 
 namespace pjx {
@@ -68,7 +78,7 @@ struct Row16 {
   static_assert(ROWB % 256 == 0 || ROWB % 256 == 128, "rows of whole or half bank lines");
   static_assert(NC % G == 0 && (kWT * NC) % 256 == 0, "tile shape");
   __device__ static int swz(int r) {
-    return FULL_LINES ? (((r & 7) << 1) | ((r >> 3) & 1)) : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
+    return FULL_LINES ? ((r & 7) << 1) : (r & 6);
   }
 };
 
@@ -276,6 +286,22 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
         for (int st = 0; st < VS; ++st) dp[kb] = E::mma16(ov.rows(vs, kb, st), dof[st], dp[kb]);
       }
     }
+    {
+      // Each row fragment read 6 reads ahead of its MFMAs.  Reads in program
+      // order: per kb, KS K rows (each feeding S, and dP for st < VS with the
+      // shared latent), then VS V rows.
+      constexpr int NR = 2 * (KS + (SHARED ? 0 : VS));
+      __builtin_amdgcn_sched_group_barrier(0x100, 6, 0);
+#pragma unroll
+      for (int i_ = 0; i_ < NR; ++i_) {
+        const int st_ = i_ % (NR / 2);
+        if (SHARED && st_ < VS)
+          __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+        else
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        if (i_ + 6 < NR) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+    }
     f32x4 dbv[2];
     const int kbase = k0 + 4 * qd;
     if constexpr (EXT == 2) {
@@ -361,6 +387,7 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dq_kernel(WideBwdArgs ba
     const typename E::v8 dsb = pack_slots<E>(s[0], s[1]);
 #pragma unroll
     for (int i = 0; i < ND; ++i) acc[i] = E::mma16(ok.trans(ks, i), dsb, acc[i]);
+    PJX_SCHED_LDS_READS_AHEAD(ND, 6, 2);  // transposed K fragments 6 MFMAs ahead
   };
 
   if (n_tiles > 0) issue(0, smem0);
@@ -777,6 +804,10 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
         for (int s = 0; s < VS; ++s)
           dpx[rb] = E::mma16(od.rows(dos, rb, s), SHARED ? kf[s] : vf[s], dpx[rb]);
       }
+      // Each MFMA's row fragment is read from LDS 6 MFMAs ahead (at one wave
+      // per SIMD the scheduler's own order waited for each read right before
+      // its MFMA).
+      PJX_SCHED_LDS_READS_AHEAD(2 * (KS + VS), 6, 1);
 #pragma unroll
       for (int rb = 0; rb < 2; ++rb) {
         const int q4 = q0 + 16 * rb + 4 * qd;
@@ -820,6 +851,16 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba
         }
       }
     }
+    // The 8 exchanged P / dS fragments and the first 3 blocks' transposed
+    // fragments first, then each block's 4 MFMAs followed by the reads of the
+    // block 3 ahead.
+    __builtin_amdgcn_sched_group_barrier(0x100, 8 + 2 * 3, 0);
+#pragma unroll
+    for (int g_ = 0; g_ < NJ + NJV - 3; ++g_) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+      __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    }
+    __builtin_amdgcn_sched_group_barrier(0x008, 4 * 3, 0);
   };
 
   // The ring of wide_bwd_dkdv_kernel; each compute adds one barrier between
