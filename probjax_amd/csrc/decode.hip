@@ -283,13 +283,15 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
   constexpr int NDB = DV / 16;    // 16-dim output blocks
   constexpr int DC = DV / 8;      // 16-byte chunks per V row
   constexpr int VU = DV / 64;     // (4 keys x 8 dims) V units per lane per 32 keys
-  constexpr int VTS = 36;         // V^T row stride (16-bit elements): 32 keys + 4 pad
   constexpr int CR = D / 8;       // 16-byte chunks per K row
   constexpr int KLD = D / 16;     // K chunks per lane per 32-key step (32 * CR / 64 = 2 * KSTEPS)
   static_assert(D % 64 == 0 && DV % 64 == 0, "head dims");
-  __shared__ __attribute__((aligned(16))) uint16_t vt_lds[4 * DV * VTS];
+  // Each wave's V^T tile: DV rows (output dims) of the step's 32 keys, 64
+  // bytes each, 4 rows to a 256-byte bank line (see vt_at); the same memory
+  // then holds the 4 waves' partial rows for the combine.
+  constexpr int VT_B = 4 * DV * 64, COMB_B = 4 * 16 * DV * 4 + 4 * 16 * 2 * 4;
+  __shared__ __attribute__((aligned(256))) uint16_t vt_lds[(VT_B > COMB_B ? VT_B : COMB_B) / 2];
   __shared__ __attribute__((aligned(16))) uint16_t k_lds[STREAM ? 4 * 32 * D : 8];  // per wave: 32 key rows
-  static_assert(4 * DV * VTS * 2 >= 4 * 16 * DV * 4 + 4 * 16 * 2 * 4, "combine scratch fits");
   // STREAM: chunk swizzle of K row r in the wave's K slab, a bijection of the
   // row's 16-byte chunks that sends the same chunk of 16 consecutive rows to
   // 16 different bank groups (rows of 128, 256 or 512 bytes)
@@ -335,7 +337,19 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
   const size_t k_tok = (size_t)a.G * D, v_tok = (size_t)a.G * DV;
   const uint16_t* Kb = a.k + ((size_t)b * a.Lk * a.G + g) * D;
   const uint16_t* Vb = a.v + ((size_t)b * a.Lk * a.G + g) * DV;
-  uint16_t* vl = vt_lds + w * DV * VTS;
+  uint16_t* vl = vt_lds + w * DV * 32;
+  // Element offset of 8-byte unit u (keys 4u .. 4u+3) of V^T row r.  The 32
+  // units of a 256-byte line (rows 4L .. 4L+3) are XOR-swizzled by F(L) so
+  // that both access patterns are free of bank conflicts: the writes of 16
+  // lanes (one LDS cycle for ds_write_b64) put one unit of rows 8*dc + e,
+  // dc = 0..15, in 16 different lines, whose F values all differ; the reads
+  // of 32 lanes (one cycle for ds_read_b64) take units u, u+1 of 16
+  // consecutive rows, 4 lines whose F values differ in bits 1-2.
+  auto vt_at = [](int row, int unit) {
+    const int L = row >> 2;
+    const int F = ((L & 3) << 1) | (((L >> 2) & 3) << 3) | ((L >> 4) & 1);
+    return 128 * L + 4 * ((8 * (row & 3) + unit) ^ F);
+  };
 
   f32x4 acc[NRB][NDB];
 #pragma unroll
@@ -419,7 +433,7 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
           pk[0] = pack_lo_halves(vr[i][0][dw], vr[i][1][dw]);
           pk[1] = pack_lo_halves(vr[i][2][dw], vr[i][3][dw]);
         }
-        *(u32x2*)(vl + (8 * dc + e) * VTS + 4 * kq) = pk;
+        *(u32x2*)(vl + vt_at(8 * dc + e, kq)) = pk;
       }
     }
   };
@@ -512,9 +526,8 @@ __global__ __launch_bounds__(256, (decode_occupancy<D, DV, NRB>())) void gqa_dec
     wave_lds_sync();
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
-      const uint16_t* vp = vl + (16 * db + c16) * VTS + 4 * q4;
-      const u32x2 lo = *(const u32x2*)vp;
-      const u32x2 hi = *(const u32x2*)(vp + 16);
+      const u32x2 lo = *(const u32x2*)(vl + vt_at(16 * db + c16, q4));
+      const u32x2 hi = *(const u32x2*)(vl + vt_at(16 * db + c16, q4 + 4));
       const u32x4 av = {lo[0], lo[1], hi[0], hi[1]};
 #pragma unroll
       for (int rb = 0; rb < NRB; ++rb) {
@@ -712,12 +725,14 @@ struct LatentTile {
   static constexpr int GRP = (NC % 16 == 0) ? 16 : 8;  // swizzle group (columns)
   static_assert(NC % 8 == 0 && STAGE_B % 4096 == 0, "latent tile shape");
   // Row r's column XOR.  Row r starts at 16-byte bank unit (r*NC) % 16, which
-  // is 0 when NC % 16 == 0 and 8*(r&1) when NC % 16 == 8; the XOR below makes
-  // (start unit) ^ (column ^ swz(r)) distinct over any 16 consecutive rows, and
-  // over any 8 rows for an aligned column pair.
-  __device__ static int swz(int r) {
-    return GRP == 16 ? (((r & 7) << 1) | ((r >> 3) & 1)) : ((((r >> 1) & 3) << 1) | ((r >> 3) & 1));
-  }
+  // is 0 when NC % 16 == 0 and 8*(r&1) when NC % 16 == 8.  K fragments
+  // (ds_read_b128) have lane l read column 4e + l/16 of row l%16, and gfx950's
+  // LDS serves lanes 0-7 with 24-31 and 8-15 with 16-23 in one cycle, so rows
+  // r < 8 of column 4e and rows r + 8 of column 4e + 1 must take different
+  // bank groups: XOR 2(r&7) (whole lines) or r&6 (half lines) sends the first
+  // to even groups and the second to odd ones.  The transposing V^T reads
+  // (32 lanes: an aligned column pair of 8 consecutive rows) stay distinct.
+  __device__ static int swz(int r) { return GRP == 16 ? ((r & 7) << 1) : (r & 6); }
 };
 
 template <typename E, int D, int DV, bool STREAM>

@@ -29,7 +29,9 @@ namespace pjx {
 // stages each (K | V | bias block [128 queries][32 keys] per stage), all
 // copied by buffer->LDS loads, NP-1 sets in flight while one is computed;
 // each group loads its own tile of a set, a quarter per wave.  Bias rows
-// (128 B) keep their 16-byte chunks XOR-swizzled by (row & 7).  Every path
+// (128 B) keep their 16-byte chunks XOR-swizzled by bias_swz(row), the D = 64
+// K rows' swizzle, for the same read pattern (lane l reads a chunk of row
+// l%32).  Every path
 // issues the same loads in the same order (tiles past the last one read
 // nothing) and the loop has no early exit, so waits are partial vmcnt counts
 // the compiler can see through; one barrier per set (after the wait for the
@@ -40,6 +42,9 @@ namespace pjx {
 // Requires Lk % 4 == 0 (16-byte bias chunks) and Lq*Lk*4 < 2^31 (32-bit
 // buffer offsets within one (batch, head) bias slice).
 // ---------------------------------------------------------------------------
+// Chunk swizzle of the 128-byte bias rows in LDS (8 chunks of 4 keys).
+__device__ __forceinline__ int bias_swz(int r) { return (r & 6) | ((r >> 3) & 1); }
+
 template <int D, int G_>
 struct BiasRing {
   using T = Bf16Tile<D, 32>;
@@ -95,7 +100,7 @@ __global__ __launch_bounds__(G_ * kThreads, 1) void flash_fwd_bf16_bias_ring_ker
   }
 
   // K/V rows 8w + .. of the group's tile; bias rows 32w + 8j + lane/8, LDS
-  // chunk lane%8 from global chunk (lane%8) ^ (row & 7).
+  // chunk lane%8 from global chunk (lane%8) ^ bias_swz(row).
   uint32_t voffK[T::NLD], voffV[T::NLD];
 #pragma unroll
   for (int j = 0; j < T::NLD; ++j) {
@@ -107,7 +112,7 @@ __global__ __launch_bounds__(G_ * kThreads, 1) void flash_fwd_bf16_bias_ring_ker
 #pragma unroll
   for (int j = 0; j < R::NLB; ++j) {
     const int r = 32 * w + 8 * j + lane / 8, slot = lane % 8;
-    voffB[j] = (uint32_t)(g.q0 + r) * (uint32_t)a.Lk * 4u + 16u * (uint32_t)(slot ^ (r & 7));
+    voffB[j] = (uint32_t)(g.q0 + r) * (uint32_t)a.Lk * 4u + 16u * (uint32_t)(slot ^ bias_swz(r));
   }
   uint32_t offK[D / 16];
 #pragma unroll
@@ -175,7 +180,7 @@ __global__ __launch_bounds__(G_ * kThreads, 1) void flash_fwd_bf16_bias_ring_ker
     // 2*(r/4) + half of this lane's row.
 #pragma unroll
     for (int gq = 0; gq < 4; ++gq) {
-      const f32x4 bv = *(const f32x4*)(bs + offB + 16 * ((2 * gq + half) ^ (brow_l & 7)));
+      const f32x4 bv = *(const f32x4*)(bs + offB + 16 * ((2 * gq + half) ^ bias_swz(brow_l)));
 #pragma unroll
       for (int j = 0; j < 4; ++j) s[4 * gq + j] = fmaf(s[4 * gq + j], a.scale, bv[j]);
     }

@@ -139,9 +139,15 @@ __device__ __forceinline__ f32x4 load_bias4(const float* row, int kk, int Lk) {
 }
 
 // bf16 K/V tile layout: BK keys per tile, row-major [key][dim] rows of D*2
-// bytes, 16-byte chunks XOR-swizzled per row (K: chunk ^ (row & (NC-1)); V:
+// bytes, 16-byte chunks XOR-swizzled per row.  K: a ds_read_b128 fragment has
+// lane l read chunk 2*st + l/32 of row l%32, and gfx950's LDS serves lanes
+// 0-7 with 24-31 and 8-15 with 16-23 in one cycle (64 banks of 4 bytes), so
+// rows r < 8 and r + 24 (or r + 8 and r + 16) must take different 16-byte
+// bank groups: chunk ^ (row & 15) at D = 128 (whole bank lines); at D = 64,
+// where odd rows start half a line later, chunk ^ ((row & 6) | ((row >> 3) & 1))
+// (with row & 7 the two halves of each cycle met in one bank group).  V:
 // chunk ^ f(row) chosen so a transposing read of 4 rows x 32 bytes per 16
-// lanes hits distinct banks).
+// lanes hits distinct banks.
 template <int D, int BK_ = 64>
 struct Bf16Tile {
   static constexpr int BK = BK_;            // keys per tile
@@ -151,7 +157,7 @@ struct Bf16Tile {
   static constexpr int STAGE_B = 2 * TILE_B;
   static constexpr int RPI = 64 / NC;       // rows per 1 KiB buffer->LDS load
   static constexpr int NLD = (BK / 4) / RPI;  // loads per wave per tensor per tile
-  __device__ static int swz_k(int r) { return r & (NC - 1); }
+  __device__ static int swz_k(int r) { return NC >= 16 ? (r & 15) : ((r & 6) | ((r >> 3) & 1)); }
   __device__ static int swz_v(int r) {
     return D == 128 ? 4 * (r & 3) + 2 * ((r >> 1) & 1) : 4 * ((r >> 1) & 1) + 2 * (r & 1);
   }
