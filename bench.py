@@ -397,7 +397,7 @@ def make_c2wb(dev, gen):
     fn = lambda: flash_attention_bwd(q, k, v, o, do, lse, sm_scale=sc, causal=True, workspace=ws)  # noqa: E731
     return dict(name="causal bwd bf16 B=2 H=16 L=4096 D=256 (dq, dk, dv)", fn=fn, flop=flop, bytes=nbytes,
                 bound="mfma", dtype="bf16",
-                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + flash_bwd_dkdv_kernel<Bf16Fmt,256,false,0,1>")
+                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + wide_bwd_dc_kernel<Bf16Fmt,256,256,false>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,

@@ -144,10 +144,12 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
   hipStream_t s = (hipStream_t)stream;
   if (head_dim == 256 && f32) return run_flash_f32_wide_bwd(ba, s);
   if (head_dim == 256) {
-    // dQ (and delta, lse*log2e): the 16-row wide kernel.  dK/dV: without
-    // extended masks the 32-key kernel above at one wave per SIMD (32x32x16
-    // MFMAs; 501 registers, no spills), else the 16-key wide kernel, one head
-    // group per KV head (no partials).
+    // dQ (and delta, lse*log2e): the 16-row wide kernel.  dK/dV: with a dense
+    // bias and no extended masks the 32-key kernel above at one wave per SIMD
+    // (32x32x16 MFMAs; 501 registers, no spills); otherwise the wide kernels,
+    // one head group per KV head (no partials): without bias or extended
+    // masks the column-split one at two workgroups per CU, which is faster
+    // than the 32-key kernel there.
     WideBwdArgs wa;
     wa.f = a;
     wa.f.dv = 256;
@@ -158,7 +160,7 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     wa.dbias = dbias;
     wa.part = nullptr;
     wa.nsplit = 1;
-    if (a.ext != 0) return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
+    if (a.ext != 0 || bias == nullptr) return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
     const int rc = run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd", true);
     if (rc != PJX_OK) return rc;
     const bool hb256 = bias != nullptr;

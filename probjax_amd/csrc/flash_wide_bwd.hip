@@ -661,8 +661,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
 // wave then reads the transposed Q / dO fragments of its own blocks only (a
 // quarter of the tile) where the key split reads all of them in every wave.
 // ---------------------------------------------------------------------------
+// At D = 256 (separate K / V) two workgroups share a CU: 73 KiB of LDS each,
+// and the instance fits 256 registers without spills (250 VGPRs).  The latent
+// widths need 147 KiB of LDS and run one.
 template <typename E, int D, int DV, bool SHARED>
-__global__ __launch_bounds__(kThreads, 1) void wide_bwd_dc_kernel(WideBwdArgs ba) {
+__global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kernel(WideBwdArgs ba) {
   const FlashArgs& a = ba.f;
   using RQ = Row16<D>;
   using RD = Row16<DV>;

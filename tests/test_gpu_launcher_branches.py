@@ -224,7 +224,8 @@ def test_forward_extended_branch(device, D, kind, with_bias):
 
 # ---------------------------------------------------------------------------
 # Backward: run_bwd_h16 (dQ then dK/dV), small grids (two wave groups, NG = 2)
-# and large grids (NG = 1), without bias, with a dense bias, with dbias
+# and large grids (NG = 1), without bias, with a dense bias, with dbias; and
+# pjx_flash_bwd's D = 256 route
 # ---------------------------------------------------------------------------
 
 BWD_CASES = {
@@ -242,12 +243,20 @@ BWD_CASES = {
     "d128_small": (128, 2, 300, 300, 8, 2, True, [300, 170], None, (2, 2)),
     "d128_small_bias": (128, 1, 256, 256, 8, 8, False, None, "bias", (2, 2)),
     "d64_small_dbias": (64, 2, 200, 256, 4, 4, True, [256, 90], "dbias", (2, 2)),
+    # D = 256: the wide dQ kernel, then the column-split wide dC kernel without
+    # bias, the 32-key dK/dV kernel with one (no grid-size branches)
+    "d256_gqa": (256, 1, 256, 256, 8, 4, True, None, None, None),
+    "d256_ragged_bias": (256, 2, 200, 300, 4, 2, False, [300, 123], "bias", None),
+    "d256_dbias": (256, 1, 256, 256, 4, 4, True, None, "dbias", None),
 }
 
 
 def _bwd_instances(E, D, mode, ng):
     dq_bias = {None: 0, "bias": 1, "dbias": 2}[mode]
     kv_bias = "false" if mode is None else "true"
+    if D == 256:
+        kv = f"wide_bwd_dc_kernel<{E}, 256, 256, false>" if mode is None else f"flash_bwd_dkdv_kernel<{E}, 256, true, 0, 1>"
+        return [f"wide_bwd_dq_kernel<{E}, 256, 256, false, {dq_bias}, 0>", kv]
     return [f"flash_bwd_dq_kernel<{E}, {D}, {dq_bias}, 0, {ng[0]}>",
             f"flash_bwd_dkdv_kernel<{E}, {D}, {kv_bias}, 0, {ng[1]}>"]
 
