@@ -382,22 +382,26 @@ def make_c2w(dev, gen):
 
 def make_c2wb(dev, gen):
     """Backward of the head-dim-256 forward (the C2W shape): one pjx_flash_bwd
-    call (the 16-row dQ kernel and the 32-key dK/dV kernel at D = 256).  FLOPs
-    by the 2.5x-forward convention, as for C2B."""
+    call on its dS route (the workspace holds the rounded dS: delta, the
+    column-split dK/dV kernel storing dS, then dQ = dS K).  FLOPs by the
+    2.5x-forward convention, as for C2B."""
     import torch
+    from probjax_amd import native
     from probjax_amd.hip_attention import flash_attention_bwd, flash_attention_fwd
 
     B, L, H, D = 2, 4096, 16, 256
     q, k, v, do = (_randn((B, L, H, D), gen, dev, torch.bfloat16) for _ in range(4))
     sc = 1 / math.sqrt(D)
     o, lse = flash_attention_fwd(q, k, v, sm_scale=sc, causal=True, return_lse=True)
-    ws = torch.empty(8 * B * H * L, dtype=torch.uint8, device=dev)
+    nws = int(native.load().pjx_flash_bwd_ds_workspace_size(native.PJX_DTYPE_BF16, B, H, L, L, D))
+    ws = torch.empty(nws, dtype=torch.uint8, device=dev)
     flop = 2.5 * 4 * B * H * L * L * D / 2
     nbytes = 2 * B * L * H * D * 2 * 4 + B * H * L * 4
     fn = lambda: flash_attention_bwd(q, k, v, o, do, lse, sm_scale=sc, causal=True, workspace=ws)  # noqa: E731
     return dict(name="causal bwd bf16 B=2 H=16 L=4096 D=256 (dq, dk, dv)", fn=fn, flop=flop, bytes=nbytes,
                 bound="mfma", dtype="bf16",
-                kernel="wide_bwd_dq_kernel<Bf16Fmt,256,256,false,0,0> + wide_bwd_dc_kernel<Bf16Fmt,256,256,false>")
+                kernel="wide_bwd_delta_kernel<Bf16Fmt,256> + wide_bwd_dc_ds_kernel<Bf16Fmt,256,256,false> + "
+                       "wide_bwd_dq_ds_kernel<Bf16Fmt,256>")
 
 
 MAKERS = {"C1": make_c1, "C2": make_c2, "C3": make_c3, "C4": make_c4, "C5": make_c5,

@@ -156,6 +156,25 @@ int pjx_flash_fwd(int dtype, const void* q, const void* k, const void* v, void* 
 size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_len);
 
 /*
+ * Bytes of workspace with which pjx_flash_bwd keeps the rounded dS between
+ * its kernels (the dS route), or 0 where the route does not exist: it exists
+ * for 16-bit inputs at head_dim 256.  A call there without bias, dbias or
+ * score modifiers (or modifiers that lower to none) whose workspace holds at
+ * least this many bytes runs: delta; dK/dV, which also stores dS (2 bytes per
+ * score, in 32-query x 16-key blocks); the dQ kernel, dQ = dS K as one
+ * product per score, where the two-kernel route recomputes S and dP for dQ
+ * (the three products of the reference's dQ scan,
+ * kernels/attention.py:1089-1150, become one).  At head dim 256 the two
+ * recomputed products cost more than storing and re-reading dS; at 64 and
+ * 128 they cost less, and those head dims keep the two-kernel route.  Same
+ * roundings as the two-kernel route.  Size: pjx_flash_bwd_workspace_size()
+ * rounded up to 256 bytes, plus 2 * batch * q_heads * q_len' * kv_len' bytes,
+ * q_len' and kv_len' rounded up to 64.
+ */
+size_t pjx_flash_bwd_ds_workspace_size(int dtype, int64_t batch, int64_t q_heads, int64_t q_len,
+                                       int64_t kv_len, int64_t head_dim);
+
+/*
  * Flash-attention backward: dq, dk, dv of pjx_flash_fwd's output.  Replaces
  * the Pallas backward of `mha` (probjax/nn/pallas_kernels/kernels/
  * attention.py: _preprocess_backward_kernel 853-867, mha_backward_kernel
@@ -179,7 +198,8 @@ size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, int64_t q_le
  * rows contribute nothing); dq [B, Lq, Hq, D], dk and dv [B, Lk, Hkv, D]
  * (fully written, zeros where no valid score reaches).  workspace: at least
  * pjx_flash_bwd_workspace_size(batch, q_heads, q_len) bytes.  mods: the
- * forward's (pjx_score_mods) or NULL.
+ * forward's (pjx_score_mods) or NULL.  A workspace of at least
+ * pjx_flash_bwd_ds_workspace_size() bytes selects the dS route where it applies.
  * dtype: PJX_DTYPE_BF16, PJX_DTYPE_F16 or PJX_DTYPE_F32 (all fp32 products, no
  * roundings).  head_dim in {64, 128, 256}.
  */

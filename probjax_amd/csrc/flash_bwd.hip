@@ -73,6 +73,16 @@ extern "C" size_t pjx_flash_bwd_workspace_size(int64_t batch, int64_t q_heads, i
   return (size_t)(2 * batch * q_heads * q_len) * sizeof(float);
 }
 
+extern "C" size_t pjx_flash_bwd_ds_workspace_size(int dtype, int64_t batch, int64_t q_heads, int64_t q_len,
+                                                  int64_t kv_len, int64_t head_dim) {
+  if (dtype != PJX_DTYPE_BF16 && dtype != PJX_DTYPE_F16) return 0;
+  if (head_dim != 256) return 0;
+  if (batch <= 0 || q_heads <= 0 || q_len <= 0 || kv_len <= 0) return 0;
+  if (q_len > (1 << 30) || kv_len > (1 << 30)) return 0;
+  return wide_bwd_ds_offset(pjx_flash_bwd_workspace_size(batch, q_heads, q_len)) +
+         wide_bwd_ds_bytes(batch, q_heads, q_len, kv_len);
+}
+
 extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void* v, const void* o,
                              const void* dout, const float* lse, void* dq, void* dk, void* dv,
                              float* dbias, void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
@@ -160,6 +170,15 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     wa.dbias = dbias;
     wa.part = nullptr;
     wa.nsplit = 1;
+    wa.ds = nullptr;
+    wa.ds_nq32 = wa.ds_nk16 = 0;
+    const size_t ds_need = pjx_flash_bwd_ds_workspace_size(dtype, batch, q_heads, q_len, kv_len, head_dim);
+    if (!f32 && !bias && a.ext == 0 && ds_need > 0 && workspace_bytes >= ds_need) {
+      // the dS route (flash_wide_bwd.hip): the workspace holds the dS blocks
+      wa.ds = (uint16_t*)((unsigned char*)workspace + wide_bwd_ds_offset(need));
+      wa.ds_nq32 = (int)(2 * ((q_len + 63) / 64));
+      wa.ds_nk16 = (int)(4 * ((kv_len + 63) / 64));
+    }
     if (a.ext != 0 || bias == nullptr) return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
     const int rc = run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd", true);
     if (rc != PJX_OK) return rc;

@@ -183,13 +183,27 @@ struct WideBwdArgs {
   float* dbias;       // [B, Hq, Lq, Lk] fp32 dL/d(bias) or null
   float* part;        // [nsplit][B][Lk][Hkv][D (+ DV)] fp32 partials when nsplit > 1
   int nsplit;         // query-head groups per KV head in the dK/dV kernel
+  // The rounded dS kept between the dK/dV and dQ kernels (the dS route of
+  // flash_wide_bwd.hip), or null: per query head, blocks of 32 queries x 16
+  // keys (1 KiB), ds_nq32 x ds_nk16 of them ([query block][key block]).
+  uint16_t* ds;
+  int ds_nq32, ds_nk16;
 };
+
+// Bytes of the wide backward's dS blocks (the dS route) for these sizes:
+// 32-query blocks over the queries rounded up to the dQ kernel's 64-row
+// tiles, 16-key blocks over the keys rounded up to the dK/dV kernel's 64-key
+// tiles.
+size_t wide_bwd_ds_bytes(int64_t B, int64_t Hq, int64_t Lq, int64_t Lk);
 
 // Runs the wide backward (dQ, then dK/dV or the latent's dC, then the partial
 // sum when nsplit > 1; with dq_only the dQ kernel alone, which also writes
 // delta and lse*log2e); returns a PJX_* status.
 int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who,
                  bool dq_only = false);
+// Byte offset of the dS blocks in a dS-route workspace whose leading part
+// (delta, lse*log2e, partials) takes `lead` bytes.
+inline size_t wide_bwd_ds_offset(size_t lead) { return (lead + 255) & ~(size_t)255; }
 
 // Wide-head bf16 forward kernels (flash_wide.hip): D = 256 with separate K/V,
 // and the absorbed latent (K = V, rank 512 / 576, output width a.dv).

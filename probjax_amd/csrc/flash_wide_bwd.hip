@@ -664,8 +664,11 @@ __global__ __launch_bounds__(kThreads, 1) void wide_bwd_dkdv_kernel(WideBwdArgs 
 // At D = 256 (separate K / V) two workgroups share a CU: 73 KiB of LDS each,
 // and the instance fits 256 registers without spills (250 VGPRs).  The latent
 // widths need 147 KiB of LDS and run one.
-template <typename E, int D, int DV, bool SHARED>
-__global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kernel(WideBwdArgs ba) {
+// DS (the dS route): each compute() also stores the wave's rounded dS block
+// (16 keys x 32 queries, zeros where no row of the tile sees the wave's keys)
+// into ba.ds; see wide_bwd_dq_ds_kernel for the layout.
+template <typename E, int D, int DV, bool SHARED, bool DS>
+__device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
   const FlashArgs& a = ba.f;
   using RQ = Row16<D>;
   using RD = Row16<DV>;
@@ -787,8 +790,9 @@ __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kern
   };
 
   auto compute = [&](int t, const unsigned char* st) {
+    int n_stores = 0;
     const int q0 = tile_q0(t);
-    if (q0 >= q_hi) return;  // uniform over the workgroup
+    if (q0 >= q_hi) return n_stores;  // uniform over the workgroup
     const unsigned char* qs = st;
     const unsigned char* dos = st + QT_B;
     // P and dS of this wave's keys (zero where no row of the tile sees them)
@@ -828,6 +832,14 @@ __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kern
       pbv = __builtin_bit_cast(u32x4, pack_slots<E>(sx[0], sx[1]));
       dsv = __builtin_bit_cast(u32x4, pack_slots<E>(dpx[0], dpx[1]));
     }
+    if constexpr (DS) {
+      // block (query block q0 / 32, key block kw / 16) of head tile_head(t):
+      // lane (c, qd) holds key kw + c, queries q0 + 4qd + [0,4) then
+      // q0 + 16 + 4qd + [0,4) (pack_slots), stored as 16 bytes at 16 * lane
+      const size_t blk = ((size_t)(b * a.Hq + tile_head(t)) * ba.ds_nq32 + q0 / 32) * ba.ds_nk16 + kw / 16;
+      *(u32x4*)(ba.ds + blk * 512 + 8 * lane) = dsv;
+      ++n_stores;
+    }
     xp[(2 * w) * 64 + lane] = pbv;
     xp[(2 * w + 1) * 64 + lane] = dsv;
     stage_barrier();
@@ -864,22 +876,38 @@ __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kern
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4 * 3, 0);
+    return n_stores;
   };
 
   // The ring of wide_bwd_dkdv_kernel; each compute adds one barrier between
   // the xp writes and reads, and the next xp writes follow the next ring
-  // barrier.
+  // barrier.  With DS the ring barrier waits for this wave's tile loads only:
+  // the dS store of the last compute() (issued after them; vmcnt counts in
+  // issue order) stays in flight, and the barrier is stage_barrier(), as
+  // __syncthreads()'s release fence would wait for it.  (The scheduling
+  // barriers keep the store after the loads issued before it.)
+  auto ring_wait = [&](int in_flight) {
+    if constexpr (DS) {
+      if (in_flight > 0) wait_vmcnt<1>();
+      else wait_vmcnt<0>();
+      stage_barrier();
+    } else {
+      __builtin_amdgcn_s_waitcnt(0);
+      __syncthreads();
+    }
+  };
+  int n_st = 0;
   if (n_tiles > 0) issue(0, smem0);
   for (int t = 0; t < n_tiles; t += 2) {
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    ring_wait(n_st);
     if (t + 1 < n_tiles) issue(t + 1, smem1);
-    compute(t, smem0);
+    if constexpr (DS) __builtin_amdgcn_sched_barrier(0);
+    n_st = compute(t, smem0);
     if (t + 1 >= n_tiles) break;
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
+    ring_wait(n_st);
     if (t + 2 < n_tiles) issue(t + 2, smem0);
-    compute(t + 1, smem1);
+    if constexpr (DS) __builtin_amdgcn_sched_barrier(0);
+    n_st = compute(t + 1, smem1);
   }
 
   // Outputs as wide_bwd_dkdv_kernel's: 16-bit rows with one group, else fp32
@@ -917,6 +945,194 @@ __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kern
 
 // Sums the head-group partials in split order and rounds to the 16-bit format:
 // out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
+template <typename E, int D, int DV, bool SHARED>
+__global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kernel(WideBwdArgs ba) {
+  wide_dc_body<E, D, DV, SHARED, false>(ba);
+}
+
+// ---------------------------------------------------------------------------
+// The dS route (head dim 256, 16-bit, no bias, no extended masks; the
+// caller's workspace holds the dS blocks).  At D = 256 the dQ kernel's
+// recomputation of S and dP (two products of 256 dims per score) costs more
+// than writing and reading back the rounded dS (2 bytes per score, whatever
+// the width), so the route runs: wide_bwd_delta_kernel; wide_bwd_dc_ds_kernel,
+// which also stores dS; then wide_bwd_dq_ds_kernel, one product per score.
+// Same roundings, sums and summation order as the two-kernel route, so the
+// results are bitwise those of that route.
+// ---------------------------------------------------------------------------
+
+template <typename E, int D, int DV, bool SHARED>
+__global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_ds_kernel(WideBwdArgs ba) {
+  wide_dc_body<E, D, DV, SHARED, true>(ba);
+}
+
+// delta * sm_scale and lse * log2e of every query row (what wide_bwd_dq_kernel
+// writes): four lanes per row, lane qd summing dims 32st + 8qd + [0,8) over
+// the DV output dims in that kernel's order, then (qd 0 + qd 1) + (qd 2 + qd 3).
+template <typename E, int DV>
+__global__ __launch_bounds__(kThreads) void wide_bwd_delta_kernel(WideBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  constexpr int VS = DV / 32;
+  const long rows = (long)a.B * a.Lq * a.Hq;
+  const long row = (long)blockIdx.x * (kThreads / 4) + (threadIdx.x >> 2);
+  const int qd = threadIdx.x & 3;
+  float dsum = 0.f;
+  if (row < rows) {
+    const uint16_t* orow = (const uint16_t*)a.o + row * DV;
+    const uint16_t* drow = (const uint16_t*)ba.dout + row * DV;
+#pragma unroll
+    for (int st = 0; st < VS; ++st) {
+      const u32x4 ro = *(const u32x4*)(orow + 32 * st + 8 * qd);
+      const u32x4 rd = *(const u32x4*)(drow + 32 * st + 8 * qd);
+#pragma unroll
+      for (int j = 0; j < 4; ++j)
+        dsum = fmaf(E::lo(ro[j]), E::lo(rd[j]), fmaf(E::hi(ro[j]), E::hi(rd[j]), dsum));
+    }
+  }
+  const float pair = dsum + __shfl_xor(dsum, 1);
+  const float delta = pair + __shfl_xor(pair, 2);
+  if (row < rows && qd == 0) {
+    const int h = (int)(row % a.Hq);
+    const long bq = row / a.Hq;
+    const int qi = (int)(bq % a.Lq), b = (int)(bq / a.Lq);
+    const size_t lidx = ((size_t)b * a.Hq + h) * a.Lq + qi;
+    ba.delta[lidx] = delta * a.scale;
+    ba.lse2[lidx] = a.lse[lidx] * kLog2e;
+  }
+}
+
+// dQ^T += K^T dS^T from the stored dS: one workgroup per (64-query tile,
+// batch, head), heaviest causal tile first.  The waves split the output dims
+// (wave w: 16-dim blocks w + 4j) and each takes all 64 queries, so a K^T
+// fragment feeds four MFMAs (16x16x32, all 32 keys of a tile) and each wave
+// reads a quarter of K^T.  Per 32-key tile the K tile (row-major, the Row16
+// swizzle) and the tile's four dS blocks (4 KiB, copied as they are) go
+// HBM -> LDS through a 2-stage ring.
+// dS blocks (ds, ds_nq32, ds_nk16): block (query block q/32, key block k/16)
+// of a query head is 64 lanes x 16 bytes; lane 16*qd + c holds key c of the
+// block and queries 4qd + [0,4) then 16 + 4qd + [0,4) (two 8-byte words).
+// The dS^T operand of query block qb (16 queries) takes, in k-slot 8qd + j,
+// key 16(j/4) + 4qd + j%4 (the order of Offs16::trans): two transposing reads
+// (ds_read_b64_tr_b16) of the words of keys 4qd + s/4 (+16) and queries
+// 4*(s%4) + [0,4) of the query block, addressed by lane s of each 16-lane
+// group.  A query block at or past the valid queries was not stored and
+// enters as zeros.
+template <typename E, int D>
+__global__ __launch_bounds__(kThreads, (D <= 256 ? 2 : 1)) void wide_bwd_dq_ds_kernel(WideBwdArgs ba) {
+  const FlashArgs& a = ba.f;
+  using OK = Offs16<E, D>;
+  using RK = Row16<D>;
+  constexpr int KT_B = RK::TILE_B, ST_B = 4096;
+  constexpr int STAGE_B = KT_B + ST_B;
+  constexpr int ND = D / 16, NJ = ND / 4;
+  static_assert(ND % 4 == 0, "dims split evenly over the 4 waves");
+  __shared__ __attribute__((aligned(1024))) unsigned char smem0[STAGE_B];
+  __shared__ __attribute__((aligned(1024))) unsigned char smem1[STAGE_B];
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int c = lane & 15, qd = lane >> 4;
+  const int BH = a.B * a.Hq;
+  const int n_qt = (a.Lq + kWQ - 1) / kWQ;
+  const int bh = (int)blockIdx.x % BH;
+  const int qt = n_qt - 1 - (int)blockIdx.x / BH;  // heaviest causal tile first
+  const int b = bh / a.Hq, h = bh % a.Hq, hkv = h / (a.Hq / a.Hkv);
+  const int q0 = qt * kWQ;
+  const int q_hi = min(a.Lq, a.q_valid);
+  int kv_end = min(a.Lk, a.kv_valid);
+  if (a.kv_lengths) kv_end = min(kv_end, max(a.kv_lengths[b], 0));
+  int kv_stop = kv_end;
+  if (q0 >= q_hi) kv_stop = 0;
+  else if (a.causal) kv_stop = min(kv_stop, min(q0 + kWQ, q_hi));
+  const int n_tiles = (kv_stop + kWT - 1) / kWT;
+
+  const uint32_t rowstride = (uint32_t)a.Hkv * 2 * D;
+  const unsigned char* Kb = (const unsigned char*)a.k + ((size_t)b * a.Lk * a.Hkv + hkv) * (2 * D);
+  // the dS blocks of query block 2qt + w/2, key block 2t + w%2: wave w's load
+  const unsigned char* Sb = (const unsigned char*)(ba.ds + (((size_t)bh * ba.ds_nq32 + 2 * qt + (w >> 1)) *
+                                                                ba.ds_nk16 + (w & 1)) * 512);
+  OK ok;
+  ok.init(lane, w, rowstride);
+  // transposing K^T reads of this wave's dim blocks w + 4j (Offs16::trans)
+  uint32_t offk[NJ];
+  {
+    const int rl = 4 * qd + (c >> 2), bsel = (c & 3) >> 1;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const int i = w + 4 * j;
+      offk[j] = 16 * RK::G * (i / OK::PT) + rl * RK::ROWB + 16 * ((2 * (i % OK::PT) + bsel) ^ RK::swz(rl)) + 8 * (c & 1);
+    }
+  }
+  // dS^T reads: query block qb, keys 4qd + c/4 (lo: block 2(qb/2)), + 16 (hi:
+  // the next key block); byte of the word: slot 16*(c%4) + 4qd + c/4, half qb%2
+  uint32_t offs[4];
+  {
+    const int slot = 16 * (c & 3) + 4 * qd + (c >> 2);
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) offs[qb] = KT_B + 1024 * (2 * (qb >> 1)) + 16 * slot + 8 * (qb & 1);
+  }
+  bool stored[4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) stored[qb] = q0 + 32 * (qb >> 1) < q_hi;
+
+  // acc[j][qb] = dQ^T[dims 16(w + 4j) + 4qd + r][query q0 + 16qb + c]
+  f32x4 acc[NJ][4];
+#pragma unroll
+  for (int j = 0; j < NJ; ++j)
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) acc[j][qb] = f32x4{};
+
+  auto issue = [&](int t, unsigned char* st) {
+    const int k0 = t * kWT;
+    ok.load(st, Kb + (size_t)k0 * rowstride, rowstride, min(kWT, kv_stop - k0), w);
+    const rsrc_t rs = make_rsrc(Sb + (size_t)t * 2048, 1024);
+    buffer_load_lds16(rs, st + KT_B + 1024 * w, 16 * lane);
+  };
+
+  auto compute = [&](const unsigned char* st) {
+    typename E::v8 dsf[4];
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      const u32x2 lo = lds_read_tr16(st + offs[qb]);
+      const u32x2 hi = lds_read_tr16(st + offs[qb] + 1024);
+      dsf[qb] = stored[qb] ? E::as8(u32x4{lo[0], lo[1], hi[0], hi[1]}) : E::as8(u32x4{0u, 0u, 0u, 0u});
+    }
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const u32x2 lo = lds_read_tr16(st + offk[j]);
+      const u32x2 hi = lds_read_tr16(st + offk[j] + 16 * RK::ROWB);
+      const typename E::v8 kt = E::as8(u32x4{lo[0], lo[1], hi[0], hi[1]});
+#pragma unroll
+      for (int qb = 0; qb < 4; ++qb) acc[j][qb] = E::mma16(kt, dsf[qb], acc[j][qb]);
+    }
+  };
+
+  if (n_tiles > 0) issue(0, smem0);
+  for (int t = 0; t < n_tiles; t += 2) {
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 1 < n_tiles) issue(t + 1, smem1);
+    compute(smem0);
+    if (t + 1 >= n_tiles) break;
+    __builtin_amdgcn_s_waitcnt(0);
+    __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, smem0);
+    compute(smem1);
+  }
+
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    const int qi = q0 + 16 * qb + c;
+    if (qi >= a.Lq) continue;
+    uint16_t* drow = (uint16_t*)ba.dq + ((size_t)(b * a.Lq + qi) * a.Hq + h) * D;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+      const u32x2 pk = {E::pack2(acc[j][qb][0], acc[j][qb][1]), E::pack2(acc[j][qb][2], acc[j][qb][3])};
+      *(u32x2*)(drow + 16 * (w + 4 * j) + 4 * qd) = pk;
+    }
+  }
+}
+
 template <typename E>
 __global__ __launch_bounds__(256) void wide_bwd_reduce_kernel(const float* part, int nsplit, size_t n,
                                                                 uint16_t* out) {
@@ -964,6 +1180,37 @@ static int run_wide_bwd_t(WideBwdArgs& ba, hipStream_t s, const char* who, bool 
   const long kv_blocks = (long)((a.Lk + kWK - 1) / kWK) * a.B * a.Hkv * ba.nsplit;
   if (dq_blocks > 0x7fffffffL || kv_blocks > 0x7fffffffL) return fail(PJX_ERR_INVALID, "wide backward: grid too large");
   const dim3 blk(kThreads);
+  // the dS route: head dim 256 only (at the latent widths the key-side kernel
+  // with the store ran at half its speed, more than the dQ kernel saves)
+  if constexpr (!SHARED) {
+   if (ba.ds && !hb && !db && !ext && !dq_only) {
+    // the dS route: delta, dK/dV (dC) storing dS, the partial sum, dQ from dS
+    const long rows = (long)a.B * a.Lq * a.Hq;
+    launch_kernel<wide_bwd_delta_kernel<E, DV>>(dim3((unsigned)((rows + kThreads / 4 - 1) / (kThreads / 4))), blk, 0, s,
+                                                ba);
+    int rc = check_launch(who);
+    if (rc != PJX_OK) return rc;
+    if (kv_blocks > 0) {
+      launch_kernel<wide_bwd_dc_ds_kernel<E, D, DV, SHARED>>(dim3((unsigned)kv_blocks), blk, 0, s, ba);
+      rc = check_launch(who);
+      if (rc != PJX_OK) return rc;
+    }
+    if (ba.nsplit > 1) {
+      const size_t nk = (size_t)a.B * a.Lk * a.Hkv * D;
+      launch_kernel<wide_bwd_reduce_kernel<E>>(dim3((unsigned)((nk / 4 + 255) / 256)), dim3(256), 0, s,
+                         (const float*)ba.part, ba.nsplit, nk, (uint16_t*)ba.dk);
+      if constexpr (!SHARED) {
+        const size_t nv = (size_t)a.B * a.Lk * a.Hkv * DV;
+        launch_kernel<wide_bwd_reduce_kernel<E>>(dim3((unsigned)((nv / 4 + 255) / 256)), dim3(256), 0, s,
+                           (const float*)(ba.part + (size_t)ba.nsplit * nk), ba.nsplit, nv, (uint16_t*)ba.dv);
+      }
+      rc = check_launch(who);
+      if (rc != PJX_OK) return rc;
+    }
+    launch_kernel<wide_bwd_dq_ds_kernel<E, D>>(dim3((unsigned)dq_blocks), blk, 0, s, ba);
+    return check_launch(who);
+   }
+  }
 #define PJX_DQ(BI, EX) launch_kernel<wide_bwd_dq_kernel<E, D, DV, SHARED, BI, EX>>(dim3((unsigned)dq_blocks), blk, 0, s, ba)
   if (ext) {
     if (db) PJX_DQ(2, 2); else if (hb) PJX_DQ(1, 2); else PJX_DQ(0, 2);
@@ -1026,6 +1273,13 @@ extern "C" size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64
                             wide_bwd_nsplit(batch, kv_len, heads, 1), true);
 }
 
+namespace pjx {
+size_t wide_bwd_ds_bytes(int64_t B, int64_t Hq, int64_t Lq, int64_t Lk) {
+  const int64_t nq32 = 2 * ((Lq + kWQ - 1) / kWQ), nk16 = 4 * ((Lk + kWK - 1) / kWK);
+  return (size_t)B * Hq * nq32 * nk16 * 1024;
+}
+}  // namespace pjx
+
 extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const void* o,
                            const void* dout, const float* lse, void* dq, void* dcache,
                            void* workspace, size_t workspace_bytes, const int32_t* kv_lengths,
@@ -1085,5 +1339,7 @@ extern "C" int pjx_mla_bwd(int dtype, const void* q, const void* cache, const vo
   ba.dk = dcache;
   ba.dv = nullptr;
   ba.dbias = nullptr;
+  ba.ds = nullptr;  // the latent keeps the two-kernel route
+  ba.ds_nq32 = ba.ds_nk16 = 0;
   return run_wide_bwd(ba, (int)rank, (int)v_dim, true, (hipStream_t)stream, who);
 }

@@ -9,6 +9,7 @@ device; nothing is copied between host and device.
 from __future__ import annotations
 
 import ctypes
+import os
 from dataclasses import dataclass
 
 import torch
@@ -176,7 +177,7 @@ def flash_attention_fwd(
 def flash_attention_bwd(
     q, k, v, o, do, lse, *, sm_scale: float, causal: bool = False, kv_lengths=None, bias=None,
     q_valid: int | None = None, kv_valid: int | None = None, workspace=None,
-    mods: ScoreModsArgs | None = None, bias_grad: bool = False,
+    mods: ScoreModsArgs | None = None, bias_grad: bool = False, ds_route: bool | None = None,
 ):
     """``pjx_flash_bwd``: gradients ``(dq, dk, dv)`` of ``flash_attention_fwd``
     (and, with ``bias_grad``, ``dbias``: dL/d(bias) summed to the bias's own
@@ -184,6 +185,14 @@ def flash_attention_bwd(
 
     ``o`` and ``lse`` are the forward's output and natural-log LSE; ``do`` the
     output gradient.  Masks, bias and scale must be the forward's.  bf16, fp16 or fp32.
+
+    ``ds_route`` (when ``workspace`` is None): the workspace this call
+    allocates.  None sizes it for the dS route (dQ from the rounded dS the
+    dK/dV kernel keeps, ``pjx_flash_bwd_ds_workspace_size``) where the route
+    exists (16-bit, head dim 256 -- after padding -- without bias or score
+    modifiers) and its ``2 * B * Hq * Lq' * Lk'`` bytes of dS fit the budget
+    (``_ds_budget``); True takes it whatever its size (ValueError where it
+    does not exist); False never does.
     """
     dev = _on_device(q, k, v, o, do, lse, bias)
     if q.ndim != 4 or k.ndim != 4 or v.ndim != 4:
@@ -220,7 +229,14 @@ def flash_attention_bwd(
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     dbias = torch.zeros((B, Hq, Lq, Lk), dtype=torch.float32, device=dev) if bias_grad else None
     lib = native.load()
-    ws = _workspace(int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq)), dev, workspace)
+    nbytes = int(lib.pjx_flash_bwd_workspace_size(B, Hq, Lq))
+    if workspace is None:
+        ds_bytes = 0
+        if bias is None and ms is None:
+            ds_bytes = int(lib.pjx_flash_bwd_ds_workspace_size(code, B, Hq, Lq, Lk, D))
+        nbytes = _ds_route_bytes(nbytes, ds_bytes, ds_route, dev,
+                                 "the dS route takes 16-bit inputs at head dim 256 without bias or score modifiers")
+    ws = _workspace(nbytes, dev, workspace)
     rc = lib.pjx_flash_bwd(
         code, _ptr(q), _ptr(k), _ptr(v), _ptr(o), _ptr(do), _ptr(lse), _ptr(dq),
         _ptr(dk), _ptr(dv), _ptr(dbias), _ptr(ws), ws.numel(), _ptr(L), _ptr(bias), bb, bh, B, Lq, Lk, Hq, Hkv, D,
@@ -234,6 +250,28 @@ def flash_attention_bwd(
     if dims:
         dbias = dbias.sum(dim=dims, keepdim=True)
     return dq, dk, dv, dbias
+
+
+def _ds_budget(dev) -> int:
+    """Bytes of dS a backward call may keep in its workspace (the dS route):
+    ``PJX_BWD_DS_MAX_BYTES`` if set, else 1/16 of the device's memory, at most
+    16 GiB."""
+    env = os.environ.get("PJX_BWD_DS_MAX_BYTES")
+    if env:
+        return int(env)
+    total = torch.cuda.get_device_properties(dev).total_memory
+    return min(total // 16, 16 << 30)
+
+
+def _ds_route_bytes(base: int, ds_bytes: int, ds_route, dev, why: str) -> int:
+    """Workspace bytes a backward call allocates: ``ds_bytes`` (the dS route,
+    0 where it does not exist) when ``ds_route`` is True, or None and the dS
+    part fits ``_ds_budget``; else ``base``."""
+    if ds_route and not ds_bytes:
+        raise ValueError(why)
+    if ds_bytes and ds_route is not False and (ds_route or ds_bytes - base <= _ds_budget(dev)):
+        return ds_bytes
+    return base
 
 
 def decode_workspace_bytes(batch, groups, rows, kv_len, v_dim, chunk=0) -> int:

@@ -56,6 +56,7 @@ _SIGNATURES = {
          _I64, _I64, _I64, _I64, ctypes.c_int, ctypes.c_float, _MODS, _P],
     ),
     "pjx_flash_bwd_workspace_size": (ctypes.c_size_t, [_I64, _I64, _I64]),
+    "pjx_flash_bwd_ds_workspace_size": (ctypes.c_size_t, [ctypes.c_int, _I64, _I64, _I64, _I64, _I64]),
     "pjx_flash_bwd": (
         ctypes.c_int,
         [ctypes.c_int, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, _P, ctypes.c_size_t, _P, _P, _I64,

@@ -243,8 +243,9 @@ BWD_CASES = {
     "d128_small": (128, 2, 300, 300, 8, 2, True, [300, 170], None, (2, 2)),
     "d128_small_bias": (128, 1, 256, 256, 8, 8, False, None, "bias", (2, 2)),
     "d64_small_dbias": (64, 2, 200, 256, 4, 4, True, [256, 90], "dbias", (2, 2)),
-    # D = 256: the wide dQ kernel, then the column-split wide dC kernel without
-    # bias, the 32-key dK/dV kernel with one (no grid-size branches)
+    # D = 256 (two-kernel route; the dS route is tests/test_gpu_bwd_ds_route.py):
+    # the wide dQ kernel, then the column-split wide dC kernel without bias,
+    # the 32-key dK/dV kernel with one (no grid-size branches)
     "d256_gqa": (256, 1, 256, 256, 8, 4, True, None, None, None),
     "d256_ragged_bias": (256, 2, 200, 300, 4, 2, False, [300, 123], "bias", None),
     "d256_dbias": (256, 1, 256, 256, 4, 4, True, None, "dbias", None),
@@ -288,7 +289,7 @@ def test_backward_branch(device, name, dtype):
     got = flash_attention_bwd(
         to_dev(q, device, tdt), to_dev(k, device, tdt), to_dev(v, device, tdt), to_dev(o, device, tdt),
         to_dev(do, device, tdt), torch.from_numpy(lse).to(device), sm_scale=scale, causal=causal,
-        kv_lengths=L, bias=bt, bias_grad=mode == "dbias",
+        kv_lengths=L, bias=bt, bias_grad=mode == "dbias", ds_route=False,
     )
     launched = _launched()
     torch.cuda.synchronize()
