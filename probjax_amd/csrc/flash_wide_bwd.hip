@@ -837,7 +837,7 @@ __device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
       // lane (c, qd) holds key kw + c, queries q0 + 4qd + [0,4) then
       // q0 + 16 + 4qd + [0,4) (pack_slots), stored as 16 bytes at 16 * lane
       const size_t blk = ((size_t)(b * a.Hq + tile_head(t)) * ba.ds_nq32 + q0 / 32) * ba.ds_nk16 + kw / 16;
-      *(u32x4*)(ba.ds + blk * 512 + 8 * lane) = dsv;
+      __builtin_nontemporal_store(dsv, (u32x4*)(ba.ds + blk * 512 + 8 * lane));  // read once, by the dQ kernel
       ++n_stores;
     }
     xp[(2 * w) * 64 + lane] = pbv;
@@ -957,6 +957,8 @@ __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kern
 // than writing and reading back the rounded dS (2 bytes per score, whatever
 // the width), so the route runs: wide_bwd_delta_kernel; wide_bwd_dc_ds_kernel,
 // which also stores dS; then wide_bwd_dq_ds_kernel, one product per score.
+// dS moves with non-temporal stores and loads (written once, read once; the
+// key-side kernel's Q / dO rows keep the L2): C2WB -4.5% against plain ones.
 // Same roundings, sums and summation order as the two-kernel route, so the
 // results are bitwise those of that route.
 // ---------------------------------------------------------------------------
@@ -1086,7 +1088,7 @@ __global__ __launch_bounds__(kThreads, (D <= 256 ? 2 : 1)) void wide_bwd_dq_ds_k
     const int k0 = t * kWT;
     ok.load(st, Kb + (size_t)k0 * rowstride, rowstride, min(kWT, kv_stop - k0), w);
     const rsrc_t rs = make_rsrc(Sb + (size_t)t * 2048, 1024);
-    buffer_load_lds16(rs, st + KT_B + 1024 * w, 16 * lane);
+    buffer_load_lds16_nt(rs, st + KT_B + 1024 * w, 16 * lane);  // dS is read once
   };
 
   auto compute = [&](const unsigned char* st) {
