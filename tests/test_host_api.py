@@ -510,3 +510,22 @@ def test_mla_decode_shape_rule():
     assert A._mla_decode_shape(128, 128) == (128, 128)
     assert A._mla_decode_shape(40, 40) == (64, 64)
     assert A._mla_decode_shape(600, 512) is None
+
+
+def test_ds_route_workspace_choice(monkeypatch):
+    """flash_attention_bwd's workspace choice for the dS route: the larger
+    workspace when the route exists and its dS fits the budget (or when asked
+    for), the plain one otherwise; asking for a route that does not exist is a
+    ValueError.  (No device is touched: the budget comes from the environment.)"""
+    from probjax_amd import hip_attention as H
+
+    monkeypatch.setenv("PJX_BWD_DS_MAX_BYTES", "1000")
+    dev = "cpu"
+    assert H._ds_route_bytes(100, 900, None, dev, "x") == 900
+    assert H._ds_route_bytes(100, 1100, None, dev, "x") == 1100  # 1000 bytes of dS: within the budget
+    assert H._ds_route_bytes(100, 1101, None, dev, "x") == 100  # 1001 bytes: the plain workspace
+    assert H._ds_route_bytes(100, 1101, True, dev, "x") == 1101
+    assert H._ds_route_bytes(100, 900, False, dev, "x") == 100
+    assert H._ds_route_bytes(100, 0, None, dev, "x") == 100
+    with pytest.raises(ValueError, match="no route"):
+        H._ds_route_bytes(100, 0, True, dev, "no route")

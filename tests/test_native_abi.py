@@ -117,6 +117,23 @@ def test_flash_bwd_workspace_size(lib):
     assert lib.pjx_flash_bwd_workspace_size(0, 3, 5) == 0
 
 
+def test_flash_bwd_ds_workspace_size(lib):
+    """The dS route exists for 16-bit inputs at head dim 256 only; its
+    workspace is the plain one rounded up to 256 bytes plus 1 KiB per block of
+    32 queries x 16 keys per head, both lengths rounded up to 64."""
+    bf16, f16, f32 = native.PJX_DTYPE_BF16, native.PJX_DTYPE_F16, native.PJX_DTYPE_F32
+    B, H, Lq, Lk = 2, 3, 300, 70
+    base = lib.pjx_flash_bwd_workspace_size(B, H, Lq)
+    lead = (base + 255) // 256 * 256
+    nq32, nk16 = 2 * ((Lq + 63) // 64), 4 * ((Lk + 63) // 64)
+    for dt in (bf16, f16):
+        assert lib.pjx_flash_bwd_ds_workspace_size(dt, B, H, Lq, Lk, 256) == lead + B * H * nq32 * nk16 * 1024
+    for dt, d in ((f32, 256), (bf16, 128), (bf16, 64), (f16, 128)):
+        assert lib.pjx_flash_bwd_ds_workspace_size(dt, B, H, Lq, Lk, d) == 0
+    assert lib.pjx_flash_bwd_ds_workspace_size(bf16, 0, H, Lq, Lk, 256) == 0
+    assert lib.pjx_flash_bwd_ds_workspace_size(bf16, B, H, Lq, 0, 256) == 0
+
+
 def test_flash_empty_batch_is_a_no_op(lib):
     assert lib.pjx_flash_fwd(*_flash_args(B=0)) == 0
 
