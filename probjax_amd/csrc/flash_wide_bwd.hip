@@ -789,10 +789,30 @@ __device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
     }
   };
 
+  // DS: element offset of this wave's dS block for the next tile, advanced
+  // per tile in the tile order (heads innermost, query tiles last to first)
+  // with uniform adds; computing it from t (t % gs, t / gs by the runtime
+  // group size) put a division on the vector unit into the tile's block and
+  // broke the S / dP fragment read-ahead order of the latent instance.
+  const long ds_plane = (long)ba.ds_nq32 * ba.ds_nk16 * 512;  // one query head's blocks
+  const long ds_wrap = -((long)(gs - 1) * ds_plane + (long)(kWT / 32) * ba.ds_nk16 * 512);
+  long ds_off = 0;
+  int ds_hh = 0;  // head of the next tile within the group
+  if constexpr (DS)
+    ds_off = (((long)(b * a.Hq + h_first) * ba.ds_nq32 + (q_begin + (n_qt - 1) * kWT) / 32) * ba.ds_nk16 + kw / 16) * 512;
+
   auto compute = [&](int t, const unsigned char* st) {
-    int n_stores = 0;
     const int q0 = tile_q0(t);
-    if (q0 >= q_hi) return n_stores;  // uniform over the workgroup
+    long my_ds = 0;
+    if constexpr (DS) {
+      my_ds = ds_off;
+      const bool wrap = ds_hh + 1 == gs;  // next tile: the group's first head, one query tile lower
+      ds_hh = wrap ? 0 : ds_hh + 1;
+      ds_off += wrap ? ds_wrap : ds_plane;
+    }
+    // uniform over the workgroup; never taken for t < n_tiles (tile_q0 < q_hi),
+    // which the DS ring's store count relies on
+    if (q0 >= q_hi) return;
     const unsigned char* qs = st;
     const unsigned char* dos = st + QT_B;
     // P and dS of this wave's keys (zero where no row of the tile sees them)
@@ -832,17 +852,15 @@ __device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
       pbv = __builtin_bit_cast(u32x4, pack_slots<E>(sx[0], sx[1]));
       dsv = __builtin_bit_cast(u32x4, pack_slots<E>(dpx[0], dpx[1]));
     }
+    xp[(2 * w) * 64 + lane] = pbv;
+    xp[(2 * w + 1) * 64 + lane] = dsv;
+    stage_barrier();
     if constexpr (DS) {
       // block (query block q0 / 32, key block kw / 16) of head tile_head(t):
       // lane (c, qd) holds key kw + c, queries q0 + 4qd + [0,4) then
       // q0 + 16 + 4qd + [0,4) (pack_slots), stored as 16 bytes at 16 * lane
-      const size_t blk = ((size_t)(b * a.Hq + tile_head(t)) * ba.ds_nq32 + q0 / 32) * ba.ds_nk16 + kw / 16;
-      __builtin_nontemporal_store(dsv, (u32x4*)(ba.ds + blk * 512 + 8 * lane));  // read once, by the dQ kernel
-      ++n_stores;
+      __builtin_nontemporal_store(dsv, (u32x4*)(ba.ds + my_ds + 8 * lane));  // read once, by the dQ kernel
     }
-    xp[(2 * w) * 64 + lane] = pbv;
-    xp[(2 * w + 1) * 64 + lane] = dsv;
-    stage_barrier();
     typename E::v8 pk[4], dk[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
@@ -876,38 +894,40 @@ __device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
       __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
     }
     __builtin_amdgcn_sched_group_barrier(0x008, 4 * 3, 0);
-    return n_stores;
   };
 
   // The ring of wide_bwd_dkdv_kernel; each compute adds one barrier between
   // the xp writes and reads, and the next xp writes follow the next ring
   // barrier.  With DS the ring barrier waits for this wave's tile loads only:
-  // the dS store of the last compute() (issued after them; vmcnt counts in
-  // issue order) stays in flight, and the barrier is stage_barrier(), as
-  // __syncthreads()'s release fence would wait for it.  (The scheduling
-  // barriers keep the store after the loads issued before it.)
-  auto ring_wait = [&](int in_flight) {
+  // the one dS store of the last compute() (issued after them; vmcnt counts
+  // in issue order) stays in flight, and the barrier is stage_barrier(), as
+  // __syncthreads()'s release fence would wait for it.  Tile 0's loads are
+  // waited for before the loop, so every ring wait is the same vmcnt(1) (a
+  // wait that depended on a per-iteration store count made the compiler
+  // duplicate the loop body: ~10x the code, and the latent instance ran at
+  // half speed).  The scheduling barriers keep the store after the loads
+  // issued before it.
+  auto ring_wait = [&]() {
     if constexpr (DS) {
-      if (in_flight > 0) wait_vmcnt<1>();
-      else wait_vmcnt<0>();
+      wait_vmcnt<1>();
       stage_barrier();
     } else {
       __builtin_amdgcn_s_waitcnt(0);
       __syncthreads();
     }
   };
-  int n_st = 0;
   if (n_tiles > 0) issue(0, smem0);
+  if constexpr (DS) wait_vmcnt<0>();
   for (int t = 0; t < n_tiles; t += 2) {
-    ring_wait(n_st);
+    ring_wait();
     if (t + 1 < n_tiles) issue(t + 1, smem1);
     if constexpr (DS) __builtin_amdgcn_sched_barrier(0);
-    n_st = compute(t, smem0);
+    compute(t, smem0);
     if (t + 1 >= n_tiles) break;
-    ring_wait(n_st);
+    ring_wait();
     if (t + 2 < n_tiles) issue(t + 2, smem0);
     if constexpr (DS) __builtin_amdgcn_sched_barrier(0);
-    n_st = compute(t + 1, smem1);
+    compute(t + 1, smem1);
   }
 
   // Outputs as wide_bwd_dkdv_kernel's: 16-bit rows with one group, else fp32
