@@ -176,8 +176,8 @@ extern "C" int pjx_flash_bwd(int dtype, const void* q, const void* k, const void
     if (!f32 && !bias && a.ext == 0 && ds_need > 0 && workspace_bytes >= ds_need) {
       // the dS route (flash_wide_bwd.hip): the workspace holds the dS blocks
       wa.ds = (uint16_t*)((unsigned char*)workspace + wide_bwd_ds_offset(need));
-      wa.ds_nq32 = (int)(2 * ((q_len + 63) / 64));
-      wa.ds_nk16 = (int)(4 * ((kv_len + 63) / 64));
+      wa.ds_nq32 = (int)wide_bwd_ds_nq32(q_len);
+      wa.ds_nk16 = (int)wide_bwd_ds_nk16(kv_len);
     }
     if (a.ext != 0 || bias == nullptr) return run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd");
     const int rc = run_wide_bwd(wa, 256, 256, false, s, "pjx_flash_bwd", true);

@@ -190,15 +190,17 @@ struct WideBwdArgs {
   int ds_nq32, ds_nk16;
 };
 
-// Bytes of the wide backward's dS blocks (the dS route) for these sizes:
-// 32-query blocks over the queries rounded up to the dQ kernel's 64-row
-// tiles, 16-key blocks over the keys rounded up to the dK/dV kernel's 64-key
-// tiles.
+// The wide backward's dS blocks (the dS route) for these sizes: 32-query
+// blocks over the queries rounded up to the dQ kernel's 64-row tiles, 16-key
+// blocks over the keys rounded up to the dK/dV kernel's 64-key tiles.
+inline int64_t wide_bwd_ds_nq32(int64_t Lq) { return 2 * ((Lq + 63) / 64); }
+inline int64_t wide_bwd_ds_nk16(int64_t Lk) { return 4 * ((Lk + 63) / 64); }
 size_t wide_bwd_ds_bytes(int64_t B, int64_t Hq, int64_t Lq, int64_t Lk);
 
 // Runs the wide backward (dQ, then dK/dV or the latent's dC, then the partial
 // sum when nsplit > 1; with dq_only the dQ kernel alone, which also writes
-// delta and lse*log2e); returns a PJX_* status.
+// delta and lse*log2e; with ba.ds at D = 256 and no bias or extended masks,
+// the dS route: delta, dK/dV storing dS, dQ from dS); returns a PJX_* status.
 int run_wide_bwd(WideBwdArgs& ba, int D, int DV, bool shared, hipStream_t s, const char* who,
                  bool dq_only = false);
 // Byte offset of the dS blocks in a dS-route workspace whose leading part

@@ -963,8 +963,6 @@ __device__ __forceinline__ void wide_dc_body(const WideBwdArgs& ba) {
   }
 }
 
-// Sums the head-group partials in split order and rounds to the 16-bit format:
-// out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
 template <typename E, int D, int DV, bool SHARED>
 __global__ __launch_bounds__(kThreads, (D == 256 ? 2 : 1)) void wide_bwd_dc_kernel(WideBwdArgs ba) {
   wide_dc_body<E, D, DV, SHARED, false>(ba);
@@ -1155,6 +1153,8 @@ __global__ __launch_bounds__(kThreads, (D <= 256 ? 2 : 1)) void wide_bwd_dq_ds_k
   }
 }
 
+// Sums the head-group partials in split order and rounds to the 16-bit format:
+// out[e] = sum_s part[s][e] for e < n (n a multiple of 4).
 template <typename E>
 __global__ __launch_bounds__(256) void wide_bwd_reduce_kernel(const float* part, int nsplit, size_t n,
                                                                 uint16_t* out) {
@@ -1296,8 +1296,9 @@ extern "C" size_t pjx_mla_bwd_workspace_size(int64_t batch, int64_t heads, int64
 }
 
 namespace pjx {
+static_assert(kWQ == 64 && kWK == 64, "the dS block counts of flash_common.h follow these tiles");
 size_t wide_bwd_ds_bytes(int64_t B, int64_t Hq, int64_t Lq, int64_t Lk) {
-  const int64_t nq32 = 2 * ((Lq + kWQ - 1) / kWQ), nk16 = 4 * ((Lk + kWK - 1) / kWK);
+  const int64_t nq32 = wide_bwd_ds_nq32(Lq), nk16 = wide_bwd_ds_nk16(Lk);
   return (size_t)B * Hq * nq32 * nk16 * 1024;
 }
 }  // namespace pjx
