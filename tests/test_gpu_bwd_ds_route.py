@@ -51,13 +51,13 @@ def _check(got, want, what):
     )
 
 
-def _omask(causal, lengths, q_valid, Lk):
+def _omask(causal, lengths, q_valid, kv_valid, Lq, Lk):
     m = oracle.CausalMask() if causal else None
     if lengths is not None:
         kl = oracle.KVLenMask(np.array(lengths, np.int32))
         m = kl if m is None else m & kl
-    if q_valid is not None:
-        ql = oracle.QKVLengthMask(q_valid, Lk)
+    if q_valid is not None or kv_valid is not None:
+        ql = oracle.QKVLengthMask(Lq if q_valid is None else q_valid, Lk if kv_valid is None else kv_valid)
         m = ql if m is None else m & ql
     return m
 
@@ -68,13 +68,15 @@ def _launched():
     return native.last_launches()
 
 
-# name: B, Lq, Lk, Hq, Hkv, causal, kv_lengths, q_valid
+# name: B, Lq, Lk, Hq, Hkv, causal, kv_lengths, q_valid, kv_valid
 FLASH_CASES = {
-    "causal_gqa": (1, 256, 256, 4, 2, True, None, None),
-    "ragged_noncausal": (2, 200, 300, 4, 2, False, [300, 123], None),
-    "causal_qvalid": (1, 300, 300, 8, 2, True, None, 250),
-    "empty_sequence": (2, 130, 70, 2, 1, False, [70, 0], None),
-    "many_heads": (1, 128, 192, 24, 24, True, None, None),
+    "causal_gqa": (1, 256, 256, 4, 2, True, None, None, None),
+    "ragged_noncausal": (2, 200, 300, 4, 2, False, [300, 123], None, None),
+    "causal_qvalid": (1, 300, 300, 8, 2, True, None, 250, None),
+    "empty_sequence": (2, 130, 70, 2, 1, False, [70, 0], None, None),
+    "many_heads": (1, 128, 192, 24, 24, True, None, None, None),
+    "kv_valid": (2, 160, 260, 4, 4, False, None, None, 201),
+    "one_query": (3, 1, 333, 8, 2, False, [333, 17, 200], None, None),
 }
 
 
@@ -84,20 +86,20 @@ def test_flash_d256_ds_route(device, name, dtype):
     import torch
     from probjax_amd.hip_attention import flash_attention_bwd
 
-    B, Lq, Lk, Hq, Hkv, causal, lengths, q_valid = FLASH_CASES[name]
+    B, Lq, Lk, Hq, Hkv, causal, lengths, q_valid, kv_valid = FLASH_CASES[name]
     D, E = 256, FMT[dtype]
     print(f"ds route flash {name} {dtype}: B={B} Lq={Lq} Lk={Lk} Hq={Hq} Hkv={Hkv} causal={causal} "
-          f"lengths={lengths} q_valid={q_valid}", flush=True)
+          f"lengths={lengths} q_valid={q_valid} kv_valid={kv_valid}", flush=True)
     q, k, v, do = (_round(x, dtype) for x in rng_normal(90 + len(name), (B, Lq, Hq, D), (B, Lk, Hkv, D),
                                                         (B, Lk, Hkv, D), (B, Lq, Hq, D)))
     scale = 1.0 / math.sqrt(D)
-    mask = _omask(causal, lengths, q_valid, Lk)
+    mask = _omask(causal, lengths, q_valid, kv_valid, Lq, Lk)
     o, lse = oracle.xla_attention(q, k, v, mask=mask, sm_scale=scale, dtype=dtype, return_lse=True)
     want = attention_backward(q, k, v, o, do, lse, mask=mask, sm_scale=scale, dtype=dtype)
     tdt = _tdt(dtype)
     L = None if lengths is None else torch.tensor(lengths, dtype=torch.int32, device=device)
     args = [to_dev(x, device, tdt) for x in (q, k, v, o, do)] + [torch.from_numpy(lse).to(device)]
-    kw = dict(sm_scale=scale, causal=causal, kv_lengths=L, q_valid=q_valid)
+    kw = dict(sm_scale=scale, causal=causal, kv_lengths=L, q_valid=q_valid, kv_valid=kv_valid)
     got = flash_attention_bwd(*args, ds_route=True, **kw)
     assert _launched() == [f"wide_bwd_delta_kernel<{E}, 256>", f"wide_bwd_dc_ds_kernel<{E}, 256, 256, false>",
                            f"wide_bwd_dq_ds_kernel<{E}, 256>"], _launched()
